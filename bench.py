@@ -1,0 +1,228 @@
+#!/usr/bin/env python3
+"""Benchmark of the attention hot path on one MI355X.
+
+One step = causal flash-attention forward (O, LSE) + backward (delta, dK/dV,
+dQ) at B=8 H=12 S=1024 D=64 bf16, on synthetic seeded
+inputs already resident in HBM: q/k are RoPE'd views of a fused qkv tensor,
+exactly as the attention block hands them over.  The kernels are called
+through the C ABI (include/mi_attn.h) with pre-built argument lists so the
+host keeps the GPU queue full.
+
+Printed: ONE JSON line with the metric of BASELINE.json (algorithmic TFLOP/s of
+fwd+bwd, causal counted as half of dense: 7*B*H*S^2*D flops per step), the
+per-kernel durations from HIP events recorded around every launch in the
+timed region, the roofline of the dominant kernel, the RoPE bandwidth, and
+the CPU baseline (the oracle's fp32 eager attention on the host cores).
+
+Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
+"""
+import argparse
+import ctypes
+import json
+import math
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "causal attn fwd+bwd TFLOP/s & % bf16 MFMA peak, B8 H12 S1024 D64"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=12.0,
+                    help="approximate CPU time budget of the baseline sample")
+    return ap.parse_args()
+
+
+def attn_flops(B, H, S, D):
+    unit = B * H * S * S * D  # one causal GEMM-equivalent (half of 2*B*H*S^2*D)
+    return {"fwd": 2 * unit, "bwd": 5 * unit, "dkdv": 4 * unit, "dq": 1 * unit,
+            "total": 7 * unit}
+
+
+def read_traffic(kernel):
+    """HBM bytes per launch for `kernel` from the committed rocprofv3 PMC summary,
+    or None when it has not been measured."""
+    path = os.path.join(ROOT, "profiles", "traffic_c2.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        parts = line.split()
+        if len(parts) == 3 and parts[0] == "traffic" and parts[1] == kernel:
+            return float(parts[2])
+    return None
+
+
+def cpu_baseline(B, H, S, D, budget_s):
+    """The oracle's fp32 eager attention fwd+bwd on the host, on a sample of heads."""
+    import torch
+    from oracle import attention_backward, attention_forward
+
+    threads = torch.get_num_threads()
+    g = torch.Generator().manual_seed(2)
+
+    def run(nh):
+        q, k, v, do = (torch.randn(1, nh, S, D, generator=g).to(torch.bfloat16).float()
+                       for _ in range(4))
+        t0 = time.perf_counter()
+        attention_forward(q, k, v, True, dtype=torch.float32)
+        attention_backward(q, k, v, do, True, dtype=torch.float32)
+        return time.perf_counter() - t0
+
+    run(1)  # warm-up
+    per_head = run(1)
+    nh = max(1, min(B * H, int(budget_s / 3 / max(per_head, 1e-6))))
+    times = [run(nh) for _ in range(3)]
+    t = statistics.median(times)
+    flops = attn_flops(1, nh, S, D)["total"]
+    return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{nh} of {B * H} (b,h) heads of B{B} H{H} S{S} D{D}: oracle fp32 eager "
+                      f"fwd+bwd on the CPU, median of 3 runs ({t:.2f} s each)"}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
+              "(attention has no cross-GPU exchange: heads and batches shard with no "
+              "communication)", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from gpt_from_scratch_amd import _lib
+    from gpt_from_scratch_amd.rope import apply_rope_qk
+    from oracle import rope_tables
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, H, S, D = 8, 12, 1024, 64
+    flops = attn_flops(B, H, S, D)
+    scale = 1.0 / math.sqrt(D)
+
+    g = torch.Generator().manual_seed(2)
+    qkv = torch.randn(S, B, 3, H, D, generator=g).to(torch.bfloat16).to(dev)
+    do = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16).to(dev)
+    cos, sin = (t.to(torch.bfloat16).to(dev) for t in rope_tables(D, S))
+    q, k, v = qkv.unbind(2)
+    qr, kr = apply_rope_qk(q, k, cos, sin)
+    Q, K, V = qr.permute(1, 2, 0, 3), kr.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3)
+    O = torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev)
+    LSE = torch.empty(B, H, S, dtype=torch.float32, device=dev)
+    DELTA = torch.empty_like(LSE)
+    dQ, dK, dV = (torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev) for _ in range(3))
+
+    lib = _lib.lib()
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    ST = lambda t: (ctypes.c_int64 * 4)(*t.stride())
+    dt = _lib.dtype_code(Q)
+    hdr = (dt, B, H, S, D)
+    fwd_args = hdr + (1, scale, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(O), ST(O), P(LSE), sp)
+    pre_args = hdr + (P(O), ST(O), P(do), ST(do), P(DELTA), sp)
+    dkdv_args = hdr + (1, scale, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(do), ST(do), P(LSE),
+                       P(DELTA), P(dK), ST(dK), P(dV), ST(dV), sp)
+    dq_args = hdr + (1, scale, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(do), ST(do), P(LSE),
+                     P(DELTA), P(dQ), ST(dQ), sp)
+    calls = [("attn_fwd", lib.mi_attn_fwd, fwd_args),
+             ("attn_bwd_preprocess", lib.mi_attn_bwd_preprocess, pre_args),
+             ("attn_bwd_dkdv", lib.mi_attn_bwd_dkdv, dkdv_args),
+             ("attn_bwd_dq", lib.mi_attn_bwd_dq, dq_args)]
+
+    def step(evs=None):
+        for i, (name, fn, a) in enumerate(calls):
+            if evs is not None:
+                evs[i].record(stream)
+            st = fn(*a)
+            if st != 0:
+                raise RuntimeError(f"{name}: {lib.mi_last_error().decode()}")
+        if evs is not None:
+            evs[len(calls)].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Timed region: exactly K steps between two events on the launch stream,
+    # with events around every launch for the per-kernel durations.
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(calls) + 1)]
+           for _ in range(args.steps)]
+    t_start = torch.cuda.Event(enable_timing=True)
+    t_end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t_start.record(stream)
+    for s in range(args.steps):
+        step(evs[s])
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    ms_per_step = t_start.elapsed_time(t_end) / args.steps
+
+    per_kernel_us = {}
+    for i, (name, _, _) in enumerate(calls):
+        per_kernel_us[name] = statistics.mean(e[i].elapsed_time(e[i + 1]) for e in evs) * 1e3
+
+    kflops = {"attn_fwd": flops["fwd"], "attn_bwd_dkdv": flops["dkdv"],
+              "attn_bwd_dq": flops["dq"]}
+    kernels = {}
+    for name, us in per_kernel_us.items():
+        ent = {"avg_us": round(us, 3)}
+        if name in kflops:
+            ent["tflops"] = round(kflops[name] / (us * 1e-6) / 1e12, 2)
+        kernels[name] = ent
+    dom = max(kflops, key=lambda n: per_kernel_us[n])
+    achieved = kflops[dom] / (per_kernel_us[dom] * 1e-6) / 1e12
+    roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
+                "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                "algorithmic_flop_per_launch": kflops[dom], "traffic": read_traffic(dom)}
+
+    # RoPE (q and k in one launch, the model's strided layout) — HBM-bound.
+    rq, rk = torch.empty_like(qr), torch.empty_like(kr)
+    for _ in range(10):
+        _lib.rope_qk(q, k, cos, sin, rq, rk, inverse=False)
+    torch.cuda.synchronize()
+    r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    n_rope = 200
+    r0.record(stream)
+    for _ in range(n_rope):
+        _lib.rope_qk(q, k, cos, sin, rq, rk, inverse=False)
+    r1.record(stream)
+    torch.cuda.synchronize()
+    rope_us = r0.elapsed_time(r1) / n_rope * 1e3
+    rope_bytes = 4 * B * S * H * D * 2 + 2 * S * (D // 2) * 2
+    rope_gbps = rope_bytes / (rope_us * 1e-6) / 1e9
+
+    tflops = flops["total"] / (ms_per_step * 1e-3) / 1e12
+    out = {
+        "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) q/k/v/dO, RoPE theta=10000 on q/k)",
+        "config": {"workload": "causal flash attention fwd+bwd (O, LSE, dQ, dK, dV), config 2",
+                   "B": B, "H": H, "S": S, "D": D, "causal": True, "layout": "model views"},
+        "pct_peak": round(100 * tflops / PEAK_BF16_TFLOPS, 2),
+        "algorithmic_gflop_per_step": flops["total"] / 1e9,
+        "kernels": kernels,
+        "roofline": roofline,
+        "rope": {"bound": "hbm", "avg_us": round(rope_us, 3), "achieved": round(rope_gbps, 1),
+                 "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                 "frac": round(rope_gbps / PEAK_HBM_GBPS, 4), "algorithmic_bytes": rope_bytes},
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(B, H, S, D, args.cpu_seconds)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,164 @@
+"""ctypes binding of libmi_attn.so, the C ABI declared in include/mi_attn.h.
+
+The library is built in-tree (``gpt_from_scratch_amd/libmi_attn.so``, see
+``gpt_from_scratch_amd/build.py``).  There is no fallback: if the library is
+missing or a tensor is not on a ROCm GPU, the calls below raise.
+
+torch is imported before the library is loaded so that the library binds to the
+HIP runtime torch already loaded (same SONAME), i.e. streams and device
+pointers handed over from torch are valid in the library.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmi_attn.so")
+
+MI_OK = 0
+_DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+
+# Every function declared in include/mi_attn.h.
+EXPORTED = ("mi_version", "mi_status_str", "mi_last_error", "mi_attn_fwd", "mi_attn_bwd",
+            "mi_attn_bwd_preprocess", "mi_attn_bwd_dkdv", "mi_attn_bwd_dq", "mi_rope",
+            "mi_rope_qk")
+
+_lib = None
+
+
+class MiError(RuntimeError):
+    """A non-OK status returned by the C ABI."""
+
+
+def _i64x4():
+    return ctypes.c_int64 * 4
+
+
+def _declare(lib):
+    p, i, f, i64p = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.POINTER(ctypes.c_int64)
+    lib.mi_version.restype = i
+    lib.mi_version.argtypes = []
+    lib.mi_status_str.restype = ctypes.c_char_p
+    lib.mi_status_str.argtypes = [i]
+    lib.mi_last_error.restype = ctypes.c_char_p
+    lib.mi_last_error.argtypes = []
+    lib.mi_attn_fwd.restype = i
+    lib.mi_attn_fwd.argtypes = [i, i, i, i, i, i, f, p, i64p, p, i64p, p, i64p, p, i64p, p, p]
+    lib.mi_attn_bwd.restype = i
+    lib.mi_attn_bwd.argtypes = [i, i, i, i, i, i, f,
+                                p, i64p, p, i64p, p, i64p, p, i64p, p, i64p,
+                                p, p, p, i64p, p, i64p, p, i64p, p]
+    lib.mi_attn_bwd_preprocess.restype = i
+    lib.mi_attn_bwd_preprocess.argtypes = [i, i, i, i, i, p, i64p, p, i64p, p, p]
+    lib.mi_attn_bwd_dkdv.restype = i
+    lib.mi_attn_bwd_dkdv.argtypes = [i, i, i, i, i, i, f, p, i64p, p, i64p, p, i64p, p, i64p,
+                                     p, p, p, i64p, p, i64p, p]
+    lib.mi_attn_bwd_dq.restype = i
+    lib.mi_attn_bwd_dq.argtypes = [i, i, i, i, i, i, f, p, i64p, p, i64p, p, i64p, p, i64p,
+                                   p, p, p, i64p, p]
+    lib.mi_rope.restype = i
+    lib.mi_rope.argtypes = [i, i, i, i, i, i, i, p, i64p, p, i64p, p, i64p, p, i64p, p]
+    lib.mi_rope_qk.restype = i
+    lib.mi_rope_qk.argtypes = [i, i, i, i, i, i, i, p, i64p, p, i64p, p, i64p, p, i64p,
+                               p, i64p, p, i64p, p]
+
+
+def lib():
+    """Load (once) and return the C library.  Raises if it was not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise ImportError(
+                f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
+                "g.build()'` (or `make -C gpt_from_scratch_amd/csrc`)")
+        handle = ctypes.CDLL(LIB_PATH, mode=ctypes.RTLD_LOCAL)
+        _declare(handle)
+        _lib = handle
+    return _lib
+
+
+def _check(status: int, what: str):
+    if status != MI_OK:
+        l = lib()
+        msg = l.mi_last_error().decode()
+        name = l.mi_status_str(status).decode()
+        raise MiError(f"{what}: {name} ({msg})")
+
+
+def dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise TypeError(f"unsupported dtype {t.dtype}: expected float32, float16 or bfloat16")
+
+
+def _strides(t: torch.Tensor, n: int):
+    arr = (ctypes.c_int64 * n)(*t.stride())
+    return arr
+
+
+def _ptr(t: torch.Tensor):
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def _require_gpu(*ts: torch.Tensor):
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise RuntimeError(
+            f"gpt_from_scratch_amd kernels run on ROCm GPUs only; got a tensor on {dev}")
+    for t in ts[1:]:
+        if t.device != dev:
+            raise RuntimeError(f"all tensors must be on {dev}; got one on {t.device}")
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def attn_fwd(q, k, v, o, lse, causal: bool, scale: float):
+    """Enqueue the forward on the current stream: writes o [B,H,S,D] and lse [B,H,S] fp32."""
+    _require_gpu(q, k, v, o, lse)
+    B, H, S, D = q.shape
+    st = lib().mi_attn_fwd(dtype_code(q), B, H, S, D, int(bool(causal)), float(scale),
+                           _ptr(q), _strides(q, 4), _ptr(k), _strides(k, 4),
+                           _ptr(v), _strides(v, 4), _ptr(o), _strides(o, 4),
+                           _ptr(lse), _stream(q))
+    _check(st, "mi_attn_fwd")
+
+
+def attn_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float):
+    """Enqueue the backward on the current stream: writes delta, dq, dk, dv."""
+    _require_gpu(q, k, v, o, do, lse, delta, dq, dk, dv)
+    B, H, S, D = q.shape
+    st = lib().mi_attn_bwd(dtype_code(q), B, H, S, D, int(bool(causal)), float(scale),
+                           _ptr(q), _strides(q, 4), _ptr(k), _strides(k, 4),
+                           _ptr(v), _strides(v, 4), _ptr(o), _strides(o, 4),
+                           _ptr(do), _strides(do, 4), _ptr(lse), _ptr(delta),
+                           _ptr(dq), _strides(dq, 4), _ptr(dk), _strides(dk, 4),
+                           _ptr(dv), _strides(dv, 4), _stream(q))
+    _check(st, "mi_attn_bwd")
+
+
+def rope(x, cos, sin, out, inverse: bool):
+    """Enqueue one rotation of x [S,B,H,D] into out with tables cos/sin [S', D/2]."""
+    _require_gpu(x, cos, sin, out)
+    S, B, H, D = x.shape
+    st = lib().mi_rope(dtype_code(x), dtype_code(cos), S, B, H, D, int(bool(inverse)),
+                       _ptr(x), _strides(x, 4), _ptr(cos), _strides(cos, 2),
+                       _ptr(sin), _strides(sin, 2), _ptr(out), _strides(out, 4), _stream(x))
+    _check(st, "mi_rope")
+
+
+def rope_qk(q, k, cos, sin, q_out, k_out, inverse: bool):
+    """Enqueue the rotation of q and k (same shape and dtype) in one launch."""
+    _require_gpu(q, k, cos, sin, q_out, k_out)
+    S, B, H, D = q.shape
+    st = lib().mi_rope_qk(dtype_code(q), dtype_code(cos), S, B, H, D, int(bool(inverse)),
+                          _ptr(q), _strides(q, 4), _ptr(k), _strides(k, 4),
+                          _ptr(cos), _strides(cos, 2), _ptr(sin), _strides(sin, 2),
+                          _ptr(q_out), _strides(q_out, 4), _ptr(k_out), _strides(k_out, 4),
+                          _stream(q))
+    _check(st, "mi_rope_qk")

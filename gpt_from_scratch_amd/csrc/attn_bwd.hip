@@ -1,0 +1,529 @@
+// attn_bwd.hip — flash-attention backward on gfx950 bf16/f16 matrix cores.
+//
+// Counterpart of FlashAttn.backward's three kernels (core/myFlashAttn.py:288-441):
+//   delta  = rowsum(dO * O) in fp32                     (`_attn_bwd_precompute` :731-790)
+//   dK, dV : per key tile, loop over query tiles         (`_attn_bwd_LoopQ` :795-1066)
+//            P = exp(S*scale - lse), dV += P^T dO, dP = dO V^T,
+//            dS = P * (dP - delta), dK += dS^T Q * scale
+//   dQ     : per query tile, loop over key tiles         (`_attn_bwd_LoopKV` :1069-1317)
+//            dQ += dS K * scale
+// The formulas are the ones stated in the reference's docstring (:289-315).
+//
+// Layout choices (wave64, 32x32x16 MFMA; see mi_device.h for operand layouts):
+//   * dK/dV kernel: a workgroup owns 128 keys (wave w: keys [32w, 32w+32)); the
+//     wave's K and V rows live in registers as B operands for the whole loop.
+//     S = Q K^T and dP = dO V^T are computed with keys along the lane index, so
+//     P and dS come out of the accumulators already in B-operand form for
+//     dV^T = dO^T P and dK^T = Q^T dS.  Q and dO tiles are staged in LDS both
+//     row-major (A operands of S and dP) and transposed (A operands of dV^T and
+//     dK^T), double-buffered, the transpose done once per tile with v_perm.
+//   * dQ kernel: a workgroup owns 128 queries; Q and dO rows live in registers;
+//     S^T = K Q^T and dP^T = V dO^T put queries along the lane index so that
+//     lse and delta are per-lane scalars and dS^T feeds dQ^T = K^T dS^T directly.
+//   * causal: key tiles only visit query tiles at or after the diagonal, query
+//     tiles only key tiles at or before it; 32-row blocks entirely above the
+//     diagonal are skipped per wave, blocks that straddle it are masked.
+#include "mi_device.h"
+#include "mi_kernels.h"
+
+namespace mi {
+
+namespace {
+
+// ---------------------------------------------------------------------------
+// delta[b,h,s] = sum_d dO[b,h,s,d] * O[b,h,s,d]   (fp32 accumulation)
+// Eight lanes per row; each lane takes every 8th chunk of VEC elements.
+// ---------------------------------------------------------------------------
+template <int DT, int VEC>
+__global__ __launch_bounds__(256) void attn_delta_kernel(AttnArgs a, FastDiv divS, FastDiv divH,
+                                                         uint32_t nrows) {
+  typedef typename Store<DT>::type T;
+  const uint32_t t = blockIdx.x * 256 + threadIdx.x;
+  const uint32_t row = t >> 3;
+  const int sub = t & 7;
+  float acc = 0.f;
+  if (row < nrows) {
+    const uint32_t bh = fdiv(row, divS);
+    const uint32_t s = row - bh * divS.d;
+    const uint32_t b = fdiv(bh, divH);
+    const uint32_t h = bh - b * divH.d;
+    const T* o = (const T*)a.o.ptr + b * a.o.sb + h * a.o.sh + s * a.o.ss;
+    const T* d = (const T*)a.dout.ptr + b * a.dout.sb + h * a.dout.sh + s * a.dout.ss;
+    for (int c = sub * VEC; c < a.D; c += 8 * VEC) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e)
+        acc += Store<DT>::ld(o, c + e) * Store<DT>::ld(d, c + e);
+    }
+  }
+  acc += __shfl_xor(acc, 1, 64);
+  acc += __shfl_xor(acc, 2, 64);
+  acc += __shfl_xor(acc, 4, 64);
+  if (row < nrows && sub == 0) a.delta[row] = acc;
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV
+// ---------------------------------------------------------------------------
+template <int D>
+struct DkvCfg {
+  static constexpr int BKV = 128;
+  static constexpr int BQ = (D == 64) ? 64 : 32;
+  static constexpr int NT = 256;
+  static constexpr int RLD = D + 8;   // row-major Q / dO tile stride (elements)
+  static constexpr int TLD = BQ + 4;  // transposed Q^T / dO^T tile stride
+  static constexpr int KS = D / 16;
+  static constexpr int DB = D / 32;
+  static constexpr int QB = BQ / 32;
+  static constexpr int CG = D / 4;    // loader column groups (4 columns each)
+  static constexpr int RG = BQ / 4;   // loader row groups (4 rows each)
+  static_assert(CG * RG == NT, "loader covers the tile with 4x4 blocks");
+  static constexpr int BUF = 2 * BQ * RLD + 2 * D * TLD;  // uint16 per buffer
+};
+
+template <typename E, int D, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, int n_kvtiles) {
+  using C = DkvCfg<D>;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2][C::BUF];
+  __shared__ __attribute__((aligned(16))) float sl[2][2 * C::BQ];  // lse*log2e, delta
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+
+  const int BH = a.B * a.H;
+  const int bid = blockIdx.x;
+  const int kt = bid / BH;  // key tile 0 sees the most query tiles: dispatched first
+  const int bh = bid % BH;
+  const int b = bh / a.H;
+  const int h = bh % a.H;
+  const int S = a.S;
+
+  const uint16_t* qp = (const uint16_t*)a.q.ptr + b * a.q.sb + h * a.q.sh;
+  const uint16_t* kp = (const uint16_t*)a.k.ptr + b * a.k.sb + h * a.k.sh;
+  const uint16_t* vp = (const uint16_t*)a.v.ptr + b * a.v.sb + h * a.v.sh;
+  const uint16_t* dop = (const uint16_t*)a.dout.ptr + b * a.dout.sb + h * a.dout.sh;
+  const float* lsep = a.lse + (int64_t)bh * S;
+  const float* delp = a.delta + (int64_t)bh * S;
+
+  const int kv0 = kt * C::BKV;
+  const int kw = kv0 + 32 * wave;
+  const bool wave_valid = kw < S;
+  const int krow = kw + l32;
+
+  u32x4 kf[C::KS], vf[C::KS];
+#pragma unroll
+  for (int ks = 0; ks < C::KS; ++ks) {
+    if (wave_valid) {
+      kf[ks] = *(const u32x4*)(kp + (int64_t)krow * a.k.ss + 16 * ks + 8 * g);
+      vf[ks] = *(const u32x4*)(vp + (int64_t)krow * a.v.ss + 16 * ks + 8 * g);
+    } else {
+      kf[ks] = u32x4{0, 0, 0, 0};
+      vf[ks] = u32x4{0, 0, 0, 0};
+    }
+  }
+
+  const int q_begin = CAUSAL ? kv0 : 0;
+  const int nq = (S - q_begin) / C::BQ;
+
+  // staging registers
+  const int rg = tid / C::CG;
+  const int cg = tid % C::CG;
+  u32x2 qreg[4], dreg[4];
+  float lreg = 0.f, dlreg = 0.f;
+
+  auto load_tile = [&](int q0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t row = q0 + 4 * rg + r;
+      qreg[r] = *(const u32x2*)(qp + row * a.q.ss + 4 * cg);
+      dreg[r] = *(const u32x2*)(dop + row * a.dout.ss + 4 * cg);
+    }
+    if (tid < C::BQ) {
+      lreg = lsep[q0 + tid] * kLog2e;
+      dlreg = delp[q0 + tid];
+    }
+  };
+  auto store_tile = [&](int buf) {
+    uint16_t* Qs = smem[buf];
+    uint16_t* dOs = Qs + C::BQ * C::RLD;
+    uint16_t* Qt = dOs + C::BQ * C::RLD;
+    uint16_t* dOt = Qt + D * C::TLD;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      *(u32x2*)(&Qs[(4 * rg + r) * C::RLD + 4 * cg]) = qreg[r];
+      *(u32x2*)(&dOs[(4 * rg + r) * C::RLD + 4 * cg]) = dreg[r];
+    }
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      u32x2 c0, c1;
+      const int d = 4 * cg + 2 * w;
+      transpose4x2(qreg[0][w], qreg[1][w], qreg[2][w], qreg[3][w], c0, c1);
+      *(u32x2*)(&Qt[d * C::TLD + 4 * rg]) = c0;
+      *(u32x2*)(&Qt[(d + 1) * C::TLD + 4 * rg]) = c1;
+      transpose4x2(dreg[0][w], dreg[1][w], dreg[2][w], dreg[3][w], c0, c1);
+      *(u32x2*)(&dOt[d * C::TLD + 4 * rg]) = c0;
+      *(u32x2*)(&dOt[(d + 1) * C::TLD + 4 * rg]) = c1;
+    }
+    if (tid < C::BQ) {
+      sl[buf][tid] = lreg;
+      sl[buf][C::BQ + tid] = dlreg;
+    }
+  };
+
+  f32x16 dk[C::DB], dv[C::DB];
+#pragma unroll
+  for (int i = 0; i < C::DB; ++i) {
+    dk[i] = f32x16{};
+    dv[i] = f32x16{};
+  }
+  const float c = a.scale_log2;
+
+  if (nq > 0) {
+    load_tile(q_begin);
+    store_tile(0);
+  }
+  __syncthreads();
+
+  for (int j = 0; j < nq; ++j) {
+    const int buf = j & 1;
+    const int q0 = q_begin + j * C::BQ;
+    if (j + 1 < nq) load_tile(q0 + C::BQ);
+
+    if (wave_valid && (!CAUSAL || q0 + C::BQ - 1 >= kw)) {
+      const uint16_t* Qs = smem[buf];
+      const uint16_t* dOs = Qs + C::BQ * C::RLD;
+      const uint16_t* Qt = dOs + C::BQ * C::RLD;
+      const uint16_t* dOt = Qt + D * C::TLD;
+      u32x4 pb[C::QB][2], sb[C::QB][2];
+      bool live[C::QB];
+#pragma unroll
+      for (int qb = 0; qb < C::QB; ++qb) {
+        const int qbs = q0 + 32 * qb;
+        live[qb] = !CAUSAL || (qbs + 31 >= kw);
+        if (!live[qb]) continue;
+        f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < C::KS; ++ks) {
+          const u32x4 qa = *(const u32x4*)(&Qs[(32 * qb + l32) * C::RLD + 16 * ks + 8 * g]);
+          s = E::mfma(qa, kf[ks], s);
+        }
+#pragma unroll
+        for (int ks = 0; ks < C::KS; ++ks) {
+          const u32x4 da = *(const u32x4*)(&dOs[(32 * qb + l32) * C::RLD + 16 * ks + 8 * g]);
+          dp = E::mfma(da, vf[ks], dp);
+        }
+        const bool diag = CAUSAL && (qbs < kw + 31);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const f32x4 l4 = *(const f32x4*)(&sl[buf][32 * qb + 8 * jj + 4 * g]);
+          const f32x4 d4 = *(const f32x4*)(&sl[buf][C::BQ + 32 * qb + 8 * jj + 4 * g]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int r = 4 * jj + i;
+            float p = fast_exp2(__builtin_fmaf(s[r], c, -l4[i]));
+            if (diag && krow > qbs + 8 * jj + 4 * g + i) p = 0.f;
+            s[r] = p;
+            dp[r] = p * (dp[r] - d4[i]);
+          }
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            pb[qb][hh][w] = E::pack2(s[8 * hh + 2 * w], s[8 * hh + 2 * w + 1]);
+            sb[qb][hh][w] = E::pack2(dp[8 * hh + 2 * w], dp[8 * hh + 2 * w + 1]);
+          }
+      }
+#pragma unroll
+      for (int qb = 0; qb < C::QB; ++qb) {
+        if (!live[qb]) continue;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+          for (int db = 0; db < C::DB; ++db) {
+            const int off = (32 * db + l32) * C::TLD + 32 * qb + 16 * hh + 4 * g;
+            const u32x2 a0 = *(const u32x2*)(&dOt[off]);
+            const u32x2 a1 = *(const u32x2*)(&dOt[off + 8]);
+            dv[db] = E::mfma(u32x4{a0[0], a0[1], a1[0], a1[1]}, pb[qb][hh], dv[db]);
+            const u32x2 b0 = *(const u32x2*)(&Qt[off]);
+            const u32x2 b1 = *(const u32x2*)(&Qt[off + 8]);
+            dk[db] = E::mfma(u32x4{b0[0], b0[1], b1[0], b1[1]}, sb[qb][hh], dk[db]);
+          }
+        }
+      }
+    }
+
+    if (j + 1 < nq) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (!wave_valid) return;
+  uint16_t* dkrow = (uint16_t*)a.dk.ptr + b * a.dk.sb + h * a.dk.sh + (int64_t)krow * a.dk.ss;
+  uint16_t* dvrow = (uint16_t*)a.dv.ptr + b * a.dv.sb + h * a.dv.sh + (int64_t)krow * a.dv.ss;
+  const float sc = a.scale;
+#pragma unroll
+  for (int db = 0; db < C::DB; ++db) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      u32x2 wk, wv;
+      wk[0] = E::pack2(dk[db][4 * jj + 0] * sc, dk[db][4 * jj + 1] * sc);
+      wk[1] = E::pack2(dk[db][4 * jj + 2] * sc, dk[db][4 * jj + 3] * sc);
+      wv[0] = E::pack2(dv[db][4 * jj + 0], dv[db][4 * jj + 1]);
+      wv[1] = E::pack2(dv[db][4 * jj + 2], dv[db][4 * jj + 3]);
+      *(u32x2*)(dkrow + 32 * db + 8 * jj + 4 * g) = wk;
+      *(u32x2*)(dvrow + 32 * db + 8 * jj + 4 * g) = wv;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dQ
+// ---------------------------------------------------------------------------
+template <int D>
+struct DqCfg {
+  static constexpr int BQ = 128;
+  static constexpr int BKV = (D == 64) ? 64 : 32;
+  static constexpr int NKB = BKV / 32;
+  static constexpr int NT = 256;
+  static constexpr int RLD = D + 8;    // row-major K / V tile stride
+  static constexpr int TLD = BKV + 4;  // transposed K^T tile stride
+  static constexpr int KS = D / 16;
+  static constexpr int DB = D / 32;
+  static constexpr int CG = D / 4;
+  static constexpr int RG = BKV / 4;
+  static_assert(CG * RG == NT, "loader covers the tile with 4x4 blocks");
+  static constexpr int BUF = 2 * BKV * RLD + D * TLD;
+};
+
+template <typename E, int D, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a, int n_qtiles) {
+  using C = DqCfg<D>;
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2][C::BUF];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+
+  const int BH = a.B * a.H;
+  const int bid = blockIdx.x;
+  const int qt = n_qtiles - 1 - bid / BH;
+  const int bh = bid % BH;
+  const int b = bh / a.H;
+  const int h = bh % a.H;
+  const int S = a.S;
+
+  const uint16_t* qp = (const uint16_t*)a.q.ptr + b * a.q.sb + h * a.q.sh;
+  const uint16_t* kp = (const uint16_t*)a.k.ptr + b * a.k.sb + h * a.k.sh;
+  const uint16_t* vp = (const uint16_t*)a.v.ptr + b * a.v.sb + h * a.v.sh;
+  const uint16_t* dop = (const uint16_t*)a.dout.ptr + b * a.dout.sb + h * a.dout.sh;
+
+  const int q0 = qt * C::BQ;
+  const int qw = q0 + 32 * wave;
+  const bool wave_valid = qw < S;
+  const int qrow = qw + l32;
+
+  u32x4 qf[C::KS], df[C::KS];
+  float lse2 = 0.f, dl = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < C::KS; ++ks) {
+    if (wave_valid) {
+      qf[ks] = *(const u32x4*)(qp + (int64_t)qrow * a.q.ss + 16 * ks + 8 * g);
+      df[ks] = *(const u32x4*)(dop + (int64_t)qrow * a.dout.ss + 16 * ks + 8 * g);
+    } else {
+      qf[ks] = u32x4{0, 0, 0, 0};
+      df[ks] = u32x4{0, 0, 0, 0};
+    }
+  }
+  if (wave_valid) {
+    lse2 = a.lse[(int64_t)bh * S + qrow] * kLog2e;
+    dl = a.delta[(int64_t)bh * S + qrow];
+  }
+
+  const int kv_end = CAUSAL ? min(q0 + C::BQ, S) : S;
+  const int nkv = kv_end / C::BKV;
+
+  const int rg = tid / C::CG;
+  const int cg = tid % C::CG;
+  u32x2 kreg[4], vreg[4];
+
+  auto load_tile = [&](int kv0) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t row = kv0 + 4 * rg + r;
+      kreg[r] = *(const u32x2*)(kp + row * a.k.ss + 4 * cg);
+      vreg[r] = *(const u32x2*)(vp + row * a.v.ss + 4 * cg);
+    }
+  };
+  auto store_tile = [&](int buf) {
+    uint16_t* Ks = smem[buf];
+    uint16_t* Vs = Ks + C::BKV * C::RLD;
+    uint16_t* Kt = Vs + C::BKV * C::RLD;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      *(u32x2*)(&Ks[(4 * rg + r) * C::RLD + 4 * cg]) = kreg[r];
+      *(u32x2*)(&Vs[(4 * rg + r) * C::RLD + 4 * cg]) = vreg[r];
+    }
+#pragma unroll
+    for (int w = 0; w < 2; ++w) {
+      u32x2 c0, c1;
+      const int d = 4 * cg + 2 * w;
+      transpose4x2(kreg[0][w], kreg[1][w], kreg[2][w], kreg[3][w], c0, c1);
+      *(u32x2*)(&Kt[d * C::TLD + 4 * rg]) = c0;
+      *(u32x2*)(&Kt[(d + 1) * C::TLD + 4 * rg]) = c1;
+    }
+  };
+
+  f32x16 acc[C::DB];
+#pragma unroll
+  for (int i = 0; i < C::DB; ++i) acc[i] = f32x16{};
+  const float c = a.scale_log2;
+
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+
+  for (int j = 0; j < nkv; ++j) {
+    const int buf = j & 1;
+    const int kv0 = j * C::BKV;
+    if (j + 1 < nkv) load_tile(kv0 + C::BKV);
+
+    if (wave_valid && (!CAUSAL || kv0 <= qw + 31)) {
+      const uint16_t* Ks = smem[buf];
+      const uint16_t* Vs = Ks + C::BKV * C::RLD;
+      const uint16_t* Kt = Vs + C::BKV * C::RLD;
+      u32x4 sb[C::NKB][2];
+      bool live[C::NKB];
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb) {
+        const int kvb = kv0 + 32 * kb;
+        live[kb] = !CAUSAL || (kvb <= qw + 31);
+        if (!live[kb]) continue;
+        f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+        for (int ks = 0; ks < C::KS; ++ks) {
+          const u32x4 ka = *(const u32x4*)(&Ks[(32 * kb + l32) * C::RLD + 16 * ks + 8 * g]);
+          s = E::mfma(ka, qf[ks], s);
+        }
+#pragma unroll
+        for (int ks = 0; ks < C::KS; ++ks) {
+          const u32x4 va = *(const u32x4*)(&Vs[(32 * kb + l32) * C::RLD + 16 * ks + 8 * g]);
+          dp = E::mfma(va, df[ks], dp);
+        }
+        const bool diag = CAUSAL && (kvb + 31 > qw);
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          float p = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
+          if (diag && kvb + 8 * (r >> 2) + 4 * g + (r & 3) > qrow) p = 0.f;
+          dp[r] = p * (dp[r] - dl);
+        }
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int w = 0; w < 4; ++w)
+            sb[kb][hh][w] = E::pack2(dp[8 * hh + 2 * w], dp[8 * hh + 2 * w + 1]);
+      }
+#pragma unroll
+      for (int kb = 0; kb < C::NKB; ++kb) {
+        if (!live[kb]) continue;
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+          for (int db = 0; db < C::DB; ++db) {
+            const int off = (32 * db + l32) * C::TLD + 32 * kb + 16 * hh + 4 * g;
+            const u32x2 a0 = *(const u32x2*)(&Kt[off]);
+            const u32x2 a1 = *(const u32x2*)(&Kt[off + 8]);
+            acc[db] = E::mfma(u32x4{a0[0], a0[1], a1[0], a1[1]}, sb[kb][hh], acc[db]);
+          }
+        }
+      }
+    }
+
+    if (j + 1 < nkv) store_tile(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (!wave_valid) return;
+  uint16_t* dqrow = (uint16_t*)a.dq.ptr + b * a.dq.sb + h * a.dq.sh + (int64_t)qrow * a.dq.ss;
+  const float sc = a.scale;
+#pragma unroll
+  for (int db = 0; db < C::DB; ++db) {
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      u32x2 w;
+      w[0] = E::pack2(acc[db][4 * jj + 0] * sc, acc[db][4 * jj + 1] * sc);
+      w[1] = E::pack2(acc[db][4 * jj + 2] * sc, acc[db][4 * jj + 3] * sc);
+      *(u32x2*)(dqrow + 32 * db + 8 * jj + 4 * g) = w;
+    }
+  }
+}
+
+template <typename E, int D>
+hipError_t launch_dkdv_d(const AttnArgs& a, hipStream_t st) {
+  const int BH = a.B * a.H;
+  const int nkt = (a.S + DkvCfg<D>::BKV - 1) / DkvCfg<D>::BKV;
+  if (a.causal)
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, true>), dim3(nkt * BH), dim3(256), 0, st, a, nkt);
+  else
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, false>), dim3(nkt * BH), dim3(256), 0, st, a, nkt);
+  return hipGetLastError();
+}
+
+template <typename E, int D>
+hipError_t launch_dq_d(const AttnArgs& a, hipStream_t st) {
+  const int BH = a.B * a.H;
+  const int nqt = (a.S + DqCfg<D>::BQ - 1) / DqCfg<D>::BQ;
+  if (a.causal)
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<E, D, true>), dim3(nqt * BH), dim3(256), 0, st, a, nqt);
+  else
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<E, D, false>), dim3(nqt * BH), dim3(256), 0, st, a, nqt);
+  return hipGetLastError();
+}
+
+template <typename E>
+hipError_t launch_dkdv_e(const AttnArgs& a, hipStream_t st) {
+  if (a.D == 64) return launch_dkdv_d<E, 64>(a, st);
+  return launch_dkdv_d<E, 128>(a, st);
+}
+
+template <typename E>
+hipError_t launch_dq_e(const AttnArgs& a, hipStream_t st) {
+  if (a.D == 64) return launch_dq_d<E, 64>(a, st);
+  return launch_dq_d<E, 128>(a, st);
+}
+
+template <int DT>
+hipError_t launch_delta_t(const AttnArgs& a, hipStream_t st) {
+  const uint32_t nrows = (uint32_t)a.B * a.H * a.S;
+  const FastDiv dS = make_fastdiv(a.S), dH = make_fastdiv(a.H);
+  const dim3 grid((nrows * 8 + 255) / 256);
+  constexpr int V16 = (DT == 0) ? 4 : 8;
+  if (a.D % (8 * V16) == 0)
+    hipLaunchKernelGGL((attn_delta_kernel<DT, V16>), grid, dim3(256), 0, st, a, dS, dH, nrows);
+  else
+    hipLaunchKernelGGL((attn_delta_kernel<DT, 1>), grid, dim3(256), 0, st, a, dS, dH, nrows);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_attn_delta(int dtype, const AttnArgs& a, hipStream_t st) {
+  if (dtype == 0) return launch_delta_t<0>(a, st);
+  if (dtype == 1) return launch_delta_t<1>(a, st);
+  return launch_delta_t<2>(a, st);
+}
+
+hipError_t launch_attn_bwd_dkdv_mfma(int dtype, const AttnArgs& a, hipStream_t st) {
+  if (dtype == 2) return launch_dkdv_e<BF16>(a, st);
+  return launch_dkdv_e<F16>(a, st);
+}
+
+hipError_t launch_attn_bwd_dq_mfma(int dtype, const AttnArgs& a, hipStream_t st) {
+  if (dtype == 2) return launch_dq_e<BF16>(a, st);
+  return launch_dq_e<F16>(a, st);
+}
+
+}  // namespace mi

@@ -1,0 +1,339 @@
+// capi.hip — the extern "C" surface declared in include/mi_attn.h.
+//
+// Validates every argument before anything is enqueued, picks the kernel
+// family (bf16/f16 MFMA when the shape and alignment allow it, exact-fp32
+// VALU otherwise) and reports failures as status codes plus a per-thread
+// message.  No allocation, no synchronisation, no global mutable state apart
+// from the thread-local error text.
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/mi_attn.h"
+#include "mi_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+mi_status fail(mi_status st, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+mi_status fail(mi_status st, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return st;
+}
+
+mi_status ok() {
+  g_last_error.clear();
+  return MI_OK;
+}
+
+int elem_size(int dt) { return dt == MI_F32 ? 4 : 2; }
+
+bool dtype_ok(int dt) { return dt == MI_F32 || dt == MI_F16 || dt == MI_BF16; }
+
+// Tensor [B,H,S,D] with strides {sb, sh, ss, sd}: require sd == 1 and a non-null pointer.
+mi_status check_attn_tensor(const char* name, const void* p, const int64_t* st) {
+  if (p == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
+  if (st == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "%s: null strides", name);
+  if (st[3] != 1)
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: dim stride must be 1 (got %lld)", name,
+                (long long)st[3]);
+  for (int i = 0; i < 3; ++i)
+    if (st[i] < 0) return fail(MI_ERR_INVALID_ARGUMENT, "%s: negative stride", name);
+  return MI_OK;
+}
+
+// 16-byte aligned base and strides that keep every row 16-byte aligned.
+bool aligned16(const void* p, const int64_t* st, int esz) {
+  if (((uintptr_t)p) % 16) return false;
+  for (int i = 0; i < 3; ++i)
+    if ((st[i] * esz) % 16) return false;
+  return true;
+}
+
+mi::TensorArg targ(const void* p, const int64_t* st) {
+  mi::TensorArg t;
+  t.ptr = p;
+  t.sb = st[0];
+  t.sh = st[1];
+  t.ss = st[2];
+  return t;
+}
+
+mi_status check_shape(int dtype, int B, int H, int S, int D, float scale) {
+  if (!dtype_ok(dtype)) return fail(MI_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+  if (B <= 0 || H <= 0 || S <= 0 || D <= 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "sizes must be positive (B=%d H=%d S=%d D=%d)", B, H, S, D);
+  if ((int64_t)B * H * S >= (1ll << 31))
+    return fail(MI_ERR_UNSUPPORTED, "B*H*S = %lld rows exceeds 2^31", (long long)B * H * S);
+  if (!(scale > 0.f) || scale != scale)
+    return fail(MI_ERR_INVALID_ARGUMENT, "scale must be a positive finite number");
+  return MI_OK;
+}
+
+mi_status launched(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(MI_ERR_LAUNCH, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+// Inputs shared by the dK/dV and dQ stages.
+mi_status check_grad_inputs(int dtype, int D, int S, const void* q, const int64_t* qs,
+                            const void* k, const int64_t* ks, const void* v, const int64_t* vs,
+                            const void* dout, const int64_t* dos, const float* lse,
+                            const float* delta) {
+  mi_status st;
+  if ((st = check_attn_tensor("q", q, qs)) != MI_OK) return st;
+  if ((st = check_attn_tensor("k", k, ks)) != MI_OK) return st;
+  if ((st = check_attn_tensor("v", v, vs)) != MI_OK) return st;
+  if ((st = check_attn_tensor("dout", dout, dos)) != MI_OK) return st;
+  if (lse == nullptr || delta == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "lse / delta: null pointer");
+  if (!mi::valu_supports(D) && !mi::mfma_supports(dtype, D, S))
+    return fail(MI_ERR_UNSUPPORTED, "head dim %d not supported (16, 32, 64, 128)", D);
+  return MI_OK;
+}
+
+mi::AttnArgs grad_args(int B, int H, int S, int D, int causal, float scale, const void* q,
+                       const int64_t* qs, const void* k, const int64_t* ks, const void* v,
+                       const int64_t* vs, const void* dout, const int64_t* dos,
+                       const float* lse, const float* delta) {
+  mi::AttnArgs a = {};
+  a.q = targ(q, qs);
+  a.k = targ(k, ks);
+  a.v = targ(v, vs);
+  a.dout = targ(dout, dos);
+  a.lse = const_cast<float*>(lse);
+  a.delta = const_cast<float*>(delta);
+  a.B = B; a.H = H; a.S = S; a.D = D;
+  a.scale = scale;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.causal = causal ? 1 : 0;
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int mi_version(void) { return (1 << 16) | 0; }
+
+const char* mi_status_str(mi_status s) {
+  switch (s) {
+    case MI_OK: return "ok";
+    case MI_ERR_INVALID_ARGUMENT: return "invalid argument";
+    case MI_ERR_UNSUPPORTED: return "unsupported";
+    case MI_ERR_LAUNCH: return "launch failed";
+  }
+  return "unknown status";
+}
+
+const char* mi_last_error(void) { return g_last_error.c_str(); }
+
+mi_status mi_attn_fwd(mi_dtype dtype, int B, int H, int S, int D, int causal, float scale,
+                      const void* q, const int64_t q_strides[4], const void* k,
+                      const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
+                      void* o, const int64_t o_strides[4], float* lse, void* stream) {
+  mi_status st;
+  if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
+  if ((st = check_attn_tensor("q", q, q_strides)) != MI_OK) return st;
+  if ((st = check_attn_tensor("k", k, k_strides)) != MI_OK) return st;
+  if ((st = check_attn_tensor("v", v, v_strides)) != MI_OK) return st;
+  if ((st = check_attn_tensor("o", o, o_strides)) != MI_OK) return st;
+  if (lse == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "lse: null pointer");
+  if (((uintptr_t)lse) % 4) return fail(MI_ERR_INVALID_ARGUMENT, "lse: misaligned");
+
+  mi::AttnArgs a = {};
+  a.q = targ(q, q_strides);
+  a.k = targ(k, k_strides);
+  a.v = targ(v, v_strides);
+  a.o = targ(o, o_strides);
+  a.lse = lse;
+  a.B = B; a.H = H; a.S = S; a.D = D;
+  a.scale = scale;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.causal = causal ? 1 : 0;
+
+  const int esz = elem_size(dtype);
+  const bool al = aligned16(q, q_strides, esz) && aligned16(k, k_strides, esz) &&
+                  aligned16(v, v_strides, esz) && aligned16(o, o_strides, esz);
+  if (al && mi::mfma_supports(dtype, D, S))
+    return launched(mi::launch_attn_fwd_mfma(dtype, a, (hipStream_t)stream), "attn_fwd_mfma");
+  if (!mi::valu_supports(D))
+    return fail(MI_ERR_UNSUPPORTED, "head dim %d not supported (16, 32, 64, 128)", D);
+  return launched(mi::launch_attn_fwd_valu(dtype, a, (hipStream_t)stream), "attn_fwd_valu");
+}
+
+mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal, float scale,
+                      const void* q, const int64_t q_strides[4], const void* k,
+                      const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
+                      const void* o, const int64_t o_strides[4], const void* dout,
+                      const int64_t dout_strides[4], const float* lse, float* delta, void* dq,
+                      const int64_t dq_strides[4], void* dk, const int64_t dk_strides[4],
+                      void* dv, const int64_t dv_strides[4], void* stream) {
+  // Validate everything up front so that nothing is enqueued on a bad call.
+  mi_status st;
+  if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
+  if ((st = check_attn_tensor("o", o, o_strides)) != MI_OK) return st;
+  if ((st = check_attn_tensor("dq", dq, dq_strides)) != MI_OK) return st;
+  if ((st = check_grad_inputs(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
+                              dout_strides, lse, delta)) != MI_OK)
+    return st;
+  if ((st = check_attn_tensor("dk", dk, dk_strides)) != MI_OK) return st;
+  if ((st = check_attn_tensor("dv", dv, dv_strides)) != MI_OK) return st;
+  if ((st = mi_attn_bwd_preprocess(dtype, B, H, S, D, o, o_strides, dout, dout_strides, delta,
+                                   stream)) != MI_OK)
+    return st;
+  if ((st = mi_attn_bwd_dkdv(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
+                             v_strides, dout, dout_strides, lse, delta, dk, dk_strides, dv,
+                             dv_strides, stream)) != MI_OK)
+    return st;
+  return mi_attn_bwd_dq(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
+                        v_strides, dout, dout_strides, lse, delta, dq, dq_strides, stream);
+}
+
+mi_status mi_attn_bwd_preprocess(mi_dtype dtype, int B, int H, int S, int D, const void* o,
+                                 const int64_t o_strides[4], const void* dout,
+                                 const int64_t dout_strides[4], float* delta, void* stream) {
+  mi_status st;
+  if ((st = check_shape(dtype, B, H, S, D, 1.f)) != MI_OK) return st;
+  if ((st = check_attn_tensor("o", o, o_strides)) != MI_OK) return st;
+  if ((st = check_attn_tensor("dout", dout, dout_strides)) != MI_OK) return st;
+  if (delta == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "delta: null pointer");
+  mi::AttnArgs a = {};
+  a.o = targ(o, o_strides);
+  a.dout = targ(dout, dout_strides);
+  a.delta = delta;
+  a.B = B; a.H = H; a.S = S; a.D = D;
+  return launched(mi::launch_attn_delta(dtype, a, (hipStream_t)stream), "attn_delta");
+}
+
+mi_status mi_attn_bwd_dkdv(mi_dtype dtype, int B, int H, int S, int D, int causal, float scale,
+                           const void* q, const int64_t q_strides[4], const void* k,
+                           const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
+                           const void* dout, const int64_t dout_strides[4], const float* lse,
+                           const float* delta, void* dk, const int64_t dk_strides[4], void* dv,
+                           const int64_t dv_strides[4], void* stream) {
+  mi_status st;
+  if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
+  if ((st = check_grad_inputs(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
+                              dout_strides, lse, delta)) != MI_OK)
+    return st;
+  if ((st = check_attn_tensor("dk", dk, dk_strides)) != MI_OK) return st;
+  if ((st = check_attn_tensor("dv", dv, dv_strides)) != MI_OK) return st;
+  mi::AttnArgs a = grad_args(B, H, S, D, causal, scale, q, q_strides, k, k_strides, v, v_strides,
+                             dout, dout_strides, lse, delta);
+  a.dk = targ(dk, dk_strides);
+  a.dv = targ(dv, dv_strides);
+  const int esz = elem_size(dtype);
+  const bool al = aligned16(q, q_strides, esz) && aligned16(k, k_strides, esz) &&
+                  aligned16(v, v_strides, esz) && aligned16(dout, dout_strides, esz) &&
+                  aligned16(dk, dk_strides, esz) && aligned16(dv, dv_strides, esz);
+  hipStream_t s = (hipStream_t)stream;
+  if (al && mi::mfma_supports(dtype, D, S))
+    return launched(mi::launch_attn_bwd_dkdv_mfma(dtype, a, s), "attn_bwd_dkdv_mfma");
+  return launched(mi::launch_attn_bwd_dkdv_valu(dtype, a, s), "attn_bwd_dkdv_valu");
+}
+
+mi_status mi_attn_bwd_dq(mi_dtype dtype, int B, int H, int S, int D, int causal, float scale,
+                         const void* q, const int64_t q_strides[4], const void* k,
+                         const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
+                         const void* dout, const int64_t dout_strides[4], const float* lse,
+                         const float* delta, void* dq, const int64_t dq_strides[4],
+                         void* stream) {
+  mi_status st;
+  if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
+  if ((st = check_grad_inputs(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
+                              dout_strides, lse, delta)) != MI_OK)
+    return st;
+  if ((st = check_attn_tensor("dq", dq, dq_strides)) != MI_OK) return st;
+  mi::AttnArgs a = grad_args(B, H, S, D, causal, scale, q, q_strides, k, k_strides, v, v_strides,
+                             dout, dout_strides, lse, delta);
+  a.dq = targ(dq, dq_strides);
+  const int esz = elem_size(dtype);
+  const bool al = aligned16(q, q_strides, esz) && aligned16(k, k_strides, esz) &&
+                  aligned16(v, v_strides, esz) && aligned16(dout, dout_strides, esz) &&
+                  aligned16(dq, dq_strides, esz);
+  hipStream_t s = (hipStream_t)stream;
+  if (al && mi::mfma_supports(dtype, D, S))
+    return launched(mi::launch_attn_bwd_dq_mfma(dtype, a, s), "attn_bwd_dq_mfma");
+  return launched(mi::launch_attn_bwd_dq_valu(dtype, a, s), "attn_bwd_dq_valu");
+}
+
+static mi_status rope_common(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, int D,
+                             int inverse, int nt, const void* const* ins,
+                             const int64_t* const* in_st, void* const* outs,
+                             const int64_t* const* out_st, const void* cos_tab,
+                             const int64_t cos_strides[2], const void* sin_tab,
+                             const int64_t sin_strides[2], void* stream) {
+  if (!dtype_ok(x_dtype) || !dtype_ok(tab_dtype))
+    return fail(MI_ERR_INVALID_ARGUMENT, "unknown dtype");
+  if (S <= 0 || B <= 0 || H <= 0 || D <= 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "sizes must be positive (S=%d B=%d H=%d D=%d)", S, B, H, D);
+  if (D % 2) return fail(MI_ERR_INVALID_ARGUMENT, "HEAD_DIM must be even (got %d)", D);
+  if ((uint64_t)nt * S * B * H * (D / 2) >= (1ull << 31))
+    return fail(MI_ERR_UNSUPPORTED, "tensor too large for one launch");
+  if (!cos_tab || !sin_tab || !cos_strides || !sin_strides)
+    return fail(MI_ERR_INVALID_ARGUMENT, "cos/sin: null pointer");
+  mi::RopeArgs a = {};
+  a.ntensors = nt;
+  a.cos_tab = cos_tab;
+  a.sin_tab = sin_tab;
+  a.cs_s = cos_strides[0];
+  a.cs_i = cos_strides[1];
+  a.ss_s = sin_strides[0];
+  a.ss_i = sin_strides[1];
+  a.S = S; a.B = B; a.H = H; a.D = D;
+  a.inverse = inverse ? 1 : 0;
+  const int esz = elem_size(x_dtype);
+  const int vecn = 16 / esz;
+  bool vec = (D % vecn == 0) && a.cs_i == 1 && a.ss_i == 1;
+  for (int t = 0; t < nt; ++t) {
+    if (!ins[t] || !outs[t] || !in_st[t] || !out_st[t])
+      return fail(MI_ERR_INVALID_ARGUMENT, "rope tensor %d: null pointer", t);
+    mi::RopeTensor& T = a.t[t];
+    T.in = ins[t];
+    T.out = outs[t];
+    T.is_s = in_st[t][0]; T.is_b = in_st[t][1]; T.is_h = in_st[t][2]; T.is_d = in_st[t][3];
+    T.os_s = out_st[t][0]; T.os_b = out_st[t][1]; T.os_h = out_st[t][2]; T.os_d = out_st[t][3];
+    if (T.is_d != 1 || T.os_d != 1) vec = false;
+    if (((uintptr_t)T.in) % 16 || ((uintptr_t)T.out) % 16) vec = false;
+    for (int i = 0; i < 3; ++i)
+      if ((in_st[t][i] * esz) % 16 || (out_st[t][i] * esz) % 16) vec = false;
+  }
+  return launched(mi::launch_rope(x_dtype, tab_dtype, a, vec, (hipStream_t)stream), "rope");
+}
+
+mi_status mi_rope(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, int D, int inverse,
+                  const void* x, const int64_t x_strides[4], const void* cos_tab,
+                  const int64_t cos_strides[2], const void* sin_tab, const int64_t sin_strides[2],
+                  void* out, const int64_t out_strides[4], void* stream) {
+  const void* ins[1] = {x};
+  const int64_t* ist[1] = {x_strides};
+  void* outs[1] = {out};
+  const int64_t* ost[1] = {out_strides};
+  return rope_common(x_dtype, tab_dtype, S, B, H, D, inverse, 1, ins, ist, outs, ost, cos_tab,
+                     cos_strides, sin_tab, sin_strides, stream);
+}
+
+mi_status mi_rope_qk(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, int D,
+                     int inverse, const void* q, const int64_t q_strides[4], const void* k,
+                     const int64_t k_strides[4], const void* cos_tab, const int64_t cos_strides[2],
+                     const void* sin_tab, const int64_t sin_strides[2], void* q_out,
+                     const int64_t q_out_strides[4], void* k_out, const int64_t k_out_strides[4],
+                     void* stream) {
+  const void* ins[2] = {q, k};
+  const int64_t* ist[2] = {q_strides, k_strides};
+  void* outs[2] = {q_out, k_out};
+  const int64_t* ost[2] = {q_out_strides, k_out_strides};
+  return rope_common(x_dtype, tab_dtype, S, B, H, D, inverse, 2, ins, ist, outs, ost, cos_tab,
+                     cos_strides, sin_tab, sin_strides, stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,151 @@
+// mi_device.h — device-side building blocks shared by the gfx950 kernels.
+//
+// Everything here is written for CDNA4 (gfx950, wave64).  The MFMA helpers wrap
+// the 32x32x16 bf16 / f16 matrix-core instructions; the operand layout they
+// assume is the hardware's:
+//   A (32 x 16): lane l holds A[l % 32][k-slot 0..7 of half l / 32]
+//   B (16 x 32): lane l holds B[k-slot 0..7 of half l / 32][l % 32]
+//   C (32 x 32): lane l, register r holds C[8*(r/4) + 4*(l/32) + r%4][l % 32]
+// The k-slot -> k mapping is the same for A and B, so any assignment of the 16
+// k indices to (half, slot) pairs gives the same product as long as A and B use
+// the same one.  The kernels rely on that to feed a C-layout accumulator
+// (softmax probabilities) straight back in as a B operand.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi {
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) float f32x4;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
+typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// ---------------------------------------------------------------------------
+// 16-bit element types: storage is raw uint16_t, arithmetic is fp32.
+// ---------------------------------------------------------------------------
+struct BF16 {
+  typedef bf16x8 vec8;
+  static __device__ __forceinline__ float to_f32(uint16_t x) {
+    return __uint_as_float(((uint32_t)x) << 16);
+  }
+  // Two floats -> packed pair (round to nearest even, v_cvt_pk_bf16_f32).
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+    bf16x2 v;
+    v[0] = (__bf16)a;
+    v[1] = (__bf16)b;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
+                                                   __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+};
+
+struct F16 {
+  typedef f16x8 vec8;
+  static __device__ __forceinline__ float to_f32(uint16_t x) {
+    return (float)__builtin_bit_cast(_Float16, x);
+  }
+  static __device__ __forceinline__ uint32_t pack2(float a, float b) {
+    typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+    f16x2 v;
+    v[0] = (_Float16)a;
+    v[1] = (_Float16)b;
+    return __builtin_bit_cast(uint32_t, v);
+  }
+  static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
+                                                  __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+};
+
+// Generic element access used by the fp32 VALU kernels and RoPE.
+template <typename T> struct Elem;
+template <> struct Elem<float> {
+  static __device__ __forceinline__ float load(const float* p) { return *p; }
+  static __device__ __forceinline__ void store(float* p, float v) { *p = v; }
+};
+struct bf16_tag {};
+struct f16_tag {};
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t x) { return BF16::to_f32(x); }
+__device__ __forceinline__ float f16_to_f32(uint16_t x) { return F16::to_f32(x); }
+__device__ __forceinline__ uint16_t f32_to_bf16(float x) {
+  return (uint16_t)(BF16::pack2(x, 0.f) & 0xffffu);
+}
+__device__ __forceinline__ uint16_t f32_to_f16(float x) {
+  return (uint16_t)(F16::pack2(x, 0.f) & 0xffffu);
+}
+
+// Storage-type traits for kernels that are generic over fp32 / f16 / bf16.
+template <int DT> struct Store;  // DT: 0 = f32, 1 = f16, 2 = bf16 (mi_dtype values)
+template <> struct Store<0> {
+  typedef float type;
+  static __device__ __forceinline__ float ld(const float* p, int64_t i) { return p[i]; }
+  static __device__ __forceinline__ void st(float* p, int64_t i, float v) { p[i] = v; }
+};
+template <> struct Store<1> {
+  typedef uint16_t type;
+  static __device__ __forceinline__ float ld(const uint16_t* p, int64_t i) { return f16_to_f32(p[i]); }
+  static __device__ __forceinline__ void st(uint16_t* p, int64_t i, float v) { p[i] = f32_to_f16(v); }
+};
+template <> struct Store<2> {
+  typedef uint16_t type;
+  static __device__ __forceinline__ float ld(const uint16_t* p, int64_t i) { return bf16_to_f32(p[i]); }
+  static __device__ __forceinline__ void st(uint16_t* p, int64_t i, float v) { p[i] = f32_to_bf16(v); }
+};
+
+// ---------------------------------------------------------------------------
+// Wave-level helpers.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float xor_shfl(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+__device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// ---------------------------------------------------------------------------
+// Division by a run-time invariant (Granlund-Montgomery): n / d for n < 2^31.
+// ---------------------------------------------------------------------------
+struct FastDiv {
+  uint32_t d, m, s;
+};
+
+__host__ inline FastDiv make_fastdiv(uint32_t d) {
+  FastDiv f;
+  f.d = d;
+  uint32_t s = 0;
+  while ((1ull << s) < d) ++s;
+  f.s = s;
+  f.m = (uint32_t)((((1ull << 32) * ((1ull << s) - d)) / d) + 1);
+  return f;
+}
+
+__device__ __forceinline__ uint32_t fdiv(uint32_t n, const FastDiv& f) {
+  return (__umulhi(n, f.m) + n) >> f.s;
+}
+
+// ---------------------------------------------------------------------------
+// Transposition of a 4-row x 2-column block of 16-bit values held as one
+// 32-bit word per row: returns the two columns, each packed as 2 words
+// (rows 0,1 | rows 2,3).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ void transpose4x2(uint32_t r0, uint32_t r1, uint32_t r2, uint32_t r3,
+                                             u32x2& c0, u32x2& c1) {
+  c0[0] = __builtin_amdgcn_perm(r1, r0, 0x05040100u);
+  c0[1] = __builtin_amdgcn_perm(r3, r2, 0x05040100u);
+  c1[0] = __builtin_amdgcn_perm(r1, r0, 0x07060302u);
+  c1[1] = __builtin_amdgcn_perm(r3, r2, 0x07060302u);
+}
+
+}  // namespace mi

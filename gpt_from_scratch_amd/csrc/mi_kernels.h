@@ -1,0 +1,61 @@
+// mi_kernels.h — argument blocks and host launchers shared between the kernel
+// translation units and the C ABI (capi.hip).  Internal to the library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace mi {
+
+// One attention tensor: base pointer and element strides (batch, head, seq);
+// the dim stride is 1 by contract.
+struct TensorArg {
+  const void* ptr;
+  int64_t sb, sh, ss;
+};
+
+struct AttnArgs {
+  TensorArg q, k, v, o, dout, dq, dk, dv;
+  float* lse;
+  float* delta;
+  int B, H, S, D;
+  float scale;       // softmax scale (1/sqrt(D) in the model)
+  float scale_log2;  // scale * log2(e)
+  int causal;
+};
+
+// Kernel-family launchers.  Each returns hipSuccess or the launch error.
+// `dtype` uses mi_dtype values (0 f32, 1 f16, 2 bf16).
+hipError_t launch_attn_fwd_mfma(int dtype, const AttnArgs& a, hipStream_t st);
+hipError_t launch_attn_bwd_dkdv_mfma(int dtype, const AttnArgs& a, hipStream_t st);
+hipError_t launch_attn_bwd_dq_mfma(int dtype, const AttnArgs& a, hipStream_t st);
+hipError_t launch_attn_fwd_valu(int dtype, const AttnArgs& a, hipStream_t st);
+hipError_t launch_attn_bwd_dkdv_valu(int dtype, const AttnArgs& a, hipStream_t st);
+hipError_t launch_attn_bwd_dq_valu(int dtype, const AttnArgs& a, hipStream_t st);
+hipError_t launch_attn_delta(int dtype, const AttnArgs& a, hipStream_t st);
+
+// Which D values each family is instantiated for.
+bool mfma_supports(int dtype, int D, int S);
+bool valu_supports(int D);
+
+struct RopeTensor {
+  const void* in;
+  void* out;
+  int64_t is_s, is_b, is_h, is_d;  // input strides
+  int64_t os_s, os_b, os_h, os_d;  // output strides
+};
+
+struct RopeArgs {
+  RopeTensor t[2];
+  int ntensors;
+  const void* cos_tab;
+  const void* sin_tab;
+  int64_t cs_s, cs_i, ss_s, ss_i;  // table strides (position, pair index)
+  int S, B, H, D;
+  int inverse;
+};
+
+hipError_t launch_rope(int x_dtype, int tab_dtype, const RopeArgs& a, bool vector_ok,
+                       hipStream_t st);
+
+}  // namespace mi

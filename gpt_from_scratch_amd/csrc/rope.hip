@@ -1,0 +1,169 @@
+// rope.hip — rotary position embedding, interleaved pairs, bandwidth-bound.
+//
+// Counterpart of `_rope_kernel` (core/rope_triton.py:74-141): x is [S,B,H,D]
+// with arbitrary strides, pairs are adjacent elements (2i, 2i+1) (:112-115),
+// angles come from cos/sin tables [S, D/2] (:118-123), and
+//   forward: (e, o) -> (e*c - o*s, e*s + o*c)             (:131-133)
+//   inverse: (e, o) -> (e*c + o*s, o*c - e*s)             (:128-130)
+// computed in fp32 and rounded once to the output type.
+//
+// One launch covers q and k (apply_rope_qk, :147-148).  The vector path moves
+// 16 bytes of x per lane (8 bf16/f16 or 4 fp32 values = 4 or 2 pairs) with
+// one global load and one store, so a wave reads whole 1 KiB segments; the
+// index decomposition uses multiply-high division by the run-time sizes.  A
+// scalar path (one pair per lane, any strides) covers layouts the vector
+// path cannot.
+#include "mi_device.h"
+#include "mi_kernels.h"
+
+namespace mi {
+
+namespace {
+
+struct RopeDivs {
+  FastDiv C, H, B, S;
+};
+
+template <int DT>
+__device__ __forceinline__ float ldx(const void* p, int64_t i) {
+  return Store<DT>::ld((const typename Store<DT>::type*)p, i);
+}
+
+__device__ __forceinline__ void rotate(float e, float o, float cs, float sn, int inverse, float& re,
+                                       float& ro) {
+  if (inverse) {
+    re = e * cs + o * sn;
+    ro = o * cs - e * sn;
+  } else {
+    re = e * cs - o * sn;
+    ro = e * sn + o * cs;
+  }
+}
+
+// 16-byte vector path: requires unit dim strides, D % VEC == 0, 16-byte
+// aligned rows, unit pair stride in the tables.
+template <int XDT, int TDT>
+__global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a, RopeDivs dv, uint32_t total) {
+  constexpr int VEC = (XDT == 0) ? 4 : 8;  // elements per lane
+  constexpr int NP = VEC / 2;               // pairs per lane
+  const uint32_t item = blockIdx.x * 256u + threadIdx.x;
+  if (item >= total) return;
+  uint32_t r = fdiv(item, dv.C);
+  const uint32_t cidx = item - r * dv.C.d;
+  uint32_t r2 = fdiv(r, dv.H);
+  const uint32_t h = r - r2 * dv.H.d;
+  r = fdiv(r2, dv.B);
+  const uint32_t b = r2 - r * dv.B.d;
+  r2 = fdiv(r, dv.S);
+  const uint32_t s = r - r2 * dv.S.d;
+  const uint32_t t = r2;  // tensor index (0 = q, 1 = k)
+
+  const RopeTensor& T = a.t[t];
+  const int64_t in_off = s * T.is_s + b * T.is_b + h * T.is_h + (int64_t)cidx * VEC;
+  const int64_t out_off = s * T.os_s + b * T.os_b + h * T.os_h + (int64_t)cidx * VEC;
+  const int pair0 = cidx * NP;
+
+  float cs[NP], sn[NP];
+#pragma unroll
+  for (int p = 0; p < NP; ++p) {
+    cs[p] = ldx<TDT>(a.cos_tab, s * a.cs_s + pair0 + p);
+    sn[p] = ldx<TDT>(a.sin_tab, s * a.ss_s + pair0 + p);
+  }
+
+  if constexpr (XDT == 0) {
+    const f32x4 x = *(const f32x4*)((const float*)T.in + in_off);
+    f32x4 y;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      float re, ro;
+      rotate(x[2 * p], x[2 * p + 1], cs[p], sn[p], a.inverse, re, ro);
+      y[2 * p] = re;
+      y[2 * p + 1] = ro;
+    }
+    *(f32x4*)((float*)T.out + out_off) = y;
+  } else {
+    const u32x4 x = *(const u32x4*)((const uint16_t*)T.in + in_off);
+    u32x4 y;
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const uint32_t w = x[p];
+      float e, o;
+      if constexpr (XDT == 2) {
+        e = __uint_as_float(w << 16);
+        o = __uint_as_float(w & 0xffff0000u);
+      } else {
+        e = F16::to_f32((uint16_t)(w & 0xffffu));
+        o = F16::to_f32((uint16_t)(w >> 16));
+      }
+      float re, ro;
+      rotate(e, o, cs[p], sn[p], a.inverse, re, ro);
+      y[p] = (XDT == 2) ? BF16::pack2(re, ro) : F16::pack2(re, ro);
+    }
+    *(u32x4*)((uint16_t*)T.out + out_off) = y;
+  }
+}
+
+// Scalar path: one pair per lane, any strides.
+template <int XDT, int TDT>
+__global__ __launch_bounds__(256) void rope_pair_kernel(RopeArgs a, RopeDivs dv, uint32_t total) {
+  typedef typename Store<XDT>::type T_;
+  const uint32_t item = blockIdx.x * 256u + threadIdx.x;
+  if (item >= total) return;
+  uint32_t r = fdiv(item, dv.C);
+  const uint32_t i = item - r * dv.C.d;
+  uint32_t r2 = fdiv(r, dv.H);
+  const uint32_t h = r - r2 * dv.H.d;
+  r = fdiv(r2, dv.B);
+  const uint32_t b = r2 - r * dv.B.d;
+  r2 = fdiv(r, dv.S);
+  const uint32_t s = r - r2 * dv.S.d;
+  const uint32_t t = r2;
+
+  const RopeTensor& T = a.t[t];
+  const T_* in = (const T_*)T.in + s * T.is_s + b * T.is_b + h * T.is_h;
+  T_* out = (T_*)T.out + s * T.os_s + b * T.os_b + h * T.os_h;
+  const float e = Store<XDT>::ld(in, (int64_t)(2 * i) * T.is_d);
+  const float o = Store<XDT>::ld(in, (int64_t)(2 * i + 1) * T.is_d);
+  const float cs = ldx<TDT>(a.cos_tab, s * a.cs_s + (int64_t)i * a.cs_i);
+  const float sn = ldx<TDT>(a.sin_tab, s * a.ss_s + (int64_t)i * a.ss_i);
+  float re, ro;
+  rotate(e, o, cs, sn, a.inverse, re, ro);
+  Store<XDT>::st(out, (int64_t)(2 * i) * T.os_d, re);
+  Store<XDT>::st(out, (int64_t)(2 * i + 1) * T.os_d, ro);
+}
+
+template <int XDT, int TDT>
+hipError_t rope_launch(const RopeArgs& a, bool vec, hipStream_t st) {
+  const int vecn = (XDT == 0) ? 4 : 8;
+  const int C = vec ? a.D / vecn : a.D / 2;
+  RopeDivs dv;
+  dv.C = make_fastdiv(C);
+  dv.H = make_fastdiv(a.H);
+  dv.B = make_fastdiv(a.B);
+  dv.S = make_fastdiv(a.S);
+  const uint64_t total = (uint64_t)a.ntensors * a.S * a.B * a.H * C;
+  const dim3 grid((uint32_t)((total + 255) / 256)), block(256);
+  if (vec)
+    hipLaunchKernelGGL((rope_vec_kernel<XDT, TDT>), grid, block, 0, st, a, dv, (uint32_t)total);
+  else
+    hipLaunchKernelGGL((rope_pair_kernel<XDT, TDT>), grid, block, 0, st, a, dv, (uint32_t)total);
+  return hipGetLastError();
+}
+
+template <int XDT>
+hipError_t rope_x(int tab_dtype, const RopeArgs& a, bool vec, hipStream_t st) {
+  if (tab_dtype == 0) return rope_launch<XDT, 0>(a, vec, st);
+  if (tab_dtype == 1) return rope_launch<XDT, 1>(a, vec, st);
+  return rope_launch<XDT, 2>(a, vec, st);
+}
+
+}  // namespace
+
+hipError_t launch_rope(int x_dtype, int tab_dtype, const RopeArgs& a, bool vector_ok,
+                       hipStream_t st) {
+  if (x_dtype == 0) return rope_x<0>(tab_dtype, a, vector_ok, st);
+  if (x_dtype == 1) return rope_x<1>(tab_dtype, a, vector_ok, st);
+  return rope_x<2>(tab_dtype, a, vector_ok, st);
+}
+
+}  // namespace mi

@@ -1,0 +1,162 @@
+/*
+ * mi_attn.h — C ABI of the MI355X (gfx950) attention hot path.
+ *
+ * Causal / non-causal flash attention (forward with saved log-sum-exp, backward
+ * producing dQ, dK, dV) and the interleaved-pair rotary position embedding.
+ * Every entry point takes plain device pointers, element strides and sizes, and
+ * enqueues its kernels on the given HIP stream (a `hipStream_t`, passed as
+ * `void*`; NULL means the null stream).  Nothing here allocates, frees or
+ * synchronises: the caller owns every output and workspace buffer.
+ *
+ * Tensor conventions
+ *   - attention tensors are logically [B, H, S, D]; `*_strides` holds the four
+ *     element strides in that order (batch, head, seq, dim).  The dim stride
+ *     must be 1 (other strides are free).
+ *   - lse and delta are dense fp32 [B, H, S] (natural-log log-sum-exp of the
+ *     scaled, masked scores; delta = rowsum(dO * O)).
+ *   - rope tensors are logically [S, B, H, D] (the layout the model hands to
+ *     RoPE); the cos/sin tables are [S, D/2] with two element strides.
+ *   - dtypes: MI_F32, MI_F16, MI_BF16.  Attention runs on bf16/f16 MFMA when
+ *     D is 64 or 128 and S % 64 == 0; every other supported case runs on an
+ *     exact-fp32 VALU kernel.  Arithmetic is fp32 in all kernels.
+ *
+ * Errors: a non-zero mi_status; mi_last_error() gives a message for the
+ * calling thread.  Arguments are validated before anything is launched.
+ */
+#ifndef MI_ATTN_H
+#define MI_ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+  MI_OK = 0,
+  MI_ERR_INVALID_ARGUMENT = 1, /* bad shape, stride, pointer or dtype */
+  MI_ERR_UNSUPPORTED = 2,      /* valid request that no kernel here covers */
+  MI_ERR_LAUNCH = 3            /* the HIP runtime refused a launch */
+} mi_status;
+
+typedef enum { MI_F32 = 0, MI_F16 = 1, MI_BF16 = 2 } mi_dtype;
+
+/* Library version, (major << 16) | minor. */
+int mi_version(void);
+
+/* Static text for a status code. */
+const char* mi_status_str(mi_status status);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* mi_last_error(void);
+
+/*
+ * Flash-attention forward: O = softmax(Q K^T * scale + mask) V, and
+ * lse[b,h,i] = log sum_j exp(scale * q_i . k_j) over unmasked j.
+ * Replaces the launch of `_attn_fwd` inside FlashAttn.forward,
+ * core/myFlashAttn.py:198-285 (grid :234-236, launch :249-277, M alloc :240).
+ */
+mi_status mi_attn_fwd(mi_dtype dtype, int B, int H, int S, int D, int causal,
+                      float scale,
+                      const void* q, const int64_t q_strides[4],
+                      const void* k, const int64_t k_strides[4],
+                      const void* v, const int64_t v_strides[4],
+                      void* o, const int64_t o_strides[4],
+                      float* lse, void* stream);
+
+/*
+ * Flash-attention backward: delta = rowsum(dO * O) into the caller's fp32
+ * [B,H,S] workspace, then dQ, dK, dV.  lse is the forward's output.
+ * Replaces FlashAttn.backward's three launches, core/myFlashAttn.py:288-441
+ * (`_attn_bwd_precompute` :330, `_attn_bwd_LoopQ` :365, `_attn_bwd_LoopKV` :409).
+ */
+mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal,
+                      float scale,
+                      const void* q, const int64_t q_strides[4],
+                      const void* k, const int64_t k_strides[4],
+                      const void* v, const int64_t v_strides[4],
+                      const void* o, const int64_t o_strides[4],
+                      const void* dout, const int64_t dout_strides[4],
+                      const float* lse, float* delta,
+                      void* dq, const int64_t dq_strides[4],
+                      void* dk, const int64_t dk_strides[4],
+                      void* dv, const int64_t dv_strides[4],
+                      void* stream);
+
+/*
+ * The three stages of mi_attn_bwd as separate entry points, one per kernel of
+ * the reference's backward; calling them in this order equals mi_attn_bwd.
+ *
+ * delta = rowsum(dO * O) (fp32).
+ * Replaces the `_attn_bwd_precompute` launch, core/myFlashAttn.py:323-346.
+ */
+mi_status mi_attn_bwd_preprocess(mi_dtype dtype, int B, int H, int S, int D,
+                                 const void* o, const int64_t o_strides[4],
+                                 const void* dout, const int64_t dout_strides[4],
+                                 float* delta, void* stream);
+
+/*
+ * dK and dV: per key tile, loop over query tiles (needs lse and delta).
+ * Replaces the `_attn_bwd_LoopQ` launch, core/myFlashAttn.py:349-396.
+ */
+mi_status mi_attn_bwd_dkdv(mi_dtype dtype, int B, int H, int S, int D, int causal,
+                           float scale,
+                           const void* q, const int64_t q_strides[4],
+                           const void* k, const int64_t k_strides[4],
+                           const void* v, const int64_t v_strides[4],
+                           const void* dout, const int64_t dout_strides[4],
+                           const float* lse, const float* delta,
+                           void* dk, const int64_t dk_strides[4],
+                           void* dv, const int64_t dv_strides[4],
+                           void* stream);
+
+/*
+ * dQ: per query tile, loop over key tiles (needs lse and delta).
+ * Replaces the `_attn_bwd_LoopKV` launch, core/myFlashAttn.py:398-439.
+ */
+mi_status mi_attn_bwd_dq(mi_dtype dtype, int B, int H, int S, int D, int causal,
+                         float scale,
+                         const void* q, const int64_t q_strides[4],
+                         const void* k, const int64_t k_strides[4],
+                         const void* v, const int64_t v_strides[4],
+                         const void* dout, const int64_t dout_strides[4],
+                         const float* lse, const float* delta,
+                         void* dq, const int64_t dq_strides[4],
+                         void* stream);
+
+/*
+ * Rotary embedding on one tensor x [S,B,H,D] with interleaved pairs (2i, 2i+1):
+ *   forward (inverse = 0): (e, o) -> (e*c - o*s, e*s + o*c)
+ *   inverse (inverse = 1): (e, o) -> (e*c + o*s, o*c - e*s)   (rotation by -theta)
+ * with c = cos[s, i], s = sin[s, i].  x_dtype and tab_dtype are independent.
+ * Replaces `_rope_kernel` launches in TritonRoPE.forward / .backward,
+ * core/rope_triton.py:10-72 (launch :33-40 and :63-70, kernel :74-141).
+ */
+mi_status mi_rope(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, int D,
+                  int inverse,
+                  const void* x, const int64_t x_strides[4],
+                  const void* cos_tab, const int64_t cos_strides[2],
+                  const void* sin_tab, const int64_t sin_strides[2],
+                  void* out, const int64_t out_strides[4],
+                  void* stream);
+
+/*
+ * The same rotation applied to q and k (same shape, dtype and tables) in one
+ * launch.  Replaces the two TritonRoPE.apply calls of apply_rope_qk,
+ * core/rope_triton.py:147-148, and their two backward launches.
+ */
+mi_status mi_rope_qk(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, int D,
+                     int inverse,
+                     const void* q, const int64_t q_strides[4],
+                     const void* k, const int64_t k_strides[4],
+                     const void* cos_tab, const int64_t cos_strides[2],
+                     const void* sin_tab, const int64_t sin_strides[2],
+                     void* q_out, const int64_t q_out_strides[4],
+                     void* k_out, const int64_t k_out_strides[4],
+                     void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI_ATTN_H */

@@ -1,0 +1,13 @@
+"""Test infrastructure: CPU restatement of the reference's attention and RoPE.
+
+Only tests/, ``__graft_entry__.smoke()`` and bench.py's ``cpu_baseline`` leg may
+import this package, and only as the checker (or the timed CPU baseline).  The
+product (gpt_from_scratch_amd) never imports it.
+"""
+from .attention import (attention_backward, attention_bruteforce, attention_forward,
+                        attention_forward_backward_chunked, attention_probs)
+from .rope import rope_apply, rope_tables, rope_tables_f64
+
+__all__ = ["attention_forward", "attention_backward", "attention_probs",
+           "attention_bruteforce", "attention_forward_backward_chunked",
+           "rope_apply", "rope_tables", "rope_tables_f64"]

@@ -1,0 +1,75 @@
+"""Shared helpers of the GPU parity tests: seeded inputs, reference evaluation
+and the tolerance metrics of the attention path.
+
+Tolerances (north star): bf16/fp16 attention outputs and gradients within
+max-abs 2e-2 and mean-rel 1e-2 of the fp32 reference, where
+mean-rel = mean(|got - ref|) / mean(|ref|); fp32 attention within 1e-4;
+RoPE within 1e-3 in fp32.
+"""
+import math
+
+import torch
+
+from oracle import attention_backward, attention_forward, rope_apply, rope_tables
+
+MAX_ABS_BF16 = 2e-2
+MEAN_REL_BF16 = 1e-2
+TOL_FP32 = 1e-4
+
+
+def seeded(shape, seed, std=1.0, dtype=torch.bfloat16):
+    """N(0, std^2) drawn on the CPU from a seeded generator, rounded to dtype."""
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g, dtype=torch.float32) * std).to(dtype)
+
+
+def metrics(got: torch.Tensor, ref: torch.Tensor):
+    got, ref = got.float(), ref.float().to(got.device)
+    err = (got - ref).abs()
+    return float(err.max()), float(err.mean() / ref.abs().mean().clamp_min(1e-30))
+
+
+def assert_close_bf16(name, got, ref, max_abs=MAX_ABS_BF16, mean_rel=MEAN_REL_BF16):
+    ma, mr = metrics(got, ref)
+    assert ma <= max_abs and mr <= mean_rel, f"{name}: max-abs {ma:.3e} mean-rel {mr:.3e}"
+    return ma, mr
+
+
+def reference(q, k, v, do, causal=True, heads_per_chunk=8, with_backward=True):
+    """fp32 evaluation of the oracle on q's device, a few heads at a time.
+
+    q, k, v, do: [B, H, S, D] (any dtype).  Returns dict of fp32 tensors.
+    """
+    B, H, S, D = q.shape
+    dev = q.device
+    out = {"o": torch.empty(B, H, S, D, device=dev), "lse": torch.empty(B, H, S, device=dev)}
+    if with_backward:
+        for n in ("dq", "dk", "dv"):
+            out[n] = torch.empty(B, H, S, D, device=dev)
+    for b in range(B):
+        for h0 in range(0, H, heads_per_chunk):
+            sl = (b, slice(h0, h0 + heads_per_chunk))
+            qq, kk, vv = (t[sl].float().contiguous() for t in (q, k, v))
+            o, lse = attention_forward(qq, kk, vv, causal, dtype=torch.float32)
+            out["o"][sl], out["lse"][sl] = o, lse
+            del o, lse
+            if with_backward:
+                dq, dk, dv, _ = attention_backward(qq, kk, vv, do[sl].float().contiguous(), causal,
+                                                   dtype=torch.float32)
+                out["dq"][sl], out["dk"][sl], out["dv"][sl] = dq, dk, dv
+    return out
+
+
+def rope_inputs(B, H, S, D, seed, std=1.0, dtype=torch.bfloat16, device="cuda"):
+    """q, k, v in the model's layout: views of one fused qkv [S, B, 3, H, D]
+    tensor (core/transformer_layer.py:38-44), plus cos/sin in `dtype` and dO
+    [B, H, S, D]."""
+    qkv = seeded((S, B, 3, H, D), seed, std, dtype).to(device)
+    q, k, v = qkv.unbind(2)
+    cos, sin = rope_tables(D, S)
+    do = seeded((B, H, S, D), seed + 1000, 1.0, dtype).to(device)
+    return q, k, v, cos.to(dtype).to(device), sin.to(dtype).to(device), do
+
+
+def scale_of(D):
+    return 1.0 / math.sqrt(D)

@@ -1,0 +1,117 @@
+"""Host-side checks of the C ABI (no GPU needed, nothing is launched).
+
+The library must load, export every function include/mi_attn.h declares, and
+reject invalid arguments with the documented status codes before it touches
+the GPU.
+"""
+import ctypes
+import os
+import re
+
+import pytest
+
+from gpt_from_scratch_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "mi_attn.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:mi_status|int|const char\*)\s+(mi_\w+)\s*\(", text,
+                                 re.M)))
+
+
+def test_header_declares_expected_api():
+    assert _declared() == sorted(_lib.EXPORTED)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.mi_version() >> 16 == 1
+
+
+def test_status_strings():
+    lib = _lib.lib()
+    assert lib.mi_status_str(0) == b"ok"
+    assert lib.mi_status_str(1) == b"invalid argument"
+    assert lib.mi_status_str(2) == b"unsupported"
+    assert lib.mi_status_str(3) == b"launch failed"
+
+
+def _i4(*v):
+    return (ctypes.c_int64 * 4)(*v)
+
+
+def test_fwd_rejects_bad_arguments_before_launch():
+    lib = _lib.lib()
+    st = _i4(0, 0, 64, 1)
+    fake = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    # unknown dtype
+    assert lib.mi_attn_fwd(7, 1, 1, 64, 64, 1, 0.125, fake, st, fake, st, fake, st, fake, st,
+                           fake, None) == 1
+    assert b"dtype" in lib.mi_last_error()
+    # non-positive size
+    assert lib.mi_attn_fwd(2, 1, 0, 64, 64, 1, 0.125, fake, st, fake, st, fake, st, fake, st,
+                           fake, None) == 1
+    # null pointer
+    assert lib.mi_attn_fwd(2, 1, 1, 64, 64, 1, 0.125, None, st, fake, st, fake, st, fake, st,
+                           fake, None) == 1
+    assert b"q: null" in lib.mi_last_error()
+    # non-unit dim stride
+    bad = _i4(0, 0, 64, 2)
+    assert lib.mi_attn_fwd(2, 1, 1, 64, 64, 1, 0.125, fake, bad, fake, st, fake, st, fake, st,
+                           fake, None) == 1
+    assert b"dim stride" in lib.mi_last_error()
+    # unsupported head dim
+    assert lib.mi_attn_fwd(0, 1, 1, 64, 48, 1, 0.125, fake, st, fake, st, fake, st, fake, st,
+                           fake, None) == 2
+    # bad scale
+    assert lib.mi_attn_fwd(2, 1, 1, 64, 64, 1, 0.0, fake, st, fake, st, fake, st, fake, st,
+                           fake, None) == 1
+
+
+def test_rope_rejects_odd_head_dim():
+    lib = _lib.lib()
+    st = _i4(0, 0, 0, 1)
+    ts = (ctypes.c_int64 * 2)(1, 1)
+    fake = ctypes.c_void_p(16)
+    assert lib.mi_rope(2, 2, 4, 1, 1, 7, 0, fake, st, fake, ts, fake, ts, fake, st, None) == 1
+    assert b"even" in lib.mi_last_error()
+
+
+def test_python_api_refuses_cpu_tensors():
+    """No CPU fallback: the product raises on host tensors."""
+    import torch
+    from gpt_from_scratch_amd import apply_flash_attn, apply_rope
+    q = torch.randn(1, 1, 64, 64)
+    with pytest.raises(RuntimeError, match="ROCm GPUs only"):
+        apply_flash_attn(q, q, q)
+    x = torch.randn(4, 1, 1, 8)
+    c = torch.ones(4, 4)
+    with pytest.raises(RuntimeError, match="ROCm GPUs only"):
+        apply_rope(x, c, c)
+
+
+def test_python_api_shape_errors():
+    import torch
+    from gpt_from_scratch_amd import apply_flash_attn, apply_rope
+    q = torch.randn(1, 1, 64, 64)
+    with pytest.raises(AssertionError):
+        apply_flash_attn(q, q[:, :, :32], q)
+    with pytest.raises(AssertionError, match="even"):
+        apply_rope(torch.randn(4, 1, 1, 7), torch.ones(4, 3), torch.ones(4, 3))
+
+
+def test_rotary_embedding_tables_cpu():
+    import torch
+    from gpt_from_scratch_amd import RotaryEmbedding
+    from oracle import rope_tables
+    re_ = RotaryEmbedding(64, max_position_embeddings=16, device="cpu")
+    x = torch.zeros(40, 1, 1, 64, dtype=torch.bfloat16)
+    cos, sin = re_(x, seq_len=40)  # beyond the cache: regrows
+    c, s = rope_tables(64, 40)
+    assert cos.dtype == torch.bfloat16 and cos.shape == (40, 32)
+    assert torch.equal(cos, c.to(torch.bfloat16)) and torch.equal(sin, s.to(torch.bfloat16))

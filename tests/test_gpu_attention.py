@@ -1,0 +1,197 @@
+"""GPU parity of the flash-attention kernels against the oracle.
+
+Configs follow the benchmark definition: C1 fp32 B1 H12 S256 D64 (fwd, 1e-4);
+C2 bf16 B8 H12 S1024 D64; C3 bf16 B2 H16 S4096 D128 (std 0.5); C4 bf16
+B1 H32 S8192 D128 — fwd+bwd within max-abs 2e-2 / mean-rel 1e-2 of fp32.
+Inputs are seeded on the CPU (seeds 1-4) and RoPE theta=10000 is applied to
+q and k through the HIP RoPE kernel first (the model's order).
+"""
+import math
+
+import pytest
+import torch
+
+from gpu_ref import (TOL_FP32, assert_close_bf16, metrics, reference, rope_inputs, seeded)
+from oracle import attention_backward, attention_forward, rope_apply, rope_tables
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(autouse=True)
+def _strict_fp32():
+    torch.backends.cuda.matmul.allow_tf32 = False
+    torch.backends.cudnn.allow_tf32 = False
+    yield
+
+
+def _run(q, k, v, do, causal=True):
+    from gpt_from_scratch_amd import apply_flash_attn
+    q = q.detach().requires_grad_()
+    k = k.detach().requires_grad_()
+    v = v.detach().requires_grad_()
+    o = apply_flash_attn(q, k, v, causal)
+    o.backward(do)
+    return o.detach(), q.grad, k.grad, v.grad
+
+
+def _lse(q, k, v, causal=True):
+    from gpt_from_scratch_amd import flash_attn_forward
+    return flash_attn_forward(q, k, v, causal)[1]
+
+
+def test_c1_fp32_forward_1e4(gpu):
+    """Config 1: fp32 B1 H12 S256 D64, RoPE on q/k with fp32 tables, fwd within 1e-4
+    of PyTorch eager on the CPU."""
+    from gpt_from_scratch_amd import apply_flash_attn, apply_rope_qk
+    B, H, S, D = 1, 12, 256, 64
+    g = torch.Generator().manual_seed(1)
+    q = torch.randn(S, B, H, D, generator=g)
+    k = torch.randn(S, B, H, D, generator=g)
+    v = torch.randn(B, H, S, D, generator=g)
+    cos, sin = rope_tables(D, S)
+    qr, kr = apply_rope_qk(q.to(gpu), k.to(gpu), cos.to(gpu), sin.to(gpu))
+    o = apply_flash_attn(qr.permute(1, 2, 0, 3), kr.permute(1, 2, 0, 3), v.to(gpu), True)
+    torch.cuda.synchronize()
+    # CPU eager fp32 reference of the whole chain
+    qc = rope_apply(q, cos, sin, dtype=torch.float32).permute(1, 2, 0, 3)
+    kc = rope_apply(k, cos, sin, dtype=torch.float32).permute(1, 2, 0, 3)
+    o_ref, lse_ref = attention_forward(qc, kc, v, True, dtype=torch.float32)
+    err = float((o.cpu() - o_ref).abs().max())
+    assert err <= TOL_FP32, err
+    lse = _lse(qr.permute(1, 2, 0, 3), kr.permute(1, 2, 0, 3), v.to(gpu))
+    assert float((lse.cpu() - lse_ref).abs().max()) <= TOL_FP32
+
+
+def test_c1_fp32_backward(gpu):
+    B, H, S, D = 1, 12, 256, 64
+    q, k, v, do = (seeded((B, H, S, D), 10 + i, dtype=torch.float32) for i in range(4))
+    o, dq, dk, dv = _run(q.to(gpu), k.to(gpu), v.to(gpu), do.to(gpu))
+    rdq, rdk, rdv, _ = attention_backward(q, k, v, do, True, dtype=torch.float64)
+    for name, got, ref in (("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+        assert float((got.cpu().double() - ref).abs().max()) <= TOL_FP32, name
+
+
+def _config_check(gpu, B, H, S, D, seed, std, causal=True, dtype=torch.bfloat16,
+                  heads_per_chunk=8):
+    from gpt_from_scratch_amd import apply_rope_qk, flash_attn_forward
+    q, k, v, cos, sin, do = rope_inputs(B, H, S, D, seed, std, dtype, gpu)
+    qr, kr = apply_rope_qk(q, k, cos, sin)
+    qb, kb, vb = qr.permute(1, 2, 0, 3), kr.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3)
+    o, dq, dk, dv = _run(qb, kb, vb, do, causal)
+    _, lse = flash_attn_forward(qb, kb, vb, causal)
+    torch.cuda.synchronize()
+    ref = reference(qb, kb, vb, do, causal, heads_per_chunk)
+    res = {}
+    for name, got in (("o", o), ("lse", lse), ("dq", dq), ("dk", dk), ("dv", dv)):
+        res[name] = assert_close_bf16(name, got, ref[name])
+    return res
+
+
+def test_c2_bf16_fwd_bwd(gpu):
+    _config_check(gpu, 8, 12, 1024, 64, seed=2, std=1.0)
+
+
+def test_c2_shape_cpu_oracle_sample(gpu):
+    """Two heads of the C2 case against the CPU oracle in float64."""
+    from gpt_from_scratch_amd import apply_rope_qk
+    q, k, v, cos, sin, do = rope_inputs(8, 12, 1024, 64, 2, 1.0, torch.bfloat16, gpu)
+    qr, kr = apply_rope_qk(q, k, cos, sin)
+    qb, kb, vb = qr.permute(1, 2, 0, 3), kr.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3)
+    o, dq, dk, dv = _run(qb, kb, vb, do, True)
+    for b, h in ((0, 0), (7, 11)):
+        args = [t[b, h].cpu().double() for t in (qb, kb, vb, do)]
+        ro, _ = attention_forward(*args[:3], True)
+        rdq, rdk, rdv, _ = attention_backward(*args, True)
+        for name, got, ref in (("o", o, ro), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+            assert_close_bf16(f"{name}[{b},{h}]", got[b, h].cpu(), ref)
+
+
+def test_c3_bf16_d128(gpu):
+    _config_check(gpu, 2, 16, 4096, 128, seed=3, std=0.5)
+
+
+def test_c4_bf16_long(gpu):
+    res = _config_check(gpu, 1, 32, 8192, 128, seed=4, std=1.0, heads_per_chunk=4)
+    print("C4 metrics", res)
+
+
+def test_c4_size_independent_properties(gpu):
+    """Causal row 0 attends to key 0 only: O[0] == V[0] exactly and lse[0] is the
+    single scaled score; every P row sums to 1, so sum_j dV_j == sum_i dO_i."""
+    from gpt_from_scratch_amd import flash_attn_forward
+    B, H, S, D = 1, 32, 8192, 128
+    q, k, v, do = (seeded((B, H, S, D), 40 + i).to(gpu) for i in range(4))
+    o, dq, dk, dv = _run(q, k, v, do, True)
+    assert torch.equal(o[:, :, 0], v[:, :, 0])
+    _, lse = flash_attn_forward(q, k, v, True)
+    s00 = (q[:, :, 0].float() * k[:, :, 0].float()).sum(-1) / math.sqrt(D)
+    assert float((lse[:, :, 0] - s00).abs().max()) < 1e-3
+    lhs, rhs = dv.float().sum(2), do.float().sum(2)
+    # bf16 rounding of each dV row bounds the error
+    assert float((lhs - rhs).abs().max() / rhs.abs().max()) < 2e-2
+
+
+@pytest.mark.parametrize("S,D", [(64, 64), (192, 64), (320, 128), (64, 128)])
+def test_partial_tiles(gpu, S, D):
+    """S a multiple of 64 but not of the 128-row tiles: half-valid workgroups."""
+    _config_check(gpu, 1, 3, S, D, seed=S + D, std=1.0)
+
+
+@pytest.mark.parametrize("S,D", [(100, 64), (37, 128), (1, 64), (130, 32)])
+def test_ragged_sequence_lengths(gpu, S, D):
+    """Lengths the matrix-core tiles do not divide (masked tails, VALU kernels)."""
+    _config_check(gpu, 2, 2, S, D, seed=7 + S, std=1.0)
+
+
+def test_noncausal(gpu):
+    _config_check(gpu, 2, 4, 512, 64, seed=11, std=1.0, causal=False)
+    _config_check(gpu, 1, 2, 256, 128, seed=12, std=0.5, causal=False)
+
+
+def test_fp16(gpu):
+    _config_check(gpu, 2, 4, 512, 64, seed=13, std=1.0, dtype=torch.float16)
+    _config_check(gpu, 1, 2, 256, 128, seed=14, std=1.0, dtype=torch.float16)
+
+
+def test_contiguous_and_strided_inputs_agree(gpu):
+    """The model hands permuted views; a contiguous copy must give bit-identical results."""
+    from gpt_from_scratch_amd import apply_rope_qk
+    q, k, v, cos, sin, do = rope_inputs(2, 4, 256, 64, 21, 1.0, torch.bfloat16, gpu)
+    qr, kr = apply_rope_qk(q, k, cos, sin)
+    views = (qr.permute(1, 2, 0, 3), kr.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3))
+    a = _run(*views, do)
+    b = _run(*(t.contiguous() for t in views), do)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_deterministic(gpu):
+    q, k, v, do = (seeded((2, 4, 512, 64), 30 + i).to(gpu) for i in range(4))
+    a = _run(q, k, v, do)
+    b = _run(q, k, v, do)
+    for x, y in zip(a, b):
+        assert torch.equal(x, y)
+
+
+def test_backward_with_strided_grad(gpu):
+    """dO arrives as a permuted view of a contiguous [S,B,H,D] gradient (the
+    reference's backward sees exactly that, core/myFlashAttn.py:338-345)."""
+    from gpt_from_scratch_amd import apply_flash_attn
+    B, H, S, D = 2, 3, 256, 64
+    q, k, v = (seeded((B, H, S, D), 50 + i).to(gpu).requires_grad_() for i in range(3))
+    o = apply_flash_attn(q, k, v)
+    g = seeded((S, B, H, D), 54).to(gpu)
+    (o.permute(2, 0, 1, 3) * g).sum().backward()
+    ref = reference(q.detach(), k.detach(), v.detach(), g.permute(1, 2, 0, 3), True)
+    for name, got in (("dq", q.grad), ("dk", k.grad), ("dv", v.grad)):
+        assert_close_bf16(name, got, ref[name])
+
+
+def test_errors_surface_as_exceptions(gpu):
+    from gpt_from_scratch_amd import apply_flash_attn
+    q = torch.randn(1, 1, 64, 48, device=gpu, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="head dim"):
+        apply_flash_attn(q, q, q)
+    q = torch.randn(1, 1, 64, 64, device=gpu, dtype=torch.bfloat16)
+    with pytest.raises(TypeError):
+        apply_flash_attn(q, q.float(), q)

@@ -1,0 +1,108 @@
+"""GPU parity of the RoPE kernel against the oracle (fp32 within 1e-3, here
+much tighter; bf16 within one bf16 rounding of the fp32 result)."""
+import pytest
+import torch
+
+from gpu_ref import rope_inputs, seeded
+from oracle import rope_apply, rope_tables, rope_tables_f64
+
+pytestmark = pytest.mark.gpu
+
+
+def _bf16_ulp_ok(got, ref):
+    """|got - ref| within one bf16 rounding step of ref (plus a denormal floor)."""
+    got, ref = got.float().cpu(), ref.float().cpu()
+    bound = ref.abs() * 2.0 ** -7 + 1e-30
+    return bool(((got - ref).abs() <= bound).all())
+
+
+def test_fp32_forward_and_inverse(gpu):
+    from gpt_from_scratch_amd import apply_rope
+    from gpt_from_scratch_amd.rope import RoPE
+    S, B, H, D = 256, 1, 12, 64
+    x = seeded((S, B, H, D), 1, dtype=torch.float32)
+    cos, sin = rope_tables(D, S)
+    y = apply_rope(x.to(gpu), cos.to(gpu), sin.to(gpu))
+    ref = rope_apply(x, cos, sin)
+    assert float((y.cpu().double() - ref).abs().max()) < 1e-5
+    # against exact float64 angles the budget is 1e-3
+    c64, s64 = rope_tables_f64(D, S)
+    assert float((y.cpu().double() - rope_apply(x, c64, s64)).abs().max()) < 1e-3
+    xg = x.to(gpu).requires_grad_()
+    g = seeded((S, B, H, D), 2, dtype=torch.float32)
+    RoPE.apply(xg, cos.to(gpu), sin.to(gpu)).backward(g.to(gpu))
+    assert float((xg.grad.cpu().double() - rope_apply(g, cos, sin, inverse=True)).abs().max()) < 1e-5
+
+
+def test_bf16_model_layout_qk(gpu):
+    """q/k are strided views of a fused qkv [S,B,3,H,D]; bf16 tables (the model casts
+    them to the activation dtype)."""
+    from gpt_from_scratch_amd import apply_rope, apply_rope_qk
+    q, k, v, cos, sin, _ = rope_inputs(8, 12, 1024, 64, 2, 1.0, torch.bfloat16, gpu)
+    assert not q.is_contiguous()
+    qr, kr = apply_rope_qk(q, k, cos, sin)
+    assert qr.shape == q.shape and qr.is_contiguous()
+    for x, y in ((q, qr), (k, kr)):
+        ref = rope_apply(x.cpu(), cos.cpu(), sin.cpu(), dtype=torch.float32)
+        assert _bf16_ulp_ok(y, ref)
+    # one launch for both == two single launches, bit for bit
+    assert torch.equal(qr, apply_rope(q, cos, sin))
+    assert torch.equal(kr, apply_rope(k, cos, sin))
+
+
+def test_qk_backward_is_inverse_rotation(gpu):
+    from gpt_from_scratch_amd import apply_rope_qk
+    q, k, v, cos, sin, _ = rope_inputs(2, 4, 128, 64, 3, 1.0, torch.bfloat16, gpu)
+    q = q.detach().requires_grad_()
+    k = k.detach().requires_grad_()
+    qr, kr = apply_rope_qk(q, k, cos, sin)
+    gq = seeded(qr.shape, 4).to(gpu)
+    gk = seeded(kr.shape, 5).to(gpu)
+    (qr.float() * gq.float()).sum().add((kr.float() * gk.float()).sum()).backward()
+    assert _bf16_ulp_ok(q.grad, rope_apply(gq.cpu(), cos.cpu(), sin.cpu(), True, torch.float32))
+    assert _bf16_ulp_ok(k.grad, rope_apply(gk.cpu(), cos.cpu(), sin.cpu(), True, torch.float32))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+def test_odd_layouts(gpu, dtype):
+    """Scalar pair path: D not a multiple of the vector width, transposed tables,
+    non-unit dim stride, S = 1, fp32 tables with 16-bit x."""
+    from gpt_from_scratch_amd import apply_rope
+    for S, B, H, D in ((5, 2, 3, 6), (1, 1, 1, 2), (17, 3, 5, 10)):
+        x = seeded((S, B, H, D), S + D, dtype=dtype).to(gpu)
+        cos, sin = rope_tables(D, S)
+        for c, s in ((cos, sin), (cos.t().contiguous().t(), sin.t().contiguous().t())):
+            y = apply_rope(x, c.to(gpu), s.to(gpu))
+            ref = rope_apply(x.cpu(), c, s, dtype=torch.float32)
+            if dtype == torch.float32:
+                assert float((y.cpu() - ref).abs().max()) < 1e-5
+            else:
+                tol = 2.0 ** -7 if dtype == torch.bfloat16 else 2.0 ** -10
+                assert float(((y.cpu().float() - ref).abs() - ref.abs() * tol).max()) <= 1e-6
+    # non-unit dim stride: every other element of a wider tensor
+    wide = seeded((8, 2, 2, 16), 99, dtype=dtype).to(gpu)
+    x = wide[..., ::2]
+    cos, sin = rope_tables(8, 8)
+    y = apply_rope(x, cos.to(gpu), sin.to(gpu))
+    ref = rope_apply(x.cpu(), cos, sin, dtype=torch.float32)
+    tol = {torch.float32: 0.0, torch.float16: 2.0 ** -10, torch.bfloat16: 2.0 ** -7}[dtype]
+    assert float(((y.cpu().float() - ref).abs() - ref.abs() * tol).max()) <= 1e-5
+
+
+def test_long_sequence_invariants(gpu):
+    """C4 shape: inverse(forward(x)) == x to rounding, per-pair norms preserved."""
+    from gpt_from_scratch_amd import apply_rope
+    from gpt_from_scratch_amd.rope import RoPE
+    S, B, H, D = 8192, 1, 32, 128
+    x = seeded((S, B, H, D), 8, dtype=torch.float32).to(gpu)
+    cos, sin = (t.to(gpu) for t in rope_tables(D, S))
+    y = apply_rope(x, cos, sin)
+    n0 = x[..., 0::2] ** 2 + x[..., 1::2] ** 2
+    n1 = y[..., 0::2] ** 2 + y[..., 1::2] ** 2
+    assert float(((n1 - n0).abs() / n0.clamp_min(1e-6)).max()) < 1e-5
+    xg = y.detach().requires_grad_()
+    RoPE.apply(xg, cos, sin).backward(torch.zeros_like(y))  # exercise the graph
+    from gpt_from_scratch_amd import _lib
+    back = torch.empty_like(y)
+    _lib.rope(y, cos, sin, back, inverse=True)
+    assert float((back - x).abs().max()) < 1e-5

@@ -1,0 +1,198 @@
+"""Pins of the CPU oracle (runs without a GPU).
+
+Every check here compares the oracle against something it does not share code
+with: autograd, finite differences, pure-Python loops, closed-form special
+cases, algebraic invariants.  A dropped term, a wrong sign, a transposed operand
+or a wrong scale in oracle/ fails at least one of them.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import (attention_backward, attention_bruteforce, attention_forward,
+                    attention_forward_backward_chunked, attention_probs, rope_apply, rope_tables,
+                    rope_tables_f64)
+
+
+def _randn(*shape, seed=0, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn(*shape, generator=g, dtype=torch.float64) * std
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_forward_matches_bruteforce(causal):
+    S, D = 9, 6
+    q, k, v = (_randn(S, D, seed=s) for s in (1, 2, 3))
+    o, lse = attention_forward(q, k, v, causal)
+    ob, lb = attention_bruteforce(q, k, v, causal)
+    assert torch.allclose(o, torch.tensor(ob, dtype=torch.float64), atol=1e-12)
+    assert torch.allclose(lse, torch.tensor(lb, dtype=torch.float64), atol=1e-12)
+
+
+def test_forward_matches_torch_sdpa_math():
+    # torch's own math-path attention on the CPU: an independent implementation.
+    q, k, v = (_randn(2, 3, 17, 8, seed=s) for s in (4, 5, 6))
+    o, _ = attention_forward(q, k, v, True)
+    ref = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True)
+    assert torch.allclose(o, ref, atol=1e-12)
+    o2, _ = attention_forward(q, k, v, False)
+    ref2 = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=False)
+    assert torch.allclose(o2, ref2, atol=1e-12)
+
+
+def test_causal_row0_is_v0_and_s1_is_identity():
+    q, k, v = (_randn(1, 2, 12, 8, seed=s) for s in (7, 8, 9))
+    o, lse = attention_forward(q, k, v, True)
+    assert torch.allclose(o[..., 0, :], v[..., 0, :], atol=1e-14)
+    # lse of row 0 is the single scaled score
+    assert torch.allclose(lse[..., 0], (q[..., 0, :] * k[..., 0, :]).sum(-1) / math.sqrt(8))
+    o1, _ = attention_forward(q[..., :1, :], k[..., :1, :], v[..., :1, :], False)
+    assert torch.allclose(o1, v[..., :1, :], atol=1e-14)
+
+
+def test_zero_query_gives_prefix_means_and_log_counts():
+    S, D = 16, 8
+    q = torch.zeros(S, D, dtype=torch.float64)
+    k, v = _randn(S, D, seed=10), _randn(S, D, seed=11)
+    o, lse = attention_forward(q, k, v, True)
+    prefix_mean = torch.cumsum(v, 0) / torch.arange(1, S + 1, dtype=torch.float64)[:, None]
+    assert torch.allclose(o, prefix_mean, atol=1e-13)
+    assert torch.allclose(lse, torch.log(torch.arange(1, S + 1, dtype=torch.float64)), atol=1e-13)
+    o2, lse2 = attention_forward(q, k, v, False)
+    assert torch.allclose(o2, v.mean(0).expand(S, D), atol=1e-13)
+    assert torch.allclose(lse2, torch.full((S,), math.log(S), dtype=torch.float64), atol=1e-13)
+
+
+def test_dominant_key_selects_its_value():
+    S, D = 8, 4
+    q = torch.zeros(S, D, dtype=torch.float64)
+    q[:, 0] = 1.0
+    k = torch.zeros(S, D, dtype=torch.float64)
+    k[3, 0] = 400.0  # scaled score 200 for key 3, 0 elsewhere
+    v = _randn(S, D, seed=12)
+    o, _ = attention_forward(q, k, v, False)
+    assert torch.allclose(o, v[3].expand(S, D), atol=1e-12)
+    oc, _ = attention_forward(q, k, v, True)
+    assert torch.allclose(oc[3:], v[3].expand(S - 3, D), atol=1e-12)
+    # rows before 3 cannot see key 3: they average the visible prefix
+    for i in range(3):
+        assert torch.allclose(oc[i], v[: i + 1].mean(0), atol=1e-12)
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_closed_form_backward_matches_autograd(causal):
+    q, k, v = (_randn(2, 2, 13, 8, seed=s).requires_grad_() for s in (13, 14, 15))
+    do = _randn(2, 2, 13, 8, seed=16)
+    o, _ = attention_forward(q, k, v, causal)
+    gq, gk, gv = torch.autograd.grad(o, (q, k, v), do)
+    dq, dk, dv, delta = attention_backward(q.detach(), k.detach(), v.detach(), do, causal)
+    assert torch.allclose(dq, gq, atol=1e-12)
+    assert torch.allclose(dk, gk, atol=1e-12)
+    assert torch.allclose(dv, gv, atol=1e-12)
+    assert torch.allclose(delta, (do * o.detach()).sum(-1), atol=1e-12)
+
+
+def test_backward_finite_differences():
+    S, D = 6, 4
+    q, k, v = (_randn(S, D, seed=s) for s in (17, 18, 19))
+    do = _randn(S, D, seed=20)
+    dq, dk, dv, _ = attention_backward(q, k, v, do, True)
+    eps = 1e-6
+
+    def loss(args):
+        return float((attention_forward(args["q"], args["k"], args["v"], True)[0] * do).sum())
+
+    base = {"q": q, "k": k, "v": v}
+    for name, g in (("q", dq), ("k", dk), ("v", dv)):
+        for idx in [(0, 0), (2, 3), (5, 1), (3, 2)]:
+            plus, minus = dict(base), dict(base)
+            plus[name] = base[name].clone()
+            minus[name] = base[name].clone()
+            plus[name][idx] += eps
+            minus[name][idx] -= eps
+            fd = (loss(plus) - loss(minus)) / (2 * eps)
+            assert abs(fd - float(g[idx])) < 1e-7, (name, idx, fd, float(g[idx]))
+
+
+def test_ds_rows_sum_to_zero_and_delta_identity():
+    q, k, v = (_randn(1, 1, 20, 8, seed=s) for s in (21, 22, 23))
+    do = _randn(1, 1, 20, 8, seed=24)
+    p = attention_probs(q, k, True)
+    dp = do @ v.transpose(-1, -2)
+    _, _, _, delta = attention_backward(q, k, v, do, True)
+    assert torch.allclose(delta, (p * dp).sum(-1), atol=1e-12)
+    ds = p * (dp - delta[..., None])
+    assert torch.allclose(ds.sum(-1), torch.zeros_like(delta), atol=1e-12)
+    # dV column sums: sum_j dV_j = sum_i dO_i (each P row sums to 1)
+    _, _, dv, _ = attention_backward(q, k, v, do, True)
+    assert torch.allclose(dv.sum(-2), do.sum(-2), atol=1e-12)
+
+
+def test_chunked_matches_batched():
+    q, k, v, do = (_randn(2, 3, 32, 8, seed=s) for s in (25, 26, 27, 28))
+    out = attention_forward_backward_chunked(q, k, v, do, True, dtype=torch.float64)
+    o, lse = attention_forward(q, k, v, True)
+    dq, dk, dv, delta = attention_backward(q, k, v, do, True)
+    for a, b in ((out["o"], o), (out["lse"], lse), (out["dq"], dq), (out["dk"], dk),
+                 (out["dv"], dv), (out["delta"], delta)):
+        assert torch.allclose(a, b, atol=1e-12)
+
+
+# ------------------------------------------------------------------ RoPE
+
+
+def test_rope_tables_match_float64_angles():
+    c32, s32 = rope_tables(64, 1024)
+    c64, s64 = rope_tables_f64(64, 1024)
+    # fp32 angle rounding at s ~ 1000 is ~6e-5 rad; tables agree to that level
+    assert float((c32.double() - c64).abs().max()) < 2e-4
+    assert float((s32.double() - s64).abs().max()) < 2e-4
+    # theta_i = 10000^(-2i/D): i = 0 is 1 rad / position, i = D/2-1 is the slowest
+    assert torch.allclose(c64[:, 0], torch.cos(torch.arange(1024, dtype=torch.float64)))
+    ang = math.pow(10000.0, -62.0 / 64.0)
+    assert torch.allclose(s64[:, 31], torch.sin(torch.arange(1024, dtype=torch.float64) * ang))
+
+
+def test_rope_is_complex_multiplication():
+    S, B, H, D = 10, 2, 3, 8
+    x = _randn(S, B, H, D, seed=29)
+    c, s = rope_tables_f64(D, S)
+    out = rope_apply(x, c, s)
+    z = torch.complex(x[..., 0::2], x[..., 1::2])
+    ang = torch.atan2(s, c)[:, None, None, :]
+    w = z * torch.exp(1j * ang)
+    assert torch.allclose(out[..., 0::2], w.real, atol=1e-12)
+    assert torch.allclose(out[..., 1::2], w.imag, atol=1e-12)
+
+
+def test_rope_invariants():
+    S, B, H, D = 12, 1, 2, 16
+    x = _randn(S, B, H, D, seed=30)
+    c, s = rope_tables_f64(D, S)
+    y = rope_apply(x, c, s)
+    # pair norms preserved
+    assert torch.allclose(y[..., 0::2] ** 2 + y[..., 1::2] ** 2,
+                          x[..., 0::2] ** 2 + x[..., 1::2] ** 2, atol=1e-12)
+    # inverse undoes forward
+    assert torch.allclose(rope_apply(y, c, s, inverse=True), x, atol=1e-12)
+    # position 0 is the identity
+    assert torch.allclose(y[0], x[0], atol=1e-14)
+    # relative-position property: <R_m q, R_n k> depends only on m - n
+    q = _randn(D, seed=31)
+    k = _randn(D, seed=32)
+    qs = rope_apply(q.expand(S, 1, 1, D).clone(), c, s)[:, 0, 0]
+    ks = rope_apply(k.expand(S, 1, 1, D).clone(), c, s)[:, 0, 0]
+    dots = qs @ ks.T
+    for m in range(3, S):
+        assert abs(float(dots[m, m - 3] - dots[3, 0])) < 1e-10
+
+
+def test_rope_gradient_is_inverse_rotation():
+    S, B, H, D = 5, 2, 2, 8
+    x = _randn(S, B, H, D, seed=33).requires_grad_()
+    c, s = rope_tables_f64(D, S)
+    g = _randn(S, B, H, D, seed=34)
+    (gx,) = torch.autograd.grad(rope_apply(x, c, s), x, g)
+    assert torch.allclose(gx, rope_apply(g, c, s, inverse=True), atol=1e-12)
