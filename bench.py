@@ -41,6 +41,9 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget of the baseline sample")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="after the timed steps, run a plain elementwise kernel that reads and "
+                         "writes 256 MiB each (reference point for HBM byte counters)")
     return ap.parse_args()
 
 
@@ -82,13 +85,15 @@ def cpu_baseline(B, H, S, D, budget_s):
     run(1)  # warm-up
     per_head = run(1)
     nh = max(1, min(B * H, int(budget_s / 3 / max(per_head, 1e-6))))
-    times = [run(nh) for _ in range(3)]
+    first = run(nh)
+    reps = max(3, min(30, int(budget_s / max(first, 1e-6))))
+    times = [first] + [run(nh) for _ in range(reps - 1)]
     t = statistics.median(times)
     flops = attn_flops(1, nh, S, D)["total"]
     return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "cores": threads,
             "kind": "port",
             "sample": f"{nh} of {B * H} (b,h) heads of B{B} H{H} S{S} D{D}: oracle fp32 eager "
-                      f"fwd+bwd on the CPU, median of 3 runs ({t:.2f} s each)"}
+                      f"fwd+bwd on the CPU, median of {reps} runs ({t:.2f} s each)"}
 
 
 def main():
@@ -202,6 +207,16 @@ def main():
     rope_us = r0.elapsed_time(r1) / n_rope * 1e3
     rope_bytes = 4 * B * S * H * D * 2 + 2 * S * (D // 2) * 2
     rope_gbps = rope_bytes / (rope_us * 1e-6) / 1e9
+
+    if args.calibrate_copy:
+        # 64 Mi fp32 elements: exactly 256 MiB read and 256 MiB written by one
+        # elementwise kernel; its byte counters scale the attention kernels'.
+        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.mul(src, 2.0, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
 
     tflops = flops["total"] / (ms_per_step * 1e-3) / 1e12
     out = {
