@@ -88,7 +88,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, int n_kv
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
@@ -304,7 +304,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a, int n_qtil
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
   const int g = lane >> 5;
 

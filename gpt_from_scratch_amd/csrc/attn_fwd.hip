@@ -6,23 +6,34 @@
 // lse = m + ln(l) (:640-649).  Causal tiles above the diagonal are never
 // visited (:670-674); only tiles that straddle the diagonal are masked.
 //
-// Work decomposition (one workgroup = 4 waves = 256 threads):
-//   * a workgroup owns BQ = 128 query rows of one (batch, head); wave w owns
-//     rows [32w, 32w + 32);
-//   * K/V tiles of BKV = 64 keys are staged through LDS, double-buffered: the
-//     next tile is fetched into registers while the current one is consumed;
+// Work decomposition:
+//   * a workgroup (4 waves) owns BQ = 128 query rows of one (batch, head);
+//     wave w owns rows [32w, 32w + 32);
 //   * everything is computed transposed, S^T = K Q^T and O^T = V^T P^T, so that
 //     in the 32x32 accumulator layout each lane holds one query column: the row
-//     statistics are per-lane scalars (one cross-half exchange for the max) and
+//     statistics are per-lane scalars (one v_permlane32_swap for the max) and
 //     the probabilities feed the P V product as a B operand without any
-//     register shuffle.  V is transposed once per tile while it is written to
-//     LDS (4x4 blocks through v_perm), so every MFMA operand read from LDS is a
-//     contiguous 8- or 16-byte access.
+//     register shuffle;
+//   * K/V tiles of BKV = 64 keys are staged through LDS; V is transposed once
+//     per tile while it is written (4x4 blocks through v_perm), so every MFMA
+//     operand read from LDS is a contiguous 8- or 16-byte access;
+//   * software pipeline: while the VALU runs the softmax of tile j, the matrix
+//     cores already compute S for tile j+1, then P V for tile j.  K is staged
+//     two tiles ahead and V one tile ahead (double buffers for each), so one
+//     barrier per tile suffices;
+//   * key tiles below the diagonal run a branch-free body; the diagonal tiles
+//     run a masked body that also skips tiles a wave cannot see;
+//   * the running max is only moved (and O, l rescaled) when a new score
+//     exceeds it by more than 2^8 in exp2 units; otherwise probabilities are
+//     taken against the stale max, which keeps them <= 256 and the result
+//     exact (O and l share the same reference point);
 //   * the grid is linearised heaviest-first: the Q tiles nearest the end of the
 //     sequence (which see the most keys under causal masking) are dispatched
-//     first, and all tiles of one head are dispatched to the same XCD
-//     (consecutive workgroups go round-robin over the 8 XCDs, and the index
-//     stride between tiles of one head is B*H).
+//     first, and all tiles of one head land on the same XCD (workgroups go
+//     round-robin over the 8 XCDs and the index stride between tiles of one
+//     head is B*H).
+#include <type_traits>
+
 #include "mi_device.h"
 #include "mi_kernels.h"
 
@@ -34,15 +45,18 @@ template <int D>
 struct FwdCfg {
   static constexpr int BQ = 128;
   static constexpr int BKV = 64;
-  static constexpr int NT = 256;
-  static constexpr int KLD = D + 8;       // row stride of the K tile in LDS (elements)
-  static constexpr int VLD = BKV + 4;     // row stride of the V^T tile in LDS
-  static constexpr int KS = D / 16;       // MFMA k-steps of Q K^T
-  static constexpr int DB = D / 32;       // 32-row blocks of O^T
-  static constexpr int KCH = BKV * D / 8 / NT;  // 16-byte K chunks per thread
+  static constexpr int NT = 256;                   // 4 waves x 32 query rows
+  static constexpr int KLD = D + 8;                // K tile row stride in LDS (elements)
+  static constexpr int VLD = BKV + 4;              // V^T tile row stride in LDS
+  static constexpr int KS = D / 16;                // MFMA k-steps of K Q^T
+  static constexpr int DB = D / 32;                // 32-row blocks of O^T
+  static constexpr int KCH = BKV * D / 8 / NT;     // 16-byte K chunks per thread
   static constexpr int VCPT = BKV * D / (NT * 4);  // V columns per thread (4 rows each)
-  static constexpr int VCG = D / VCPT;    // V column groups
+  static constexpr int VCG = D / VCPT;             // V column groups
+  static_assert(VCPT == 4 || VCPT == 8, "V staging uses 8- or 16-byte rows");
 };
+
+constexpr float kRescaleSlack = 8.f;  // log2 units: probabilities stay <= 2^8
 
 template <typename E, int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qtiles) {
@@ -52,7 +66,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
@@ -70,51 +84,58 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
   uint16_t* op = (uint16_t*)a.o.ptr + b * a.o.sb + h * a.o.sh;
 
   const int q0 = qt * C::BQ;
-  const int qw = q0 + 32 * wave;          // first query row of this wave
-  const bool wave_valid = qw < S;
-  const int qrow = qw + l32;              // the query row this lane carries
+  const int qw = q0 + 32 * wave;       // first query row of this wave (SGPR)
+  const bool wave_valid = qw < S;      // S % 64 == 0: 32-row blocks are all-or-nothing
+  const int qrow = qw + l32;
 
-  // Q^T operand fragments (B operand of S^T = K Q^T), kept for the whole loop.
   u32x4 qf[C::KS];
 #pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) {
-    if (wave_valid)
-      qf[ks] = *(const u32x4*)(qp + (int64_t)qrow * a.q.ss + 16 * ks + 8 * g);
-    else
-      qf[ks] = u32x4{0, 0, 0, 0};
-  }
+  for (int ks = 0; ks < C::KS; ++ks)
+    qf[ks] = wave_valid ? *(const u32x4*)(qp + (int64_t)qrow * a.q.ss + 16 * ks + 8 * g)
+                        : u32x4{0, 0, 0, 0};
 
   const int kv_end = CAUSAL ? min(q0 + C::BQ, S) : S;
   const int nkv = kv_end / C::BKV;
 
-  // Per-thread staging registers for one K and one V tile.
+  // ---- staging (global -> registers -> LDS) ----
+  // Buffer loads: one descriptor per tile, rebased with scalar arithmetic; the
+  // per-lane byte offsets inside a tile are fixed.
   u32x4 kreg[C::KCH];
   typedef __attribute__((ext_vector_type(C::VCPT / 2))) uint32_t vrow_t;
   vrow_t vreg[4];
-
-  const int v_rg = tid / C::VCG;  // V row group (4 rows)
-  const int v_cg = tid % C::VCG;  // V column group (VCPT columns)
-
-  auto load_tile = [&](int kv0) {
+  const int v_rg = tid / C::VCG;
+  const int v_cg = tid % C::VCG;
+  uint32_t koff[C::KCH], voff[4];
 #pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int ci = tid + C::NT * i;
-      const int row = ci / (D / 8);
-      const int col = (ci % (D / 8)) * 8;
-      kreg[i] = *(const u32x4*)(kp + (int64_t)(kv0 + row) * a.k.ss + col);
-    }
+  for (int i = 0; i < C::KCH; ++i) {
+    const int ci = tid + C::NT * i;
+    koff[i] = (uint32_t)(((ci / (D / 8)) * a.k.ss + (ci % (D / 8)) * 8) * 2);
+  }
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      vreg[r] = *(const vrow_t*)(vp + (int64_t)(kv0 + 4 * v_rg + r) * a.v.ss + C::VCPT * v_cg);
+  for (int r = 0; r < 4; ++r) voff[r] = (uint32_t)(((4 * v_rg + r) * a.v.ss + C::VCPT * v_cg) * 2);
+  auto load_k = [&](int t) {
+    const auto rs = tile_rsrc(kp + (int64_t)t * C::BKV * a.k.ss);
+#pragma unroll
+    for (int i = 0; i < C::KCH; ++i) kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, koff[i], 0, 0);
   };
-  auto store_tile = [&](int buf) {
+  auto load_v = [&](int t) {
+    const auto rs = tile_rsrc(vp + (int64_t)t * C::BKV * a.v.ss);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      if constexpr (C::VCPT == 8)
+        vreg[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[r], 0, 0);
+      else
+        vreg[r] = __builtin_amdgcn_raw_buffer_load_b64(rs, voff[r], 0, 0);
+    }
+  };
+  auto store_k = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < C::KCH; ++i) {
       const int ci = tid + C::NT * i;
-      const int row = ci / (D / 8);
-      const int col = (ci % (D / 8)) * 8;
-      *(u32x4*)(&Ks[buf][row * C::KLD + col]) = kreg[i];
+      *(u32x4*)(&Ks[buf][(ci / (D / 8)) * C::KLD + (ci % (D / 8)) * 8]) = kreg[i];
     }
+  };
+  auto store_v = [&](int buf) {
 #pragma unroll
     for (int w = 0; w < C::VCPT / 2; ++w) {
       u32x2 c0, c1;
@@ -125,99 +146,152 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
     }
   };
 
+  // ---- per-wave compute pieces ----
   f32x16 acc[C::DB];
 #pragma unroll
   for (int i = 0; i < C::DB; ++i) acc[i] = f32x16{};
-  float m_run = -INFINITY;  // running max of scaled scores (log2 units)
-  float l_run = 0.f;        // running sum, this lane's half of the keys only
+  float m_run = -INFINITY;  // running reference max (exp2 units)
+  float l_run = 0.f;        // running sum over this lane's half of the keys
   const float c = a.scale_log2;
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-
-  for (int j = 0; j < nkv; ++j) {
-    const int buf = j & 1;
-    const int kv0 = j * C::BKV;
-    if (j + 1 < nkv) load_tile(kv0 + C::BKV);
-
-    if (wave_valid && (!CAUSAL || kv0 <= qw + 31)) {
-      f32x16 s[2];
-      bool live[2];
+  // S^T for one key tile (two 32-key blocks) from LDS buffer `buf`.
+  auto qk = [&](int buf, f32x16(&s)[2]) {
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        live[kb] = !CAUSAL || (kv0 + 32 * kb <= qw + 31);
-        s[kb] = f32x16{};
-        if (live[kb]) {
-#pragma unroll
-          for (int ks = 0; ks < C::KS; ++ks) {
-            const u32x4 kf = *(const u32x4*)(&Ks[buf][(32 * kb + l32) * C::KLD + 16 * ks + 8 * g]);
-            s[kb] = E::mfma(kf, qf[ks], s[kb]);
-          }
-        }
+        const u32x4 kf = *(const u32x4*)(&Ks[buf][(32 * kb + l32) * C::KLD + 16 * ks + 8 * g]);
+        s[kb] = E::mfma(kf, qf[ks], ks == 0 ? f32x16{} : s[kb]);
       }
-      // Causal mask on blocks that straddle the diagonal; fully masked blocks
-      // are dropped below.
-      float mx = -INFINITY;
+    }
+  };
+  // Softmax of S^T in place, probabilities packed into pb; key tile starts at kv0.
+  auto softmax = [&](f32x16(&s)[2], u32x4(&pb)[2][2], int kv0, bool masked) {
+    if (masked) {
+      const int rel = qrow - kv0 - 4 * g;  // visible iff (kv - kv0 - 4g) <= rel
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        if (!live[kb]) continue;
-        if (CAUSAL && kv0 + 32 * kb + 31 > qw) {
+      for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int kv = kv0 + 32 * kb + 8 * (r >> 2) + 4 * g + (r & 3);
-            if (kv > qrow) s[kb][r] = -INFINITY;
-          }
-        }
+        for (int r = 0; r < 16; ++r)
+          if (32 * kb + 8 * (r >> 2) + (r & 3) > rel) s[kb][r] = -INFINITY;
+    }
+    // NaN-propagating maximum: v_maximum3_f32 chains without input
+    // canonicalisation (2 scores per instruction).
+    float mx = vmax(s[0][0], s[0][1]);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-      }
-      mx = fmaxf(mx, xor_shfl(mx, 32));
-      const float m_new = fmaxf(m_run, mx * c);
+    for (int i = 2; i < 32; i += 2) mx = vmax(vmax(mx, s[i >> 4][i & 15]), s[i >> 4][(i & 15) + 1]);
+    mx = max_halves(mx) * c;
+    if (__any(mx > m_run + kRescaleSlack)) {
+      const float m_new = fmaxf(m_run, mx);
       const float alpha = fast_exp2(m_run - m_new);
       m_run = m_new;
-      float psum = 0.f;
-      u32x4 pb[2][2];
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const float p = live[kb] ? fast_exp2(__builtin_fmaf(s[kb][r], c, -m_new)) : 0.f;
-          s[kb][r] = p;
-          psum += p;
-        }
-#pragma unroll
-        for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-          for (int w = 0; w < 4; ++w)
-            pb[kb][hh][w] = E::pack2(s[kb][8 * hh + 2 * w], s[kb][8 * hh + 2 * w + 1]);
-      }
-      l_run = l_run * alpha + psum;
+      l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < C::DB; ++db) acc[db] *= alpha;
+    }
+    const float mref = m_run;
+    float psum = 0.f;
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-        if (!live[kb]) continue;
+    for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(__builtin_fmaf(s[kb][r], c, -mref));
+        s[kb][r] = p;
+        psum += p;
+      }
 #pragma unroll
-          for (int db = 0; db < C::DB; ++db) {
-            const uint16_t* vrow = &Vt[buf][(32 * db + l32) * C::VLD + 32 * kb + 16 * hh + 4 * g];
-            const u32x2 lo = *(const u32x2*)vrow;
-            const u32x2 hi = *(const u32x2*)(vrow + 8);
-            const u32x4 vf = u32x4{lo[0], lo[1], hi[0], hi[1]};
-            acc[db] = E::mfma(vf, pb[kb][hh], acc[db]);
-          }
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+          pb[kb][hh][w] = E::pack2(s[kb][8 * hh + 2 * w], s[kb][8 * hh + 2 * w + 1]);
+    }
+    l_run += psum;
+  };
+  // O^T += V^T P^T with V^T from LDS buffer `buf`.
+  auto pv = [&](int buf, const u32x4(&pb)[2][2]) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+#pragma unroll
+        for (int db = 0; db < C::DB; ++db) {
+          const uint16_t* vrow = &Vt[buf][(32 * db + l32) * C::VLD + 32 * kb + 16 * hh + 4 * g];
+          const u32x2 lo = *(const u32x2*)vrow;
+          const u32x2 hi = *(const u32x2*)(vrow + 8);
+          acc[db] = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[kb][hh], acc[db]);
         }
       }
     }
+  };
 
-    if (j + 1 < nkv) store_tile(buf ^ 1);
-    __syncthreads();
+  // ---- prologue: K0, V0, K1 in LDS, K2 and V1 in flight; S for tile 0 ----
+  load_k(0);
+  load_v(0);
+  store_k(0);
+  store_v(0);
+  if (nkv > 1) {
+    load_k(1);
+    store_k(1);
+    load_v(1);
   }
+  if (nkv > 2) load_k(2);
+  __syncthreads();
+
+  f32x16 sA[2], sB[2];
+  if (wave_valid) qk(0, sA);
+  // Step 0 overwrites K buffer 0 (K_2 lands where K_0 was): every wave must
+  // be done reading it.
+  __syncthreads();
+
+  // Tile j.  LDS writes first: K_{j+2} into K_j's buffer and V_{j+1} into
+  // V_{j-1}'s buffer (both were last read before the previous barrier); then
+  // the loads of K_{j+3} and V_{j+2} go out, with a whole tile of compute to
+  // land.  S_{j+1} runs on the matrix cores while the VALU turns S_j into P_j;
+  // then O += P_j V_j.
+  auto step = [&](int j, f32x16(&scur)[2], f32x16(&snext)[2], auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
+    const int kv0 = j * C::BKV;
+    if (j + 2 < nkv) store_k(j & 1);
+    if (j + 1 < nkv) store_v((j + 1) & 1);
+    if (j + 3 < nkv) load_k(j + 3);
+    if (j + 2 < nkv) load_v(j + 2);
+    u32x4 pb[2][2];
+    if (!MASKED) {
+      qk((j + 1) & 1, snext);
+      softmax(scur, pb, kv0, false);
+      pv(j & 1, pb);
+    } else if (wave_valid) {
+      if (j + 1 < nkv && (!CAUSAL || (j + 1) * C::BKV <= qw + 31)) qk((j + 1) & 1, snext);
+      if (!CAUSAL || kv0 <= qw + 31) {
+        softmax(scur, pb, kv0, CAUSAL && kv0 + C::BKV - 1 > qw);
+        pv(j & 1, pb);
+      }
+    }
+    __syncthreads();
+  };
+
+  // Branch-free body: tile j lies below the diagonal for every wave of the
+  // workgroup and tile j+1 exists and is visible to every wave.
+  const int n_main = wave_valid ? (CAUSAL ? min(q0 / C::BKV, nkv - 1) : nkv - 1) : 0;
+  int j = 0;
+  for (; j + 1 < n_main; j += 2) {
+    step(j, sA, sB, std::false_type{});
+    step(j + 1, sB, sA, std::false_type{});
+  }
+  if (j < n_main) {
+    step(j, sA, sB, std::false_type{});
+    ++j;
+    sA[0] = sB[0];
+    sA[1] = sB[1];
+  }
+  for (; j + 1 < nkv; j += 2) {
+    step(j, sA, sB, std::true_type{});
+    step(j + 1, sB, sA, std::true_type{});
+  }
+  if (j < nkv) step(j, sA, sB, std::true_type{});
 
   if (!wave_valid) return;
-  const float l_tot = l_run + xor_shfl(l_run, 32);
+  const float l_tot = sum_halves(l_run);
   const float inv_l = 1.f / l_tot;
   uint16_t* orow = op + (int64_t)qrow * a.o.ss;
 #pragma unroll
@@ -236,7 +310,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
 template <typename E, int D>
 hipError_t launch_fwd_d(const AttnArgs& a, hipStream_t st) {
   const int n_qtiles = (a.S + FwdCfg<D>::BQ - 1) / FwdCfg<D>::BQ;
-  dim3 grid(n_qtiles * a.B * a.H), block(256);
+  dim3 grid(n_qtiles * a.B * a.H), block(FwdCfg<D>::NT);
   if (a.causal)
     hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, true>), grid, block, 0, st, a, n_qtiles);
   else

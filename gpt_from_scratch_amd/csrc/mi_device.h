@@ -48,6 +48,12 @@ struct BF16 {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a),
                                                    __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
   }
+  // acc + lo + hi of a packed pair (v_dot2c_f32_bf16 against (1, 1)).
+  static __device__ __forceinline__ float sum2(uint32_t pair, float acc) {
+    typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+    const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pair), one, acc, false);
+  }
 };
 
 struct F16 {
@@ -65,6 +71,11 @@ struct F16 {
   static __device__ __forceinline__ f32x16 mfma(u32x4 a, u32x4 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a),
                                                   __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float sum2(uint32_t pair, float acc) {
+    typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+    const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pair), one, acc, false);
   }
 };
 
@@ -111,8 +122,37 @@ __device__ __forceinline__ float xor_shfl(float v, int mask) {
   return __shfl_xor(v, mask, 64);
 }
 
+// IEEE 754-2019 maximum (NaN-propagating); lowers to v_maximum3_f32 chains.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
+// Reductions over lanes l and l ^ 32 (the two halves of a wave), one
+// v_permlane32_swap each: the swap exchanges the upper half of its first
+// operand with the lower half of its second, so swapping x with itself puts
+// x[l ^ 32] into one of the two results for every lane.
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
+
+// ---------------------------------------------------------------------------
+// Buffer resource for raw buffer loads based at `p` (wave-uniform pointer, so
+// the descriptor lives in SGPRs and per-tile rebasing is scalar arithmetic).
+// Word 3 = 0x00020000: 32-bit data format, no swizzle, no stride (gfx9 family).
+// The range is left open: callers only address rows that exist.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* p) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 0x7fffffff,
+                                           0x00020000);
+}
 
 // ---------------------------------------------------------------------------
 // Division by a run-time invariant (Granlund-Montgomery): n / d for n < 2^31.
