@@ -80,11 +80,13 @@ struct DkvCfg {
   static constexpr int BUF = 2 * BQ * RLD + 2 * D * TLD;  // uint16 per buffer
 };
 
+// One key tile `kt` of head `bh`.  smem: 2 staging buffers; sl: lse*log2e and
+// delta of the staged query tiles.
 template <typename E, int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, int n_kvtiles) {
+__device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const int bh,
+                                          uint16_t (*smem)[DkvCfg<D>::BUF],
+                                          float (*sl)[2 * DkvCfg<D>::BQ]) {
   using C = DkvCfg<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2][C::BUF];
-  __shared__ __attribute__((aligned(16))) float sl[2][2 * C::BQ];  // lse*log2e, delta
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -92,10 +94,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a, int n_kv
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  const int BH = a.B * a.H;
-  const int bid = blockIdx.x;
-  const int kt = bid / BH;  // key tile 0 sees the most query tiles: dispatched first
-  const int bh = bid % BH;
   const int b = bh / a.H;
   const int h = bh % a.H;
   const int S = a.S;
@@ -297,10 +295,11 @@ struct DqCfg {
   static constexpr int BUF = 2 * BKV * RLD + D * TLD;
 };
 
+// One query tile `qt` of head `bh`.  smem: 2 staging buffers.
 template <typename E, int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a, int n_qtiles) {
+__device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const int bh,
+                                        uint16_t (*smem)[DqCfg<D>::BUF]) {
   using C = DqCfg<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2][C::BUF];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -308,10 +307,6 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a, int n_qtil
   const int l32 = lane & 31;
   const int g = lane >> 5;
 
-  const int BH = a.B * a.H;
-  const int bid = blockIdx.x;
-  const int qt = n_qtiles - 1 - bid / BH;
-  const int bh = bid % BH;
   const int b = bh / a.H;
   const int h = bh % a.H;
   const int S = a.S;
@@ -461,14 +456,56 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a, int n_qtil
   }
 }
 
+template <typename E, int D, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2][DkvCfg<D>::BUF];
+  __shared__ __attribute__((aligned(16))) float sl[2][2 * DkvCfg<D>::BQ];
+  const int BH = a.B * a.H;
+  // key tile 0 sees the most query tiles: dispatched first
+  dkdv_body<E, D, CAUSAL>(a, blockIdx.x / BH, blockIdx.x % BH, smem, sl);
+}
+
+template <typename E, int D, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a, int n_qtiles) {
+  __shared__ __attribute__((aligned(16))) uint16_t smem[2][DqCfg<D>::BUF];
+  const int BH = a.B * a.H;
+  dq_body<E, D, CAUSAL>(a, n_qtiles - 1 - (int)(blockIdx.x / BH), blockIdx.x % BH, smem);
+}
+
+// dK/dV and dQ in one launch.  The two workgroup kinds alternate in dispatch
+// order, each heaviest-first (key tile 0 and the last query tile see the most
+// tiles under causal masking), so the short tails of both kinds overlap the
+// long heads of the other and the launch keeps the whole chip busy.  They
+// share one LDS allocation.
+template <int D>
+struct BwdLds {
+  static constexpr int DKV = 2 * DkvCfg<D>::BUF * 2 + 2 * 2 * DkvCfg<D>::BQ * 4;
+  static constexpr int DQ = 2 * DqCfg<D>::BUF * 2;
+  static constexpr int BYTES = DKV > DQ ? DKV : DQ;
+};
+
+template <typename E, int D, bool CAUSAL>
+__global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs a, int n_tiles) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[BwdLds<D>::BYTES];
+  const int BH = a.B * a.H;
+  const int rank = blockIdx.x / BH;
+  const int bh = blockIdx.x % BH;
+  if (rank & 1) {
+    dq_body<E, D, CAUSAL>(a, n_tiles - 1 - (rank >> 1), bh, (uint16_t(*)[DqCfg<D>::BUF])lds);
+  } else {
+    dkdv_body<E, D, CAUSAL>(a, rank >> 1, bh, (uint16_t(*)[DkvCfg<D>::BUF])lds,
+                            (float(*)[2 * DkvCfg<D>::BQ])(lds + 2 * DkvCfg<D>::BUF * 2));
+  }
+}
+
 template <typename E, int D>
 hipError_t launch_dkdv_d(const AttnArgs& a, hipStream_t st) {
   const int BH = a.B * a.H;
   const int nkt = (a.S + DkvCfg<D>::BKV - 1) / DkvCfg<D>::BKV;
   if (a.causal)
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, true>), dim3(nkt * BH), dim3(256), 0, st, a, nkt);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, true>), dim3(nkt * BH), dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, false>), dim3(nkt * BH), dim3(256), 0, st, a, nkt);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, false>), dim3(nkt * BH), dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
@@ -483,6 +520,18 @@ hipError_t launch_dq_d(const AttnArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <typename E, int D>
+hipError_t launch_both_d(const AttnArgs& a, hipStream_t st) {
+  static_assert(DkvCfg<D>::BKV == DqCfg<D>::BQ, "both kinds tile the sequence alike");
+  const int BH = a.B * a.H;
+  const int n = (a.S + DqCfg<D>::BQ - 1) / DqCfg<D>::BQ;
+  if (a.causal)
+    hipLaunchKernelGGL((attn_bwd_kernel<E, D, true>), dim3(2 * n * BH), dim3(256), 0, st, a, n);
+  else
+    hipLaunchKernelGGL((attn_bwd_kernel<E, D, false>), dim3(2 * n * BH), dim3(256), 0, st, a, n);
+  return hipGetLastError();
+}
+
 template <typename E>
 hipError_t launch_dkdv_e(const AttnArgs& a, hipStream_t st) {
   if (a.D == 64) return launch_dkdv_d<E, 64>(a, st);
@@ -492,6 +541,16 @@ hipError_t launch_dkdv_e(const AttnArgs& a, hipStream_t st) {
 template <typename E>
 hipError_t launch_dq_e(const AttnArgs& a, hipStream_t st) {
   if (a.D == 64) return launch_dq_d<E, 64>(a, st);
+  return launch_dq_d<E, 128>(a, st);
+}
+
+// D = 128: the two kinds need different register budgets (the dK/dV kind
+// alone runs at 1 wave/SIMD), so they stay separate launches.
+template <typename E>
+hipError_t launch_both_e(const AttnArgs& a, hipStream_t st) {
+  if (a.D == 64) return launch_both_d<E, 64>(a, st);
+  hipError_t e = launch_dkdv_d<E, 128>(a, st);
+  if (e != hipSuccess) return e;
   return launch_dq_d<E, 128>(a, st);
 }
 
@@ -524,6 +583,11 @@ hipError_t launch_attn_bwd_dkdv_mfma(int dtype, const AttnArgs& a, hipStream_t s
 hipError_t launch_attn_bwd_dq_mfma(int dtype, const AttnArgs& a, hipStream_t st) {
   if (dtype == 2) return launch_dq_e<BF16>(a, st);
   return launch_dq_e<F16>(a, st);
+}
+
+hipError_t launch_attn_bwd_mfma(int dtype, const AttnArgs& a, hipStream_t st) {
+  if (dtype == 2) return launch_both_e<BF16>(a, st);
+  return launch_both_e<F16>(a, st);
 }
 
 }  // namespace mi

@@ -224,6 +224,84 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
     }
   };
 
+  // Mask-free tile with the matrix-core work woven into the softmax.  The 32
+  // scores per lane form 4 groups of 8 (one B operand of P V each).  Group g
+  // issues 1/4 of the next tile's K Q^T MFMAs, turns its 8 scores into
+  // probabilities, and issues the P V MFMAs of group g-1, so that every MFMA
+  // has ~7 VALU instructions behind it to overlap with.  sched_barrier keeps
+  // the compiler from clustering the MFMAs back together.
+  auto hot = [&](int kbuf, int vbuf, f32x16(&s)[2], f32x16(&sn)[2]) {
+    constexpr int KPG = C::KS / 4;  // k-steps of the next tile's S per group
+    // K fragments of group g+1 are read while group g computes.
+    u32x4 kf[2][KPG][2];
+    auto read_k = [&](int grp, u32x4(&dst)[KPG][2]) {
+#pragma unroll
+      for (int kk = 0; kk < KPG; ++kk)
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          dst[kk][nb] = *(const u32x4*)(&Ks[kbuf][(32 * nb + l32) * C::KLD +
+                                                  16 * (KPG * grp + kk) + 8 * g]);
+    };
+    read_k(0, kf[0]);
+
+    float mx = vmax(s[0][0], s[0][1]);
+#pragma unroll
+    for (int i = 2; i < 32; i += 2) mx = vmax(vmax(mx, s[i >> 4][i & 15]), s[i >> 4][(i & 15) + 1]);
+    mx = max_halves(mx) * c;
+    if (__any(mx > m_run + kRescaleSlack)) {
+      const float m_new = fmaxf(m_run, mx);
+      const float alpha = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= alpha;
+#pragma unroll
+      for (int db = 0; db < C::DB; ++db) acc[db] *= alpha;
+    }
+    const float mref = m_run;
+    float psum = 0.f;
+    u32x4 pb[4];
+    auto pv_group = [&](int grp) {
+      const int kb = grp >> 1, hh = grp & 1;
+#pragma unroll
+      for (int db = 0; db < C::DB; ++db) {
+        const uint16_t* vrow = &Vt[vbuf][(32 * db + l32) * C::VLD + 32 * kb + 16 * hh + 4 * g];
+        const u32x2 lo = *(const u32x2*)vrow;
+        const u32x2 hi = *(const u32x2*)(vrow + 8);
+        acc[db] = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[grp], acc[db]);
+      }
+    };
+#pragma unroll
+    for (int grp = 0; grp < 4; ++grp) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int kb = grp >> 1, hh = grp & 1;
+      if (grp < 3) read_k(grp + 1, kf[(grp + 1) & 1]);
+#pragma unroll
+      for (int kk = 0; kk < KPG; ++kk) {
+        const int ks = KPG * grp + kk;
+#pragma unroll
+        for (int nb = 0; nb < 2; ++nb)
+          sn[nb] = E::mfma(kf[grp & 1][kk][nb], qf[ks], ks == 0 ? f32x16{} : sn[nb]);
+      }
+      float p[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        p[i] = fast_exp2(__builtin_fmaf(s[kb][8 * hh + i], c, -mref));
+        psum += p[i];
+      }
+#pragma unroll
+      for (int w = 0; w < 4; ++w) pb[grp][w] = E::pack2(p[2 * w], p[2 * w + 1]);
+      if (grp > 0) pv_group(grp - 1);
+      // 2*KPG + DB MFMAs against ~28 VALU ops: one MFMA, then a run of VALU.
+#pragma unroll
+      for (int m = 0; m < 2 * KPG + (grp > 0 ? C::DB : 0); ++m) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    pv_group(3);
+    l_run += psum;
+  };
+
   // ---- prologue: K0, V0, K1 in LDS, K2 and V1 in flight; S for tile 0 ----
   load_k(0);
   load_v(0);
@@ -257,9 +335,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
     if (j + 2 < nkv) load_v(j + 2);
     u32x4 pb[2][2];
     if (!MASKED) {
-      qk((j + 1) & 1, snext);
-      softmax(scur, pb, kv0, false);
-      pv(j & 1, pb);
+      hot((j + 1) & 1, j & 1, scur, snext);
     } else if (wave_valid) {
       if (j + 1 < nkv && (!CAUSAL || (j + 1) * C::BKV <= qw + 31)) qk((j + 1) & 1, snext);
       if (!CAUSAL || kv0 <= qw + 31) {

@@ -190,6 +190,19 @@ mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal, fl
   if ((st = mi_attn_bwd_preprocess(dtype, B, H, S, D, o, o_strides, dout, dout_strides, delta,
                                    stream)) != MI_OK)
     return st;
+  const int esz = elem_size(dtype);
+  if (mi::mfma_supports(dtype, D, S) && aligned16(q, q_strides, esz) &&
+      aligned16(k, k_strides, esz) && aligned16(v, v_strides, esz) &&
+      aligned16(dout, dout_strides, esz) && aligned16(dq, dq_strides, esz) &&
+      aligned16(dk, dk_strides, esz) && aligned16(dv, dv_strides, esz)) {
+    // dK/dV and dQ in one launch.
+    mi::AttnArgs a = grad_args(B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
+                               v_strides, dout, dout_strides, lse, delta);
+    a.dq = targ(dq, dq_strides);
+    a.dk = targ(dk, dk_strides);
+    a.dv = targ(dv, dv_strides);
+    return launched(mi::launch_attn_bwd_mfma(dtype, a, (hipStream_t)stream), "attn_bwd_mfma");
+  }
   if ((st = mi_attn_bwd_dkdv(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
                              v_strides, dout, dout_strides, lse, delta, dk, dk_strides, dv,
                              dv_strides, stream)) != MI_OK)

@@ -28,6 +28,8 @@ struct AttnArgs {
 // `dtype` uses mi_dtype values (0 f32, 1 f16, 2 bf16).
 hipError_t launch_attn_fwd_mfma(int dtype, const AttnArgs& a, hipStream_t st);
 hipError_t launch_attn_bwd_dkdv_mfma(int dtype, const AttnArgs& a, hipStream_t st);
+// dK/dV and dQ in one launch (same results as the two launches above).
+hipError_t launch_attn_bwd_mfma(int dtype, const AttnArgs& a, hipStream_t st);
 hipError_t launch_attn_bwd_dq_mfma(int dtype, const AttnArgs& a, hipStream_t st);
 hipError_t launch_attn_fwd_valu(int dtype, const AttnArgs& a, hipStream_t st);
 hipError_t launch_attn_bwd_dkdv_valu(int dtype, const AttnArgs& a, hipStream_t st);
