@@ -1,0 +1,96 @@
+"""CPU checks of the config-5 harness pieces (no kernels involved: attention and
+RoPE are the oracle's here)."""
+import math
+
+import torch
+
+from gpt_from_scratch_amd.harness import GPT, GPTConfig, MixedPrecisionAdamW, SoftmaxCrossEntropy
+from gpt_from_scratch_amd.harness.gpt import RMSNorm
+from oracle import attention_forward, rope_apply
+
+
+def eager_attention(q, k, v):
+    return attention_forward(q, k, v, True, dtype=torch.float32)[0].to(q.dtype)
+
+
+def eager_rope(q, k, cos, sin):
+    return (rope_apply(q, cos, sin, dtype=torch.float32).to(q.dtype),
+            rope_apply(k, cos, sin, dtype=torch.float32).to(k.dtype))
+
+
+def test_cross_entropy_matches_torch():
+    z = torch.randn(7, 3, 19, dtype=torch.float64, requires_grad=True)
+    t = torch.randint(0, 19, (7, 3))
+    loss = SoftmaxCrossEntropy.apply(z, t)
+    ref = torch.nn.functional.cross_entropy(z.reshape(-1, 19), t.reshape(-1), reduction="none")
+    assert torch.allclose(loss, ref.reshape(7, 3), atol=1e-12)
+    (g,) = torch.autograd.grad(loss.sum(), z)
+    z2 = z.detach().requires_grad_()
+    (g2,) = torch.autograd.grad(
+        torch.nn.functional.cross_entropy(z2.reshape(-1, 19), t.reshape(-1), reduction="sum"), z2)
+    assert torch.allclose(g, g2, atol=1e-12)
+
+
+def test_rmsnorm_formula():
+    n = RMSNorm(16, 1e-5, "cpu")
+    n.weight.data.uniform_(0.5, 1.5)
+    x = torch.randn(4, 16, dtype=torch.float64)
+    y = n(x)
+    ref = x / torch.sqrt((x ** 2).mean(-1, keepdim=True) + 1e-5) * n.weight.double()
+    assert torch.allclose(y, ref, atol=1e-6)
+
+
+def test_parameter_count_matches_reference_config():
+    m = GPT(GPTConfig(), "cpu")
+    # embedding + head 2*V*H, per layer qkv 3H^2 + out H^2 + gate_up 2HI + down IH + 2 norms,
+    # final norm
+    V, H, I, L = 50257, 768, 3072, 12
+    expect = 2 * V * H + L * (4 * H * H + 3 * H * I + 2 * H) + H
+    assert sum(p.numel() for p in m.parameters()) == expect == 190_460_160
+
+
+def test_optimizer_matches_adamw_in_fp32_math():
+    torch.manual_seed(0)
+    lin = torch.nn.Linear(8, 4, bias=False)
+    ref = lin.weight.detach().clone().to(torch.bfloat16).float().requires_grad_(True)
+    opt = MixedPrecisionAdamW(lin, clip=0.0)
+    ref_opt = torch.optim.AdamW([ref], lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1)
+    for i in range(3):
+        opt.zero_grad()
+        x = torch.randn(5, 8).to(torch.bfloat16)
+        lin(x).float().pow(2).sum().backward()
+        g = lin.weight.grad.float().clone()
+        opt.step()
+        ref.grad = g
+        ref_opt.step()
+        assert torch.equal(lin.weight.data, ref.detach().to(torch.bfloat16))
+
+
+def test_clipping_bounds_the_update():
+    torch.manual_seed(1)
+    lin = torch.nn.Linear(4, 4, bias=False)
+    opt = MixedPrecisionAdamW(lin, clip=1.0)
+    opt.zero_grad()
+    lin.weight.grad.copy_(torch.full((4, 4), 100.0))
+    opt.step()
+    # the gradient buffer was rescaled in place to the clip norm before the step
+    assert abs(float(opt.grad_buf.float().norm()) - 1.0) < 1e-2
+
+
+def test_tiny_model_trains_on_cpu_with_eager_attention():
+    cfg = GPTConfig(vocab_size=97, hidden_size=64, num_layers=2, num_attention_heads=4,
+                    max_position_embeddings=32, intermediate_size=128)
+    torch.manual_seed(3)
+    model = GPT(cfg, "cpu", attention=eager_attention, rope=eager_rope)
+    opt = MixedPrecisionAdamW(model)
+    ids = torch.randint(0, 97, (2, 17))
+    inputs, labels = ids[:, :-1], ids[:, 1:].transpose(0, 1).contiguous()
+    losses = []
+    for _ in range(8):
+        opt.zero_grad()
+        loss = SoftmaxCrossEntropy.apply(model(inputs), labels).mean()
+        loss.backward()
+        opt.step()
+        losses.append(float(loss))
+    assert abs(losses[0] - math.log(97)) < 0.5
+    assert losses[-1] < losses[0]
