@@ -41,6 +41,8 @@ def parse_args():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget of the baseline sample")
+    ap.add_argument("--no-gpt", action="store_true",
+                    help="skip the config-5 GPT train-step measurement")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run a plain elementwise kernel that reads and "
                          "writes 256 MiB each (reference point for HBM byte counters)")
@@ -96,6 +98,33 @@ def cpu_baseline(B, H, S, D, budget_s):
                       f"fwd+bwd on the CPU, median of {reps} runs ({t:.2f} s each)"}
 
 
+def gpt_train(dev, steps=20, warmup=3):
+    """Config 5: GPT train step (12L / 768 / 12 heads / SwiGLU 3072 / RMSNorm /
+    vocab 50257, B=8, S=1024, TP=1, DP=1) with attention and RoPE on the HIP
+    kernels; tokens/s = B*S*steps / wall time (train.py:196-198), beside the
+    same step with attention done by plain PyTorch matmul/softmax (fp32 math)."""
+    import torch
+    from gpt_from_scratch_amd.harness import GPTConfig, train
+
+    def eager_attention(q, k, v):
+        S, Dh = q.shape[-2], q.shape[-1]
+        s = torch.matmul(q.float(), k.float().transpose(-1, -2).contiguous()) / math.sqrt(Dh)
+        mask = torch.ones(S, S, dtype=torch.bool, device=q.device).tril()
+        p = torch.softmax(s.masked_fill(~mask, float("-inf")), dim=-1)
+        return torch.matmul(p, v.float()).to(q.dtype)
+
+    cfg = GPTConfig()
+    losses, tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup)
+    _, eager_tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup,
+                         attention=eager_attention)
+    return {"workload": "config 5: 12L/768/12H SwiGLU RMSNorm vocab 50257, B8 S1024, bf16 params "
+                        "+ fp32 AdamW master, TP=1 DP=1, synthetic uint16 ids",
+            "steps": steps, "tokens_per_s": round(tps, 1),
+            "ms_per_step": round(8 * 1024 / tps * 1e3, 3),
+            "tokens_per_s_eager_attention": round(eager_tps, 1),
+            "loss_first": round(losses[0], 4), "loss_last": round(losses[-1], 4)}
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -136,14 +165,12 @@ def main():
     hdr = (dt, B, H, S, D)
     fwd_args = hdr + (1, scale, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(O), ST(O), P(LSE), sp)
     pre_args = hdr + (P(O), ST(O), P(do), ST(do), P(DELTA), sp)
-    dkdv_args = hdr + (1, scale, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(do), ST(do), P(LSE),
-                       P(DELTA), P(dK), ST(dK), P(dV), ST(dV), sp)
-    dq_args = hdr + (1, scale, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(do), ST(do), P(LSE),
-                     P(DELTA), P(dQ), ST(dQ), sp)
+    grads_args = hdr + (1, scale, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(do), ST(do), P(LSE),
+                        P(DELTA), P(dQ), ST(dQ), P(dK), ST(dK), P(dV), ST(dV), sp)
+    # The product path: mi_attn_fwd, then mi_attn_bwd = preprocess + grads.
     calls = [("attn_fwd", lib.mi_attn_fwd, fwd_args),
              ("attn_bwd_preprocess", lib.mi_attn_bwd_preprocess, pre_args),
-             ("attn_bwd_dkdv", lib.mi_attn_bwd_dkdv, dkdv_args),
-             ("attn_bwd_dq", lib.mi_attn_bwd_dq, dq_args)]
+             ("attn_bwd", lib.mi_attn_bwd_grads, grads_args)]
 
     def step(evs=None):
         for i, (name, fn, a) in enumerate(calls):
@@ -177,8 +204,7 @@ def main():
     for i, (name, _, _) in enumerate(calls):
         per_kernel_us[name] = statistics.mean(e[i].elapsed_time(e[i + 1]) for e in evs) * 1e3
 
-    kflops = {"attn_fwd": flops["fwd"], "attn_bwd_dkdv": flops["dkdv"],
-              "attn_bwd_dq": flops["dq"]}
+    kflops = {"attn_fwd": flops["fwd"], "attn_bwd": flops["bwd"]}
     kernels = {}
     for name, us in per_kernel_us.items():
         ent = {"avg_us": round(us, 3)}
@@ -234,6 +260,8 @@ def main():
                  "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                  "frac": round(rope_gbps / PEAK_HBM_GBPS, 4), "algorithmic_bytes": rope_bytes},
     }
+    if not args.no_gpt:
+        out["gpt_train"] = gpt_train(dev)
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(B, H, S, D, args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -23,7 +23,8 @@ _DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 
 # Every function declared in include/mi_attn.h.
 EXPORTED = ("mi_version", "mi_status_str", "mi_last_error", "mi_attn_fwd", "mi_attn_bwd",
-            "mi_attn_bwd_preprocess", "mi_attn_bwd_dkdv", "mi_attn_bwd_dq", "mi_rope",
+            "mi_attn_bwd_preprocess", "mi_attn_bwd_grads", "mi_attn_bwd_dkdv", "mi_attn_bwd_dq",
+            "mi_rope",
             "mi_rope_qk")
 
 _lib = None
@@ -53,6 +54,9 @@ def _declare(lib):
                                 p, p, p, i64p, p, i64p, p, i64p, p]
     lib.mi_attn_bwd_preprocess.restype = i
     lib.mi_attn_bwd_preprocess.argtypes = [i, i, i, i, i, p, i64p, p, i64p, p, p]
+    lib.mi_attn_bwd_grads.restype = i
+    lib.mi_attn_bwd_grads.argtypes = [i, i, i, i, i, i, f, p, i64p, p, i64p, p, i64p, p, i64p,
+                                      p, p, p, i64p, p, i64p, p, i64p, p]
     lib.mi_attn_bwd_dkdv.restype = i
     lib.mi_attn_bwd_dkdv.argtypes = [i, i, i, i, i, i, f, p, i64p, p, i64p, p, i64p, p, i64p,
                                      p, p, p, i64p, p, i64p, p]

@@ -190,12 +190,32 @@ mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal, fl
   if ((st = mi_attn_bwd_preprocess(dtype, B, H, S, D, o, o_strides, dout, dout_strides, delta,
                                    stream)) != MI_OK)
     return st;
+  return mi_attn_bwd_grads(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
+                           v_strides, dout, dout_strides, lse, delta, dq, dq_strides, dk,
+                           dk_strides, dv, dv_strides, stream);
+}
+
+mi_status mi_attn_bwd_grads(mi_dtype dtype, int B, int H, int S, int D, int causal, float scale,
+                            const void* q, const int64_t q_strides[4], const void* k,
+                            const int64_t k_strides[4], const void* v,
+                            const int64_t v_strides[4], const void* dout,
+                            const int64_t dout_strides[4], const float* lse, const float* delta,
+                            void* dq, const int64_t dq_strides[4], void* dk,
+                            const int64_t dk_strides[4], void* dv, const int64_t dv_strides[4],
+                            void* stream) {
+  mi_status st;
+  if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
+  if ((st = check_grad_inputs(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
+                              dout_strides, lse, delta)) != MI_OK)
+    return st;
+  if ((st = check_attn_tensor("dq", dq, dq_strides)) != MI_OK) return st;
+  if ((st = check_attn_tensor("dk", dk, dk_strides)) != MI_OK) return st;
+  if ((st = check_attn_tensor("dv", dv, dv_strides)) != MI_OK) return st;
   const int esz = elem_size(dtype);
   if (mi::mfma_supports(dtype, D, S) && aligned16(q, q_strides, esz) &&
       aligned16(k, k_strides, esz) && aligned16(v, v_strides, esz) &&
       aligned16(dout, dout_strides, esz) && aligned16(dq, dq_strides, esz) &&
       aligned16(dk, dk_strides, esz) && aligned16(dv, dv_strides, esz)) {
-    // dK/dV and dQ in one launch.
     mi::AttnArgs a = grad_args(B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
                                v_strides, dout, dout_strides, lse, delta);
     a.dq = targ(dq, dq_strides);

@@ -227,10 +227,10 @@ def train(cfg: GPTConfig, batch=8, seq=1024, steps=20, seed=5, device="cuda", at
     def one_step():
         opt.zero_grad()
         logits = model(inputs)
-        loss = SoftmaxCrossEntropy.apply(logits, labels_t).mean()
-        loss.backward()
+        per_token = SoftmaxCrossEntropy.apply(logits, labels_t)
+        per_token.mean().backward()  # mean in the logits' dtype, as the reference does
         opt.step()
-        return loss.detach()
+        return per_token.detach().float().mean()  # logged in fp32 for resolution
 
     for _ in range(warmup):
         one_step()

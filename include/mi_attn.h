@@ -84,9 +84,25 @@ mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal,
                       void* stream);
 
 /*
- * The three stages of mi_attn_bwd as separate entry points, one per kernel of
- * the reference's backward; calling them in this order equals mi_attn_bwd.
- *
+ * mi_attn_bwd is mi_attn_bwd_preprocess followed by mi_attn_bwd_grads.  The
+ * latter produces dQ, dK and dV in one launch where the matrix-core path
+ * applies (dK/dV and dQ work interleaved in one grid) and otherwise runs
+ * mi_attn_bwd_dkdv then mi_attn_bwd_dq.  The four are exposed separately, one
+ * per kernel of the reference's backward, for callers that schedule them.
+ */
+mi_status mi_attn_bwd_grads(mi_dtype dtype, int B, int H, int S, int D, int causal,
+                            float scale,
+                            const void* q, const int64_t q_strides[4],
+                            const void* k, const int64_t k_strides[4],
+                            const void* v, const int64_t v_strides[4],
+                            const void* dout, const int64_t dout_strides[4],
+                            const float* lse, const float* delta,
+                            void* dq, const int64_t dq_strides[4],
+                            void* dk, const int64_t dk_strides[4],
+                            void* dv, const int64_t dv_strides[4],
+                            void* stream);
+
+/*
  * delta = rowsum(dO * O) (fp32).
  * Replaces the `_attn_bwd_precompute` launch, core/myFlashAttn.py:323-346.
  */
