@@ -258,7 +258,8 @@ def main():
         "roofline": roofline,
         "rope": {"bound": "hbm", "avg_us": round(rope_us, 3), "achieved": round(rope_gbps, 1),
                  "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                 "frac": round(rope_gbps / PEAK_HBM_GBPS, 4), "algorithmic_bytes": rope_bytes},
+                 "frac": round(rope_gbps / PEAK_HBM_GBPS, 4), "algorithmic_bytes": rope_bytes,
+                 "traffic": read_traffic("rope_qk")},
     }
     if not args.no_gpt:
         out["gpt_train"] = gpt_train(dev)
