@@ -23,6 +23,8 @@
 //   * causal: key tiles only visit query tiles at or after the diagonal, query
 //     tiles only key tiles at or before it; 32-row blocks entirely above the
 //     diagonal are skipped per wave, blocks that straddle it are masked.
+#include <type_traits>
+
 #include "mi_device.h"
 #include "mi_kernels.h"
 
@@ -131,16 +133,24 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
   u32x2 qreg[4], dreg[4];
   float lreg = 0.f, dlreg = 0.f;
 
+  // Buffer loads: one descriptor per tile, a fixed per-lane byte offset and
+  // the row step as a scalar offset, so no per-lane address arithmetic.
+  const uint32_t qoff = (uint32_t)((4 * rg * a.q.ss + 4 * cg) * 2);
+  const uint32_t doff = (uint32_t)((4 * rg * a.dout.ss + 4 * cg) * 2);
+  const uint32_t qrow_b = (uint32_t)(a.q.ss * 2), drow_b = (uint32_t)(a.dout.ss * 2);
   auto load_tile = [&](int q0) {
+    const auto rq = tile_rsrc(qp + (int64_t)q0 * a.q.ss);
+    const auto rd = tile_rsrc(dop + (int64_t)q0 * a.dout.ss);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int64_t row = q0 + 4 * rg + r;
-      qreg[r] = *(const u32x2*)(qp + row * a.q.ss + 4 * cg);
-      dreg[r] = *(const u32x2*)(dop + row * a.dout.ss + 4 * cg);
+      qreg[r] = __builtin_amdgcn_raw_buffer_load_b64(rq, qoff, r * qrow_b, 0);
+      dreg[r] = __builtin_amdgcn_raw_buffer_load_b64(rd, doff, r * drow_b, 0);
     }
     if (tid < C::BQ) {
-      lreg = lsep[q0 + tid] * kLog2e;
-      dlreg = delp[q0 + tid];
+      const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(lsep + q0), tid * 4, 0, 0);
+      const uint32_t dl = __builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(delp + q0), tid * 4, 0, 0);
+      lreg = __builtin_bit_cast(float, lo) * kLog2e;
+      dlreg = -__builtin_bit_cast(float, dl);  // dP accumulators start at -delta
     }
   };
   auto store_tile = [&](int buf) {
@@ -184,12 +194,18 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
   }
   __syncthreads();
 
-  for (int j = 0; j < nq; ++j) {
+  // Query tile j.  MASKED steps are the ones that straddle this workgroup's
+  // keys (causal only): there a 32-row block entirely before a wave's keys is
+  // skipped and the block on the wave's diagonal (qbs == kw, everything is
+  // 32-aligned) is masked with the fixed triangle key > query.  All later
+  // tiles see every key of the workgroup and run the branch-free body.
+  auto step = [&](int j, auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
     const int buf = j & 1;
     const int q0 = q_begin + j * C::BQ;
     if (j + 1 < nq) load_tile(q0 + C::BQ);
 
-    if (wave_valid && (!CAUSAL || q0 + C::BQ - 1 >= kw)) {
+    if (wave_valid && (!MASKED || q0 + C::BQ - 1 >= kw)) {
       const uint16_t* Qs = smem[buf];
       const uint16_t* dOs = Qs + C::BQ * C::RLD;
       const uint16_t* Qt = dOs + C::BQ * C::RLD;
@@ -199,9 +215,16 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
 #pragma unroll
       for (int qb = 0; qb < C::QB; ++qb) {
         const int qbs = q0 + 32 * qb;
-        live[qb] = !CAUSAL || (qbs + 31 >= kw);
+        live[qb] = !MASKED || (qbs + 31 >= kw);
         if (!live[qb]) continue;
-        f32x16 s = f32x16{}, dp = f32x16{};
+        // dP starts at -delta (row = query), so the MFMAs leave dP - delta.
+        f32x16 s = f32x16{}, dp;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          const f32x4 d4 = *(const f32x4*)(&sl[buf][C::BQ + 32 * qb + 8 * jj + 4 * g]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) dp[4 * jj + i] = d4[i];
+        }
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
           const u32x4 qa = *(const u32x4*)(&Qs[(32 * qb + l32) * C::RLD + 16 * ks + 8 * g]);
@@ -212,18 +235,17 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
           const u32x4 da = *(const u32x4*)(&dOs[(32 * qb + l32) * C::RLD + 16 * ks + 8 * g]);
           dp = E::mfma(da, vf[ks], dp);
         }
-        const bool diag = CAUSAL && (qbs < kw + 31);
+        const bool diag = MASKED && qbs == kw;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const f32x4 l4 = *(const f32x4*)(&sl[buf][32 * qb + 8 * jj + 4 * g]);
-          const f32x4 d4 = *(const f32x4*)(&sl[buf][C::BQ + 32 * qb + 8 * jj + 4 * g]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * jj + i;
             float p = fast_exp2(__builtin_fmaf(s[r], c, -l4[i]));
-            if (diag && krow > qbs + 8 * jj + 4 * g + i) p = 0.f;
+            if (MASKED && diag && l32 > 8 * jj + 4 * g + i) p = 0.f;
             s[r] = p;
-            dp[r] = p * (dp[r] - d4[i]);
+            dp[r] = p * dp[r];
           }
         }
 #pragma unroll
@@ -255,7 +277,13 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
 
     if (j + 1 < nq) store_tile(buf ^ 1);
     __syncthreads();
-  }
+  };
+
+  const int n_diag = CAUSAL ? min(nq, C::BKV / C::BQ) : 0;
+  int j = 0;
+  if constexpr (CAUSAL)
+    for (; j < n_diag; ++j) step(j, std::true_type{});
+  for (; j < nq; ++j) step(j, std::false_type{});
 
   if (!wave_valid) return;
   uint16_t* dkrow = (uint16_t*)a.dk.ptr + b * a.dk.sb + h * a.dk.sh + (int64_t)krow * a.dk.ss;
@@ -345,12 +373,16 @@ __device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const i
   const int cg = tid % C::CG;
   u32x2 kreg[4], vreg[4];
 
+  const uint32_t koff = (uint32_t)((4 * rg * a.k.ss + 4 * cg) * 2);
+  const uint32_t voff = (uint32_t)((4 * rg * a.v.ss + 4 * cg) * 2);
+  const uint32_t krow_b = (uint32_t)(a.k.ss * 2), vrow_b = (uint32_t)(a.v.ss * 2);
   auto load_tile = [&](int kv0) {
+    const auto rk = tile_rsrc(kp + (int64_t)kv0 * a.k.ss);
+    const auto rv = tile_rsrc(vp + (int64_t)kv0 * a.v.ss);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int64_t row = kv0 + 4 * rg + r;
-      kreg[r] = *(const u32x2*)(kp + row * a.k.ss + 4 * cg);
-      vreg[r] = *(const u32x2*)(vp + row * a.v.ss + 4 * cg);
+      kreg[r] = __builtin_amdgcn_raw_buffer_load_b64(rk, koff, r * krow_b, 0);
+      vreg[r] = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, r * vrow_b, 0);
     }
   };
   auto store_tile = [&](int buf) {
@@ -381,12 +413,17 @@ __device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const i
   store_tile(0);
   __syncthreads();
 
-  for (int j = 0; j < nkv; ++j) {
+  // Key tile j.  MASKED steps are the causal ones that straddle this
+  // workgroup's queries: a 32-key block after a wave's queries is skipped and
+  // the block on the wave's diagonal (kvb == qw) gets the fixed triangle mask.
+  // Earlier tiles are visible to every query and run the branch-free body.
+  auto step = [&](int j, auto masked_tag) {
+    constexpr bool MASKED = decltype(masked_tag)::value;
     const int buf = j & 1;
     const int kv0 = j * C::BKV;
     if (j + 1 < nkv) load_tile(kv0 + C::BKV);
 
-    if (wave_valid && (!CAUSAL || kv0 <= qw + 31)) {
+    if (wave_valid && (!MASKED || kv0 <= qw + 31)) {
       const uint16_t* Ks = smem[buf];
       const uint16_t* Vs = Ks + C::BKV * C::RLD;
       const uint16_t* Kt = Vs + C::BKV * C::RLD;
@@ -395,7 +432,7 @@ __device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const i
 #pragma unroll
       for (int kb = 0; kb < C::NKB; ++kb) {
         const int kvb = kv0 + 32 * kb;
-        live[kb] = !CAUSAL || (kvb <= qw + 31);
+        live[kb] = !MASKED || (kvb <= qw + 31);
         if (!live[kb]) continue;
         f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
@@ -408,11 +445,11 @@ __device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const i
           const u32x4 va = *(const u32x4*)(&Vs[(32 * kb + l32) * C::RLD + 16 * ks + 8 * g]);
           dp = E::mfma(va, df[ks], dp);
         }
-        const bool diag = CAUSAL && (kvb + 31 > qw);
+        const bool diag = MASKED && kvb == qw;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           float p = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
-          if (diag && kvb + 8 * (r >> 2) + 4 * g + (r & 3) > qrow) p = 0.f;
+          if (MASKED && diag && 8 * (r >> 2) + 4 * g + (r & 3) > l32) p = 0.f;
           dp[r] = p * (dp[r] - dl);
         }
 #pragma unroll
@@ -439,7 +476,13 @@ __device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const i
 
     if (j + 1 < nkv) store_tile(buf ^ 1);
     __syncthreads();
-  }
+  };
+
+  const int n_main = CAUSAL ? max(0, nkv - C::BQ / C::BKV) : nkv;
+  int j = 0;
+  for (; j < n_main; ++j) step(j, std::false_type{});
+  if constexpr (CAUSAL)
+    for (; j < nkv; ++j) step(j, std::true_type{});
 
   if (!wave_valid) return;
   uint16_t* dqrow = (uint16_t*)a.dq.ptr + b * a.dq.sb + h * a.dq.sh + (int64_t)qrow * a.dq.ss;

@@ -50,12 +50,15 @@ mi_status check_attn_tensor(const char* name, const void* p, const int64_t* st) 
   return MI_OK;
 }
 
-// 16-byte aligned base and strides that keep every row 16-byte aligned.
+// The matrix-core kernels' operand tensors: 16-byte aligned base and strides
+// that keep every row 16-byte aligned, and a row stride small enough that the
+// byte offset of any row inside a 256-row tile fits the 32-bit offsets of
+// their buffer loads.
 bool aligned16(const void* p, const int64_t* st, int esz) {
   if (((uintptr_t)p) % 16) return false;
   for (int i = 0; i < 3; ++i)
     if ((st[i] * esz) % 16) return false;
-  return true;
+  return st[2] * esz * 256 < (int64_t(1) << 31);
 }
 
 mi::TensorArg targ(const void* p, const int64_t* st) {
