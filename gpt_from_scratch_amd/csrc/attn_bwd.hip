@@ -14,12 +14,14 @@
 //     wave's K and V rows live in registers as B operands for the whole loop.
 //     S = Q K^T and dP = dO V^T are computed with keys along the lane index, so
 //     P and dS come out of the accumulators already in B-operand form for
-//     dV^T = dO^T P and dK^T = Q^T dS.  Q and dO tiles are staged in LDS both
-//     row-major (A operands of S and dP) and transposed (A operands of dV^T and
-//     dK^T), double-buffered, the transpose done once per tile with v_perm.
+//     dV^T = dO^T P and dK^T = Q^T dS.  Q and dO tiles are staged row-major in
+//     LDS (double-buffered): the A operands of S and dP are plain 16-byte
+//     reads, those of dV^T and dK^T come from the same tiles through the
+//     transposing LDS read (ds_read_b64_tr_b16).
 //   * dQ kernel: a workgroup owns 128 queries; Q and dO rows live in registers;
 //     S^T = K Q^T and dP^T = V dO^T put queries along the lane index so that
-//     lse and delta are per-lane scalars and dS^T feeds dQ^T = K^T dS^T directly.
+//     lse and delta are per-lane scalars and dS^T feeds dQ^T = K^T dS^T directly
+//     (K^T read transposed from the row-major K tile).
 //   * causal: key tiles only visit query tiles at or after the diagonal, query
 //     tiles only key tiles at or before it; 32-row blocks entirely above the
 //     diagonal are skipped per wave, blocks that straddle it are masked.
@@ -72,14 +74,13 @@ struct DkvCfg {
   static constexpr int BQ = (D == 64) ? 64 : 32;
   static constexpr int NT = 256;
   static constexpr int RLD = D + 8;   // row-major Q / dO tile stride (elements)
-  static constexpr int TLD = BQ + 4;  // transposed Q^T / dO^T tile stride
   static constexpr int KS = D / 16;
   static constexpr int DB = D / 32;
   static constexpr int QB = BQ / 32;
   static constexpr int CG = D / 4;    // loader column groups (4 columns each)
   static constexpr int RG = BQ / 4;   // loader row groups (4 rows each)
   static_assert(CG * RG == NT, "loader covers the tile with 4x4 blocks");
-  static constexpr int BUF = 2 * BQ * RLD + 2 * D * TLD;  // uint16 per buffer
+  static constexpr int BUF = 2 * BQ * RLD;  // uint16 per buffer: Q and dO tiles
 };
 
 // One key tile `kt` of head `bh`.  smem: 2 staging buffers; sl: lse*log2e and
@@ -111,6 +112,7 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
   const int kw = kv0 + 32 * wave;
   const bool wave_valid = kw < S;
   const int krow = kw + l32;
+  const int tro = tr_lane_offset(lane, C::RLD);
 
   u32x4 kf[C::KS], vf[C::KS];
 #pragma unroll
@@ -156,23 +158,10 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
   auto store_tile = [&](int buf) {
     uint16_t* Qs = smem[buf];
     uint16_t* dOs = Qs + C::BQ * C::RLD;
-    uint16_t* Qt = dOs + C::BQ * C::RLD;
-    uint16_t* dOt = Qt + D * C::TLD;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       *(u32x2*)(&Qs[(4 * rg + r) * C::RLD + 4 * cg]) = qreg[r];
       *(u32x2*)(&dOs[(4 * rg + r) * C::RLD + 4 * cg]) = dreg[r];
-    }
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      u32x2 c0, c1;
-      const int d = 4 * cg + 2 * w;
-      transpose4x2(qreg[0][w], qreg[1][w], qreg[2][w], qreg[3][w], c0, c1);
-      *(u32x2*)(&Qt[d * C::TLD + 4 * rg]) = c0;
-      *(u32x2*)(&Qt[(d + 1) * C::TLD + 4 * rg]) = c1;
-      transpose4x2(dreg[0][w], dreg[1][w], dreg[2][w], dreg[3][w], c0, c1);
-      *(u32x2*)(&dOt[d * C::TLD + 4 * rg]) = c0;
-      *(u32x2*)(&dOt[(d + 1) * C::TLD + 4 * rg]) = c1;
     }
     if (tid < C::BQ) {
       sl[buf][tid] = lreg;
@@ -208,8 +197,6 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
     if (wave_valid && (!MASKED || q0 + C::BQ - 1 >= kw)) {
       const uint16_t* Qs = smem[buf];
       const uint16_t* dOs = Qs + C::BQ * C::RLD;
-      const uint16_t* Qt = dOs + C::BQ * C::RLD;
-      const uint16_t* dOt = Qt + D * C::TLD;
       u32x4 pb[C::QB][2], sb[C::QB][2];
       bool live[C::QB];
 #pragma unroll
@@ -263,13 +250,10 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
           for (int db = 0; db < C::DB; ++db) {
-            const int off = (32 * db + l32) * C::TLD + 32 * qb + 16 * hh + 4 * g;
-            const u32x2 a0 = *(const u32x2*)(&dOt[off]);
-            const u32x2 a1 = *(const u32x2*)(&dOt[off + 8]);
-            dv[db] = E::mfma(u32x4{a0[0], a0[1], a1[0], a1[1]}, pb[qb][hh], dv[db]);
-            const u32x2 b0 = *(const u32x2*)(&Qt[off]);
-            const u32x2 b1 = *(const u32x2*)(&Qt[off + 8]);
-            dk[db] = E::mfma(u32x4{b0[0], b0[1], b1[0], b1[1]}, sb[qb][hh], dk[db]);
+            // dO^T and Q^T operands read transposed from the row-major tiles.
+            const int off = (32 * qb + 16 * hh) * C::RLD + 32 * db + tro;
+            dv[db] = E::mfma(tr_operand(&dOs[off], C::RLD), pb[qb][hh], dv[db]);
+            dk[db] = E::mfma(tr_operand(&Qs[off], C::RLD), sb[qb][hh], dk[db]);
           }
         }
       }
@@ -314,13 +298,12 @@ struct DqCfg {
   static constexpr int NKB = BKV / 32;
   static constexpr int NT = 256;
   static constexpr int RLD = D + 8;    // row-major K / V tile stride
-  static constexpr int TLD = BKV + 4;  // transposed K^T tile stride
   static constexpr int KS = D / 16;
   static constexpr int DB = D / 32;
   static constexpr int CG = D / 4;
   static constexpr int RG = BKV / 4;
   static_assert(CG * RG == NT, "loader covers the tile with 4x4 blocks");
-  static constexpr int BUF = 2 * BKV * RLD + D * TLD;
+  static constexpr int BUF = 2 * BKV * RLD;  // uint16 per buffer: K and V tiles
 };
 
 // One query tile `qt` of head `bh`.  smem: 2 staging buffers.
@@ -348,6 +331,7 @@ __device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const i
   const int qw = q0 + 32 * wave;
   const bool wave_valid = qw < S;
   const int qrow = qw + l32;
+  const int tro = tr_lane_offset(lane, C::RLD);
 
   u32x4 qf[C::KS], df[C::KS];
   float lse2 = 0.f, dl = 0.f;
@@ -388,19 +372,10 @@ __device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const i
   auto store_tile = [&](int buf) {
     uint16_t* Ks = smem[buf];
     uint16_t* Vs = Ks + C::BKV * C::RLD;
-    uint16_t* Kt = Vs + C::BKV * C::RLD;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       *(u32x2*)(&Ks[(4 * rg + r) * C::RLD + 4 * cg]) = kreg[r];
       *(u32x2*)(&Vs[(4 * rg + r) * C::RLD + 4 * cg]) = vreg[r];
-    }
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      u32x2 c0, c1;
-      const int d = 4 * cg + 2 * w;
-      transpose4x2(kreg[0][w], kreg[1][w], kreg[2][w], kreg[3][w], c0, c1);
-      *(u32x2*)(&Kt[d * C::TLD + 4 * rg]) = c0;
-      *(u32x2*)(&Kt[(d + 1) * C::TLD + 4 * rg]) = c1;
     }
   };
 
@@ -426,7 +401,6 @@ __device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const i
     if (wave_valid && (!MASKED || kv0 <= qw + 31)) {
       const uint16_t* Ks = smem[buf];
       const uint16_t* Vs = Ks + C::BKV * C::RLD;
-      const uint16_t* Kt = Vs + C::BKV * C::RLD;
       u32x4 sb[C::NKB][2];
       bool live[C::NKB];
 #pragma unroll
@@ -465,10 +439,9 @@ __device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const i
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
           for (int db = 0; db < C::DB; ++db) {
-            const int off = (32 * db + l32) * C::TLD + 32 * kb + 16 * hh + 4 * g;
-            const u32x2 a0 = *(const u32x2*)(&Kt[off]);
-            const u32x2 a1 = *(const u32x2*)(&Kt[off + 8]);
-            acc[db] = E::mfma(u32x4{a0[0], a0[1], a1[0], a1[1]}, sb[kb][hh], acc[db]);
+            // K^T operand read transposed from the row-major K tile.
+            const int off = (32 * kb + 16 * hh) * C::RLD + 32 * db + tro;
+            acc[db] = E::mfma(tr_operand(&Ks[off], C::RLD), sb[kb][hh], acc[db]);
           }
         }
       }

@@ -188,4 +188,39 @@ __device__ __forceinline__ void transpose4x2(uint32_t r0, uint32_t r1, uint32_t 
   c1[1] = __builtin_amdgcn_perm(r3, r2, 0x07060302u);
 }
 
+// ---------------------------------------------------------------------------
+// Transposed MFMA A operand straight from a row-major LDS tile.
+//
+// ds_read_b64_tr_b16 works on groups of 16 lanes: lane j of a group supplies
+// the address of 4 consecutive 16-bit elements (chunk j) and lane i receives
+// element i%4 of chunks i/4, 4 + i/4, 8 + i/4 and 12 + i/4.
+//
+// For a tile T[k][m] (row stride ld elements) the 32x32x16 A operand wants
+// lane l to hold column m = l%32 at eight k values.  With every lane pointing
+// at row tr_row(l) = 4*(l/32) + (l%16)/4 and column tr_col(l) = 16*((l/16)%2)
+// + 4*(l%4) of a 16-row window, one read gives lane l the column l%32 at rows
+// 4*(l/32) + {0,1,2,3}, and a second read 8 rows further down the rows
+// 8 + 4*(l/32) + {0,1,2,3}: the k-slot order of a B operand taken from a
+// 32x32 accumulator (registers 8h .. 8h+7 hold rows 16h + 4*(l/32) + {0..3}
+// and 16h + 8 + 4*(l/32) + {0..3}).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int tr_lane_offset(int lane, int ld) {
+  return (4 * (lane >> 5) + ((lane & 15) >> 2)) * ld + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+}
+
+__device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t* p) {
+  typedef __attribute__((ext_vector_type(4))) short s16x4;
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (s16x4 __attribute__((address_space(3)))*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// A operand for rows [m0, m0+32) of T^T and k rows [k0, k0+16) of T, where
+// `p` = tile + k0*ld + m0 + tr_lane_offset(lane, ld).
+__device__ __forceinline__ u32x4 tr_operand(const uint16_t* p, int ld) {
+  const u32x2 lo = ds_read_tr16(p);
+  const u32x2 hi = ds_read_tr16(p + 8 * ld);
+  return u32x4{lo[0], lo[1], hi[0], hi[1]};
+}
+
 }  // namespace mi
