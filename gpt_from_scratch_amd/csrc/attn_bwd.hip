@@ -66,108 +66,201 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(AttnArgs a, FastDiv div
 }
 
 // ---------------------------------------------------------------------------
-// dK / dV
+// Work items.  The gradients are produced by items of two kinds:
+//   kind 0 (dK/dV, `_attn_bwd_LoopQ`): OWN keys of one head; the item loops
+//          over query tiles, with K and V rows of its keys in registers;
+//   kind 1 (dQ, `_attn_bwd_LoopKV`):   OWN queries of one head; the item loops
+//          over key tiles, with Q and dO rows of its queries in registers.
+// Both stream TILE-row tiles of the other two tensors through LDS (double
+// buffered) and keep the same register layout: two resident row sets (B
+// operands) and one staged tile, so one launch can run both kinds.
 // ---------------------------------------------------------------------------
 template <int D>
-struct DkvCfg {
-  static constexpr int BKV = 128;
-  static constexpr int BQ = (D == 64) ? 64 : 32;
+struct BwdCfg {
+  static constexpr int OWN = 128;                   // rows owned by an item
+  static constexpr int TILE = (D == 64) ? 64 : 32;  // rows of a streamed tile
   static constexpr int NT = 256;
-  static constexpr int RLD = D + 8;   // row-major Q / dO tile stride (elements)
+  static constexpr int RLD = D + 8;  // row stride of the row-major LDS tiles (elements)
   static constexpr int KS = D / 16;
   static constexpr int DB = D / 32;
-  static constexpr int QB = BQ / 32;
-  static constexpr int CG = D / 4;    // loader column groups (4 columns each)
-  static constexpr int RG = BQ / 4;   // loader row groups (4 rows each)
+  static constexpr int TB = TILE / 32;  // 32-row blocks per streamed tile
+  static constexpr int CG = D / 4;      // loader column groups (4 columns each)
+  static constexpr int RG = TILE / 4;   // loader row groups (4 rows each)
   static_assert(CG * RG == NT, "loader covers the tile with 4x4 blocks");
-  static constexpr int BUF = 2 * BQ * RLD;  // uint16 per buffer: Q and dO tiles
+  static constexpr int BUF = 2 * TILE * RLD;  // uint16 per LDS buffer: both streamed tensors
+  // two buffers, then lse*log2e and -delta of each buffer's query rows (dK/dV kind)
+  static constexpr int LDS_BYTES = 2 * BUF * 2 + 2 * 2 * TILE * 4;
 };
 
-// One key tile `kt` of head `bh`.  smem: 2 staging buffers; sl: lse*log2e and
-// delta of the staged query tiles.
-template <typename E, int D, bool CAUSAL>
-__device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const int bh,
-                                          uint16_t (*smem)[DkvCfg<D>::BUF],
-                                          float (*sl)[2 * DkvCfg<D>::BQ]) {
-  using C = DkvCfg<D>;
+struct BwdItem {
+  int kind;  // 0: dK/dV, 1: dQ
+  int tile;  // key tile (kind 0) or query tile (kind 1), OWN rows each
+  int bh;
+};
 
+template <int D>
+struct Resident {
+  u32x4 r[2][D / 16];  // kind 0: K, V rows; kind 1: Q, dO rows (lane: row l%32, 8 columns)
+  float lse2, dl;      // kind 1: lse*log2e and delta of this lane's query row
+};
+
+struct Staged {
+  u32x2 t[2][4];  // one streamed tile: 4 rows x 4 columns of each tensor per thread
+  float s0, s1;   // kind 0: lse*log2e and -delta of query row `tid` (tid < TILE)
+};
+
+// Where an item's streamed tiles come from: head bases, strides and this
+// thread's fixed byte offset inside a tile (buffer loads, so that advancing
+// a tile is scalar arithmetic).
+struct StageSrc {
+  const uint16_t* p0;
+  const uint16_t* p1;
+  int64_t ss0, ss1;
+  uint32_t off0, off1;
+  const float* lse;
+  const float* delta;
+};
+
+__device__ __forceinline__ const uint16_t* head_ptr(const TensorArg& t, int b, int h) {
+  return (const uint16_t*)t.ptr + b * t.sb + h * t.sh;
+}
+
+template <int D, bool CAUSAL>
+__device__ __forceinline__ int first_row(const BwdItem& it) {
+  return (CAUSAL && it.kind == 0) ? it.tile * BwdCfg<D>::OWN : 0;
+}
+
+template <int D>
+__device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& it,
+                                              Resident<D>& res) {
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int b = it.bh / a.H;
+  const int h = it.bh % a.H;
+  const TensorArg& t0 = it.kind ? a.q : a.k;
+  const TensorArg& t1 = it.kind ? a.dout : a.v;
+  const int w0 = it.tile * BwdCfg<D>::OWN + 32 * wave;  // first row of this wave (SGPR)
+  if (w0 < a.S) {
+    // wave base in the descriptor, lane offset (row l%32, 8 columns) in one VGPR
+    const auto r0 = tile_rsrc(head_ptr(t0, b, h) + (int64_t)w0 * t0.ss);
+    const auto r1 = tile_rsrc(head_ptr(t1, b, h) + (int64_t)w0 * t1.ss);
+    const uint32_t o0 = (uint32_t)(((lane & 31) * t0.ss + 8 * (lane >> 5)) * 2);
+    const uint32_t o1 = (uint32_t)(((lane & 31) * t1.ss + 8 * (lane >> 5)) * 2);
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      res.r[0][ks] = __builtin_amdgcn_raw_buffer_load_b128(r0, o0 + 32 * ks, 0, 0);
+      res.r[1][ks] = __builtin_amdgcn_raw_buffer_load_b128(r1, o1 + 32 * ks, 0, 0);
+    }
+    if (it.kind) {
+      const int64_t o = (int64_t)it.bh * a.S + w0;
+      res.lse2 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                     tile_rsrc(a.lse + o), (lane & 31) * 4, 0, 0)) * kLog2e;
+      res.dl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                   tile_rsrc(a.delta + o), (lane & 31) * 4, 0, 0));
+    }
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < D / 16; ++ks) {
+      res.r[0][ks] = u32x4{0, 0, 0, 0};
+      res.r[1][ks] = u32x4{0, 0, 0, 0};
+    }
+    res.lse2 = 0.f;
+    res.dl = 0.f;
+  }
+}
+
+template <int D>
+__device__ __forceinline__ StageSrc stage_src(const AttnArgs& a, const BwdItem& it) {
+  using C = BwdCfg<D>;
   const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+  const int rg = tid / C::CG;
+  const int cg = tid % C::CG;
+  const int b = it.bh / a.H;
+  const int h = it.bh % a.H;
+  const TensorArg& t0 = it.kind ? a.k : a.q;
+  const TensorArg& t1 = it.kind ? a.v : a.dout;
+  StageSrc s;
+  s.p0 = head_ptr(t0, b, h);
+  s.p1 = head_ptr(t1, b, h);
+  s.ss0 = t0.ss;
+  s.ss1 = t1.ss;
+  s.off0 = (uint32_t)((4 * rg * t0.ss + 4 * cg) * 2);
+  s.off1 = (uint32_t)((4 * rg * t1.ss + 4 * cg) * 2);
+  s.lse = a.lse + (int64_t)it.bh * a.S;
+  s.delta = a.delta + (int64_t)it.bh * a.S;
+  return s;
+}
+
+// Streamed tile starting at row `row0` into registers.
+template <int D>
+__device__ __forceinline__ void load_stage(const StageSrc& s, int kind, int row0, Staged& st) {
+  const auto r0 = tile_rsrc(s.p0 + (int64_t)row0 * s.ss0);
+  const auto r1 = tile_rsrc(s.p1 + (int64_t)row0 * s.ss1);
+  const uint32_t rb0 = (uint32_t)(s.ss0 * 2), rb1 = (uint32_t)(s.ss1 * 2);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    st.t[0][r] = __builtin_amdgcn_raw_buffer_load_b64(r0, s.off0, r * rb0, 0);
+    st.t[1][r] = __builtin_amdgcn_raw_buffer_load_b64(r1, s.off1, r * rb1, 0);
+  }
+  const int tid = threadIdx.x;
+  if (kind == 0 && tid < BwdCfg<D>::TILE) {
+    const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(s.lse + row0), tid * 4, 0, 0);
+    const uint32_t dl = __builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(s.delta + row0), tid * 4, 0, 0);
+    st.s0 = __builtin_bit_cast(float, lo) * kLog2e;
+    st.s1 = -__builtin_bit_cast(float, dl);  // dP accumulators start at -delta
+  }
+}
+
+// Staged tile into one LDS buffer (row-major, both tensors) and, for the
+// dK/dV kind, its query rows' lse and -delta.
+template <int D>
+__device__ __forceinline__ void store_stage(const Staged& st, int kind, uint16_t* buf, float* slb) {
+  using C = BwdCfg<D>;
+  const int tid = threadIdx.x;
+  const int rg = tid / C::CG;
+  const int cg = tid % C::CG;
+  uint16_t* t1 = buf + C::TILE * C::RLD;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    *(u32x2*)(&buf[(4 * rg + r) * C::RLD + 4 * cg]) = st.t[0][r];
+    *(u32x2*)(&t1[(4 * rg + r) * C::RLD + 4 * cg]) = st.t[1][r];
+  }
+  if (kind == 0 && tid < C::TILE) {
+    slb[tid] = st.s0;
+    slb[C::TILE + tid] = st.s1;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK / dV item.  Wave w owns keys [kv0 + 32w, +32).  S = Q K^T and
+// dP = dO V^T are computed with keys along the lane index, so P and dS leave
+// the accumulators in B-operand form for dV^T = dO^T P and dK^T = Q^T dS; the
+// dO^T and Q^T A operands are read transposed from the row-major tiles.
+// `stg` holds the item's first query tile on entry.
+// ---------------------------------------------------------------------------
+template <typename E, int D, bool CAUSAL>
+__device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
+                                          const Resident<D>& res, Staged& stg,
+                                          uint16_t (*smem)[BwdCfg<D>::BUF],
+                                          float (*sl)[2 * BwdCfg<D>::TILE]) {
+  using C = BwdCfg<D>;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
   const int g = lane >> 5;
-
-  const int b = bh / a.H;
-  const int h = bh % a.H;
   const int S = a.S;
 
-  const uint16_t* qp = (const uint16_t*)a.q.ptr + b * a.q.sb + h * a.q.sh;
-  const uint16_t* kp = (const uint16_t*)a.k.ptr + b * a.k.sb + h * a.k.sh;
-  const uint16_t* vp = (const uint16_t*)a.v.ptr + b * a.v.sb + h * a.v.sh;
-  const uint16_t* dop = (const uint16_t*)a.dout.ptr + b * a.dout.sb + h * a.dout.sh;
-  const float* lsep = a.lse + (int64_t)bh * S;
-  const float* delp = a.delta + (int64_t)bh * S;
-
-  const int kv0 = kt * C::BKV;
+  const int kv0 = it.tile * C::OWN;
   const int kw = kv0 + 32 * wave;
   const bool wave_valid = kw < S;
   const int krow = kw + l32;
   const int tro = tr_lane_offset(lane, C::RLD);
+  const u32x4(&kf)[C::KS] = res.r[0];
+  const u32x4(&vf)[C::KS] = res.r[1];
 
-  u32x4 kf[C::KS], vf[C::KS];
-#pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) {
-    if (wave_valid) {
-      kf[ks] = *(const u32x4*)(kp + (int64_t)krow * a.k.ss + 16 * ks + 8 * g);
-      vf[ks] = *(const u32x4*)(vp + (int64_t)krow * a.v.ss + 16 * ks + 8 * g);
-    } else {
-      kf[ks] = u32x4{0, 0, 0, 0};
-      vf[ks] = u32x4{0, 0, 0, 0};
-    }
-  }
-
-  const int q_begin = CAUSAL ? kv0 : 0;
-  const int nq = (S - q_begin) / C::BQ;
-
-  // staging registers
-  const int rg = tid / C::CG;
-  const int cg = tid % C::CG;
-  u32x2 qreg[4], dreg[4];
-  float lreg = 0.f, dlreg = 0.f;
-
-  // Buffer loads: one descriptor per tile, a fixed per-lane byte offset and
-  // the row step as a scalar offset, so no per-lane address arithmetic.
-  const uint32_t qoff = (uint32_t)((4 * rg * a.q.ss + 4 * cg) * 2);
-  const uint32_t doff = (uint32_t)((4 * rg * a.dout.ss + 4 * cg) * 2);
-  const uint32_t qrow_b = (uint32_t)(a.q.ss * 2), drow_b = (uint32_t)(a.dout.ss * 2);
-  auto load_tile = [&](int q0) {
-    const auto rq = tile_rsrc(qp + (int64_t)q0 * a.q.ss);
-    const auto rd = tile_rsrc(dop + (int64_t)q0 * a.dout.ss);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      qreg[r] = __builtin_amdgcn_raw_buffer_load_b64(rq, qoff, r * qrow_b, 0);
-      dreg[r] = __builtin_amdgcn_raw_buffer_load_b64(rd, doff, r * drow_b, 0);
-    }
-    if (tid < C::BQ) {
-      const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(lsep + q0), tid * 4, 0, 0);
-      const uint32_t dl = __builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(delp + q0), tid * 4, 0, 0);
-      lreg = __builtin_bit_cast(float, lo) * kLog2e;
-      dlreg = -__builtin_bit_cast(float, dl);  // dP accumulators start at -delta
-    }
-  };
-  auto store_tile = [&](int buf) {
-    uint16_t* Qs = smem[buf];
-    uint16_t* dOs = Qs + C::BQ * C::RLD;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      *(u32x2*)(&Qs[(4 * rg + r) * C::RLD + 4 * cg]) = qreg[r];
-      *(u32x2*)(&dOs[(4 * rg + r) * C::RLD + 4 * cg]) = dreg[r];
-    }
-    if (tid < C::BQ) {
-      sl[buf][tid] = lreg;
-      sl[buf][C::BQ + tid] = dlreg;
-    }
-  };
+  const int q_begin = first_row<D, CAUSAL>(it);
+  const int nq = (S - q_begin) / C::TILE;
+  const StageSrc src = stage_src<D>(a, it);
 
   f32x16 dk[C::DB], dv[C::DB];
 #pragma unroll
@@ -177,30 +270,29 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
   }
   const float c = a.scale_log2;
 
-  if (nq > 0) {
-    load_tile(q_begin);
-    store_tile(0);
-  }
+  store_stage<D>(stg, 0, smem[0], sl[0]);
   __syncthreads();
 
-  // Query tile j.  MASKED steps are the ones that straddle this workgroup's
-  // keys (causal only): there a 32-row block entirely before a wave's keys is
+  // Query tile j.  MASKED steps are the ones that straddle this item's keys
+  // (causal only): there a 32-row block entirely before a wave's keys is
   // skipped and the block on the wave's diagonal (qbs == kw, everything is
   // 32-aligned) is masked with the fixed triangle key > query.  All later
-  // tiles see every key of the workgroup and run the branch-free body.
-  auto step = [&](int j, auto masked_tag) {
+  // tiles see every key of the item and run the branch-free body.
+  auto step = [&](int j, auto masked_tag, auto last_tag) {
     constexpr bool MASKED = decltype(masked_tag)::value;
+    constexpr bool LAST = decltype(last_tag)::value;
     const int buf = j & 1;
-    const int q0 = q_begin + j * C::BQ;
-    if (j + 1 < nq) load_tile(q0 + C::BQ);
+    const int q0 = q_begin + j * C::TILE;
+    if (!LAST) load_stage<D>(src, 0, q0 + C::TILE, stg);
 
-    if (wave_valid && (!MASKED || q0 + C::BQ - 1 >= kw)) {
-      const uint16_t* Qs = smem[buf];
-      const uint16_t* dOs = Qs + C::BQ * C::RLD;
-      u32x4 pb[C::QB][2], sb[C::QB][2];
-      bool live[C::QB];
+    const bool active = wave_valid && (!MASKED || q0 + C::TILE - 1 >= kw);
+    const uint16_t* Qs = smem[buf];
+    const uint16_t* dOs = Qs + C::TILE * C::RLD;
+    u32x4 pb[C::TB][2], sb[C::TB][2];
+    bool live[C::TB];
+    if (active) {
 #pragma unroll
-      for (int qb = 0; qb < C::QB; ++qb) {
+      for (int qb = 0; qb < C::TB; ++qb) {
         const int qbs = q0 + 32 * qb;
         live[qb] = !MASKED || (qbs + 31 >= kw);
         if (!live[qb]) continue;
@@ -208,7 +300,7 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
         f32x16 s = f32x16{}, dp;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const f32x4 d4 = *(const f32x4*)(&sl[buf][C::BQ + 32 * qb + 8 * jj + 4 * g]);
+          const f32x4 d4 = *(const f32x4*)(&sl[buf][C::TILE + 32 * qb + 8 * jj + 4 * g]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) dp[4 * jj + i] = d4[i];
         }
@@ -243,14 +335,15 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
             sb[qb][hh][w] = E::pack2(dp[8 * hh + 2 * w], dp[8 * hh + 2 * w + 1]);
           }
       }
+    }
+    if (active) {
 #pragma unroll
-      for (int qb = 0; qb < C::QB; ++qb) {
+      for (int qb = 0; qb < C::TB; ++qb) {
         if (!live[qb]) continue;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
           for (int db = 0; db < C::DB; ++db) {
-            // dO^T and Q^T operands read transposed from the row-major tiles.
             const int off = (32 * qb + 16 * hh) * C::RLD + 32 * db + tro;
             dv[db] = E::mfma(tr_operand(&dOs[off], C::RLD), pb[qb][hh], dv[db]);
             dk[db] = E::mfma(tr_operand(&Qs[off], C::RLD), sb[qb][hh], dk[db]);
@@ -259,17 +352,24 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
       }
     }
 
-    if (j + 1 < nq) store_tile(buf ^ 1);
+    if (!LAST) store_stage<D>(stg, 0, smem[buf ^ 1], sl[buf ^ 1]);
     __syncthreads();
   };
 
-  const int n_diag = CAUSAL ? min(nq, C::BKV / C::BQ) : 0;
+  // nq >= 1: the matrix-core path needs S % 64 == 0.
+  const int n_diag = CAUSAL ? min(nq, C::OWN / C::TILE) : 0;
   int j = 0;
   if constexpr (CAUSAL)
-    for (; j < n_diag; ++j) step(j, std::true_type{});
-  for (; j < nq; ++j) step(j, std::false_type{});
+    for (; j < n_diag && j + 1 < nq; ++j) step(j, std::true_type{}, std::false_type{});
+  for (; j + 1 < nq; ++j) step(j, std::false_type{}, std::false_type{});
+  if (CAUSAL && j < n_diag)
+    step(j, std::true_type{}, std::true_type{});
+  else
+    step(j, std::false_type{}, std::true_type{});
 
   if (!wave_valid) return;
+  const int b = it.bh / a.H;
+  const int h = it.bh % a.H;
   uint16_t* dkrow = (uint16_t*)a.dk.ptr + b * a.dk.sb + h * a.dk.sh + (int64_t)krow * a.dk.ss;
   uint16_t* dvrow = (uint16_t*)a.dv.ptr + b * a.dv.sb + h * a.dv.sh + (int64_t)krow * a.dv.ss;
   const float sc = a.scale;
@@ -289,122 +389,63 @@ __device__ __forceinline__ void dkdv_body(const AttnArgs& a, const int kt, const
 }
 
 // ---------------------------------------------------------------------------
-// dQ
+// dQ item.  Wave w owns queries [q0 + 32w, +32).  S^T = K Q^T and
+// dP^T = V dO^T put queries along the lane index, so lse and delta are
+// per-lane scalars and dS^T feeds dQ^T = K^T dS^T directly (K^T read
+// transposed from the row-major K tile).
 // ---------------------------------------------------------------------------
-template <int D>
-struct DqCfg {
-  static constexpr int BQ = 128;
-  static constexpr int BKV = (D == 64) ? 64 : 32;
-  static constexpr int NKB = BKV / 32;
-  static constexpr int NT = 256;
-  static constexpr int RLD = D + 8;    // row-major K / V tile stride
-  static constexpr int KS = D / 16;
-  static constexpr int DB = D / 32;
-  static constexpr int CG = D / 4;
-  static constexpr int RG = BKV / 4;
-  static_assert(CG * RG == NT, "loader covers the tile with 4x4 blocks");
-  static constexpr int BUF = 2 * BKV * RLD;  // uint16 per buffer: K and V tiles
-};
-
-// One query tile `qt` of head `bh`.  smem: 2 staging buffers.
 template <typename E, int D, bool CAUSAL>
-__device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const int bh,
-                                        uint16_t (*smem)[DqCfg<D>::BUF]) {
-  using C = DqCfg<D>;
-
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (SGPR)
+__device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
+                                        const Resident<D>& res, Staged& stg,
+                                        uint16_t (*smem)[BwdCfg<D>::BUF]) {
+  using C = BwdCfg<D>;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
   const int g = lane >> 5;
-
-  const int b = bh / a.H;
-  const int h = bh % a.H;
   const int S = a.S;
 
-  const uint16_t* qp = (const uint16_t*)a.q.ptr + b * a.q.sb + h * a.q.sh;
-  const uint16_t* kp = (const uint16_t*)a.k.ptr + b * a.k.sb + h * a.k.sh;
-  const uint16_t* vp = (const uint16_t*)a.v.ptr + b * a.v.sb + h * a.v.sh;
-  const uint16_t* dop = (const uint16_t*)a.dout.ptr + b * a.dout.sb + h * a.dout.sh;
-
-  const int q0 = qt * C::BQ;
+  const int q0 = it.tile * C::OWN;
   const int qw = q0 + 32 * wave;
   const bool wave_valid = qw < S;
   const int qrow = qw + l32;
   const int tro = tr_lane_offset(lane, C::RLD);
+  const u32x4(&qf)[C::KS] = res.r[0];
+  const u32x4(&df)[C::KS] = res.r[1];
+  const float lse2 = res.lse2;
+  const float dl = res.dl;
 
-  u32x4 qf[C::KS], df[C::KS];
-  float lse2 = 0.f, dl = 0.f;
-#pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) {
-    if (wave_valid) {
-      qf[ks] = *(const u32x4*)(qp + (int64_t)qrow * a.q.ss + 16 * ks + 8 * g);
-      df[ks] = *(const u32x4*)(dop + (int64_t)qrow * a.dout.ss + 16 * ks + 8 * g);
-    } else {
-      qf[ks] = u32x4{0, 0, 0, 0};
-      df[ks] = u32x4{0, 0, 0, 0};
-    }
-  }
-  if (wave_valid) {
-    lse2 = a.lse[(int64_t)bh * S + qrow] * kLog2e;
-    dl = a.delta[(int64_t)bh * S + qrow];
-  }
-
-  const int kv_end = CAUSAL ? min(q0 + C::BQ, S) : S;
-  const int nkv = kv_end / C::BKV;
-
-  const int rg = tid / C::CG;
-  const int cg = tid % C::CG;
-  u32x2 kreg[4], vreg[4];
-
-  const uint32_t koff = (uint32_t)((4 * rg * a.k.ss + 4 * cg) * 2);
-  const uint32_t voff = (uint32_t)((4 * rg * a.v.ss + 4 * cg) * 2);
-  const uint32_t krow_b = (uint32_t)(a.k.ss * 2), vrow_b = (uint32_t)(a.v.ss * 2);
-  auto load_tile = [&](int kv0) {
-    const auto rk = tile_rsrc(kp + (int64_t)kv0 * a.k.ss);
-    const auto rv = tile_rsrc(vp + (int64_t)kv0 * a.v.ss);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      kreg[r] = __builtin_amdgcn_raw_buffer_load_b64(rk, koff, r * krow_b, 0);
-      vreg[r] = __builtin_amdgcn_raw_buffer_load_b64(rv, voff, r * vrow_b, 0);
-    }
-  };
-  auto store_tile = [&](int buf) {
-    uint16_t* Ks = smem[buf];
-    uint16_t* Vs = Ks + C::BKV * C::RLD;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      *(u32x2*)(&Ks[(4 * rg + r) * C::RLD + 4 * cg]) = kreg[r];
-      *(u32x2*)(&Vs[(4 * rg + r) * C::RLD + 4 * cg]) = vreg[r];
-    }
-  };
+  const int kv_end = CAUSAL ? min(q0 + C::OWN, S) : S;
+  const int nkv = kv_end / C::TILE;
+  const StageSrc src = stage_src<D>(a, it);
 
   f32x16 acc[C::DB];
 #pragma unroll
   for (int i = 0; i < C::DB; ++i) acc[i] = f32x16{};
   const float c = a.scale_log2;
 
-  load_tile(0);
-  store_tile(0);
+  store_stage<D>(stg, 1, smem[0], nullptr);
   __syncthreads();
 
-  // Key tile j.  MASKED steps are the causal ones that straddle this
-  // workgroup's queries: a 32-key block after a wave's queries is skipped and
-  // the block on the wave's diagonal (kvb == qw) gets the fixed triangle mask.
-  // Earlier tiles are visible to every query and run the branch-free body.
-  auto step = [&](int j, auto masked_tag) {
+  // Key tile j.  MASKED steps are the causal ones that straddle this item's
+  // queries: a 32-key block after a wave's queries is skipped and the block on
+  // the wave's diagonal (kvb == qw) gets the fixed triangle mask.  Earlier
+  // tiles are visible to every query and run the branch-free body.
+  auto step = [&](int j, auto masked_tag, auto last_tag) {
     constexpr bool MASKED = decltype(masked_tag)::value;
+    constexpr bool LAST = decltype(last_tag)::value;
     const int buf = j & 1;
-    const int kv0 = j * C::BKV;
-    if (j + 1 < nkv) load_tile(kv0 + C::BKV);
+    const int kv0 = j * C::TILE;
+    if (!LAST) load_stage<D>(src, 1, kv0 + C::TILE, stg);
 
-    if (wave_valid && (!MASKED || kv0 <= qw + 31)) {
-      const uint16_t* Ks = smem[buf];
-      const uint16_t* Vs = Ks + C::BKV * C::RLD;
-      u32x4 sb[C::NKB][2];
-      bool live[C::NKB];
+    const bool active = wave_valid && (!MASKED || kv0 <= qw + 31);
+    const uint16_t* Ks = smem[buf];
+    const uint16_t* Vs = Ks + C::TILE * C::RLD;
+    u32x4 sb[C::TB][2];
+    bool live[C::TB];
+    if (active) {
 #pragma unroll
-      for (int kb = 0; kb < C::NKB; ++kb) {
+      for (int kb = 0; kb < C::TB; ++kb) {
         const int kvb = kv0 + 32 * kb;
         live[kb] = !MASKED || (kvb <= qw + 31);
         if (!live[kb]) continue;
@@ -432,14 +473,15 @@ __device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const i
           for (int w = 0; w < 4; ++w)
             sb[kb][hh][w] = E::pack2(dp[8 * hh + 2 * w], dp[8 * hh + 2 * w + 1]);
       }
+    }
+    if (active) {
 #pragma unroll
-      for (int kb = 0; kb < C::NKB; ++kb) {
+      for (int kb = 0; kb < C::TB; ++kb) {
         if (!live[kb]) continue;
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
           for (int db = 0; db < C::DB; ++db) {
-            // K^T operand read transposed from the row-major K tile.
             const int off = (32 * kb + 16 * hh) * C::RLD + 32 * db + tro;
             acc[db] = E::mfma(tr_operand(&Ks[off], C::RLD), sb[kb][hh], acc[db]);
           }
@@ -447,17 +489,24 @@ __device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const i
       }
     }
 
-    if (j + 1 < nkv) store_tile(buf ^ 1);
+    if (!LAST) store_stage<D>(stg, 1, smem[buf ^ 1], nullptr);
     __syncthreads();
   };
 
-  const int n_main = CAUSAL ? max(0, nkv - C::BQ / C::BKV) : nkv;
+  // nkv >= 1: the matrix-core path needs S % 64 == 0.
+  const int n_main = CAUSAL ? max(0, nkv - C::OWN / C::TILE) : nkv;
   int j = 0;
-  for (; j < n_main; ++j) step(j, std::false_type{});
+  for (; j < n_main && j + 1 < nkv; ++j) step(j, std::false_type{}, std::false_type{});
   if constexpr (CAUSAL)
-    for (; j < nkv; ++j) step(j, std::true_type{});
+    for (; j + 1 < nkv; ++j) step(j, std::true_type{}, std::false_type{});
+  if (!CAUSAL || j < n_main)
+    step(j, std::false_type{}, std::true_type{});
+  else
+    step(j, std::true_type{}, std::true_type{});
 
   if (!wave_valid) return;
+  const int b = it.bh / a.H;
+  const int h = it.bh % a.H;
   uint16_t* dqrow = (uint16_t*)a.dq.ptr + b * a.dq.sb + h * a.dq.sh + (int64_t)qrow * a.dq.ss;
   const float sc = a.scale;
 #pragma unroll
@@ -472,52 +521,55 @@ __device__ __forceinline__ void dq_body(const AttnArgs& a, const int qt, const i
   }
 }
 
+// One item per workgroup.
+template <typename E, int D, bool CAUSAL>
+__device__ __forceinline__ void run_item(const AttnArgs& a, const BwdItem it) {
+  using C = BwdCfg<D>;
+  __shared__ __attribute__((aligned(16))) unsigned char lds[C::LDS_BYTES];
+  auto smem = (uint16_t(*)[C::BUF])lds;
+  auto sl = (float(*)[2 * C::TILE])(lds + 2 * C::BUF * 2);
+  Resident<D> res;
+  Staged stg;
+  load_resident<D>(a, it, res);
+  load_stage<D>(stage_src<D>(a, it), it.kind, first_row<D, CAUSAL>(it), stg);
+  if (it.kind)
+    dq_item<E, D, CAUSAL>(a, it, res, stg, smem);
+  else
+    dkdv_item<E, D, CAUSAL>(a, it, res, stg, smem, sl);
+}
+
 template <typename E, int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2][DkvCfg<D>::BUF];
-  __shared__ __attribute__((aligned(16))) float sl[2][2 * DkvCfg<D>::BQ];
-  const int BH = a.B * a.H;
   // key tile 0 sees the most query tiles: dispatched first
-  dkdv_body<E, D, CAUSAL>(a, blockIdx.x / BH, blockIdx.x % BH, smem, sl);
+  const int BH = a.B * a.H;
+  run_item<E, D, CAUSAL>(a, BwdItem{0, (int)(blockIdx.x / BH), (int)(blockIdx.x % BH)});
 }
 
 template <typename E, int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a, int n_qtiles) {
-  __shared__ __attribute__((aligned(16))) uint16_t smem[2][DqCfg<D>::BUF];
   const int BH = a.B * a.H;
-  dq_body<E, D, CAUSAL>(a, n_qtiles - 1 - (int)(blockIdx.x / BH), blockIdx.x % BH, smem);
+  run_item<E, D, CAUSAL>(
+      a, BwdItem{1, n_qtiles - 1 - (int)(blockIdx.x / BH), (int)(blockIdx.x % BH)});
 }
 
-// dK/dV and dQ in one launch.  The two workgroup kinds alternate in dispatch
-// order, each heaviest-first (key tile 0 and the last query tile see the most
-// tiles under causal masking), so the short tails of both kinds overlap the
-// long heads of the other and the launch keeps the whole chip busy.  They
-// share one LDS allocation.
-template <int D>
-struct BwdLds {
-  static constexpr int DKV = 2 * DkvCfg<D>::BUF * 2 + 2 * 2 * DkvCfg<D>::BQ * 4;
-  static constexpr int DQ = 2 * DqCfg<D>::BUF * 2;
-  static constexpr int BYTES = DKV > DQ ? DKV : DQ;
-};
-
+// dK/dV and dQ in one launch.  Workgroups are ordered heaviest-first with the
+// two kinds alternating (rank r: kind r & 1; key tile r/2, or query tile
+// n_tiles-1-r/2, the tiles that see the most of the sequence under causal
+// masking), so the short tails of both kinds overlap the long heads of the
+// other and the launch keeps the whole chip busy.
 template <typename E, int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs a, int n_tiles) {
-  __shared__ __attribute__((aligned(16))) unsigned char lds[BwdLds<D>::BYTES];
   const int BH = a.B * a.H;
   const int rank = blockIdx.x / BH;
-  const int bh = blockIdx.x % BH;
-  if (rank & 1) {
-    dq_body<E, D, CAUSAL>(a, n_tiles - 1 - (rank >> 1), bh, (uint16_t(*)[DqCfg<D>::BUF])lds);
-  } else {
-    dkdv_body<E, D, CAUSAL>(a, rank >> 1, bh, (uint16_t(*)[DkvCfg<D>::BUF])lds,
-                            (float(*)[2 * DkvCfg<D>::BQ])(lds + 2 * DkvCfg<D>::BUF * 2));
-  }
+  const int kind = rank & 1;
+  run_item<E, D, CAUSAL>(
+      a, BwdItem{kind, kind ? n_tiles - 1 - (rank >> 1) : (rank >> 1), (int)(blockIdx.x % BH)});
 }
 
 template <typename E, int D>
 hipError_t launch_dkdv_d(const AttnArgs& a, hipStream_t st) {
   const int BH = a.B * a.H;
-  const int nkt = (a.S + DkvCfg<D>::BKV - 1) / DkvCfg<D>::BKV;
+  const int nkt = (a.S + BwdCfg<D>::OWN - 1) / BwdCfg<D>::OWN;
   if (a.causal)
     hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, true>), dim3(nkt * BH), dim3(256), 0, st, a);
   else
@@ -528,7 +580,7 @@ hipError_t launch_dkdv_d(const AttnArgs& a, hipStream_t st) {
 template <typename E, int D>
 hipError_t launch_dq_d(const AttnArgs& a, hipStream_t st) {
   const int BH = a.B * a.H;
-  const int nqt = (a.S + DqCfg<D>::BQ - 1) / DqCfg<D>::BQ;
+  const int nqt = (a.S + BwdCfg<D>::OWN - 1) / BwdCfg<D>::OWN;
   if (a.causal)
     hipLaunchKernelGGL((attn_bwd_dq_kernel<E, D, true>), dim3(nqt * BH), dim3(256), 0, st, a, nqt);
   else
@@ -536,16 +588,17 @@ hipError_t launch_dq_d(const AttnArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <typename E, int D, bool CAUSAL>
+hipError_t launch_both_dc(const AttnArgs& a, hipStream_t st) {
+  const int BH = a.B * a.H;
+  const int n = (a.S + BwdCfg<D>::OWN - 1) / BwdCfg<D>::OWN;
+  hipLaunchKernelGGL((attn_bwd_kernel<E, D, CAUSAL>), dim3(2 * n * BH), dim3(256), 0, st, a, n);
+  return hipGetLastError();
+}
+
 template <typename E, int D>
 hipError_t launch_both_d(const AttnArgs& a, hipStream_t st) {
-  static_assert(DkvCfg<D>::BKV == DqCfg<D>::BQ, "both kinds tile the sequence alike");
-  const int BH = a.B * a.H;
-  const int n = (a.S + DqCfg<D>::BQ - 1) / DqCfg<D>::BQ;
-  if (a.causal)
-    hipLaunchKernelGGL((attn_bwd_kernel<E, D, true>), dim3(2 * n * BH), dim3(256), 0, st, a, n);
-  else
-    hipLaunchKernelGGL((attn_bwd_kernel<E, D, false>), dim3(2 * n * BH), dim3(256), 0, st, a, n);
-  return hipGetLastError();
+  return a.causal ? launch_both_dc<E, D, true>(a, st) : launch_both_dc<E, D, false>(a, st);
 }
 
 template <typename E>
