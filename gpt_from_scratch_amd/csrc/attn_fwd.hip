@@ -14,9 +14,10 @@
 //     statistics are per-lane scalars (one v_permlane32_swap for the max) and
 //     the probabilities feed the P V product as a B operand without any
 //     register shuffle;
-//   * K/V tiles of BKV = 64 keys are staged through LDS; V is transposed once
-//     per tile while it is written (4x4 blocks through v_perm), so every MFMA
-//     operand read from LDS is a contiguous 8- or 16-byte access;
+//   * K/V tiles of BKV = 64 keys are staged row-major through LDS; the K
+//     operand is a contiguous 16-byte read, the V^T operand of P V comes from
+//     the same row-major V tile through the transposing LDS read
+//     (ds_read_b64_tr_b16);
 //   * software pipeline: while the VALU runs the softmax of tile j, the matrix
 //     cores already compute S for tile j+1, then P V for tile j.  K is staged
 //     two tiles ahead and V one tile ahead (double buffers for each), so one
@@ -46,14 +47,10 @@ struct FwdCfg {
   static constexpr int BQ = 128;
   static constexpr int BKV = 64;
   static constexpr int NT = 256;                   // 4 waves x 32 query rows
-  static constexpr int KLD = D + 8;                // K tile row stride in LDS (elements)
-  static constexpr int VLD = BKV + 4;              // V^T tile row stride in LDS
-  static constexpr int KS = D / 16;                // MFMA k-steps of K Q^T
-  static constexpr int DB = D / 32;                // 32-row blocks of O^T
-  static constexpr int KCH = BKV * D / 8 / NT;     // 16-byte K chunks per thread
-  static constexpr int VCPT = BKV * D / (NT * 4);  // V columns per thread (4 rows each)
-  static constexpr int VCG = D / VCPT;             // V column groups
-  static_assert(VCPT == 4 || VCPT == 8, "V staging uses 8- or 16-byte rows");
+  static constexpr int KLD = D + 8;             // K / V tile row stride in LDS (elements)
+  static constexpr int KS = D / 16;             // MFMA k-steps of K Q^T
+  static constexpr int DB = D / 32;             // 32-row blocks of O^T
+  static constexpr int KCH = BKV * D / 8 / NT;  // 16-byte chunks per thread of a K or V tile
 };
 
 constexpr float kRescaleSlack = 8.f;  // log2 units: probabilities stay <= 2^8
@@ -62,7 +59,7 @@ template <typename E, int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qtiles) {
   using C = FwdCfg<D>;
   __shared__ __attribute__((aligned(16))) uint16_t Ks[2][C::BKV * C::KLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Vt[2][D * C::VLD];
+  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][C::BKV * C::KLD];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -87,6 +84,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
   const int qw = q0 + 32 * wave;       // first query row of this wave (SGPR)
   const bool wave_valid = qw < S;      // S % 64 == 0: 32-row blocks are all-or-nothing
   const int qrow = qw + l32;
+  const int tro = tr_lane_offset(lane, C::KLD);
 
   u32x4 qf[C::KS];
 #pragma unroll
@@ -99,52 +97,33 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
 
   // ---- staging (global -> registers -> LDS) ----
   // Buffer loads: one descriptor per tile, rebased with scalar arithmetic; the
-  // per-lane byte offsets inside a tile are fixed.
-  u32x4 kreg[C::KCH];
-  typedef __attribute__((ext_vector_type(C::VCPT / 2))) uint32_t vrow_t;
-  vrow_t vreg[4];
-  const int v_rg = tid / C::VCG;
-  const int v_cg = tid % C::VCG;
-  uint32_t koff[C::KCH], voff[4];
+  // per-lane byte offsets inside a tile are fixed.  K and V use the same
+  // 16-byte chunk layout.
+  u32x4 kreg[C::KCH], vreg[C::KCH];
+  uint32_t koff[C::KCH], voff[C::KCH];
+  int soff[C::KCH];  // LDS element offset of each chunk
 #pragma unroll
   for (int i = 0; i < C::KCH; ++i) {
     const int ci = tid + C::NT * i;
-    koff[i] = (uint32_t)(((ci / (D / 8)) * a.k.ss + (ci % (D / 8)) * 8) * 2);
+    const int row = ci / (D / 8), col = (ci % (D / 8)) * 8;
+    koff[i] = (uint32_t)((row * a.k.ss + col) * 2);
+    voff[i] = (uint32_t)((row * a.v.ss + col) * 2);
+    soff[i] = row * C::KLD + col;
   }
+  auto load_into = [&](const uint16_t* base, int64_t ss, const uint32_t(&off)[C::KCH], int t,
+                       u32x4(&dst)[C::KCH]) {
+    const auto rs = tile_rsrc(base + (int64_t)t * C::BKV * ss);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) voff[r] = (uint32_t)(((4 * v_rg + r) * a.v.ss + C::VCPT * v_cg) * 2);
-  auto load_k = [&](int t) {
-    const auto rs = tile_rsrc(kp + (int64_t)t * C::BKV * a.k.ss);
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) kreg[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, koff[i], 0, 0);
+    for (int i = 0; i < C::KCH; ++i) dst[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[i], 0, 0);
   };
-  auto load_v = [&](int t) {
-    const auto rs = tile_rsrc(vp + (int64_t)t * C::BKV * a.v.ss);
+  auto store_from = [&](uint16_t* tile, const u32x4(&src)[C::KCH]) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      if constexpr (C::VCPT == 8)
-        vreg[r] = __builtin_amdgcn_raw_buffer_load_b128(rs, voff[r], 0, 0);
-      else
-        vreg[r] = __builtin_amdgcn_raw_buffer_load_b64(rs, voff[r], 0, 0);
-    }
+    for (int i = 0; i < C::KCH; ++i) *(u32x4*)(&tile[soff[i]]) = src[i];
   };
-  auto store_k = [&](int buf) {
-#pragma unroll
-    for (int i = 0; i < C::KCH; ++i) {
-      const int ci = tid + C::NT * i;
-      *(u32x4*)(&Ks[buf][(ci / (D / 8)) * C::KLD + (ci % (D / 8)) * 8]) = kreg[i];
-    }
-  };
-  auto store_v = [&](int buf) {
-#pragma unroll
-    for (int w = 0; w < C::VCPT / 2; ++w) {
-      u32x2 c0, c1;
-      transpose4x2(vreg[0][w], vreg[1][w], vreg[2][w], vreg[3][w], c0, c1);
-      const int d = C::VCPT * v_cg + 2 * w;
-      *(u32x2*)(&Vt[buf][d * C::VLD + 4 * v_rg]) = c0;
-      *(u32x2*)(&Vt[buf][(d + 1) * C::VLD + 4 * v_rg]) = c1;
-    }
-  };
+  auto load_k = [&](int t) { load_into(kp, a.k.ss, koff, t, kreg); };
+  auto load_v = [&](int t) { load_into(vp, a.v.ss, voff, t, vreg); };
+  auto store_k = [&](int buf) { store_from(Ks[buf], kreg); };
+  auto store_v = [&](int buf) { store_from(Vs[buf], vreg); };
 
   // ---- per-wave compute pieces ----
   f32x16 acc[C::DB];
@@ -214,12 +193,9 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-        for (int db = 0; db < C::DB; ++db) {
-          const uint16_t* vrow = &Vt[buf][(32 * db + l32) * C::VLD + 32 * kb + 16 * hh + 4 * g];
-          const u32x2 lo = *(const u32x2*)vrow;
-          const u32x2 hi = *(const u32x2*)(vrow + 8);
-          acc[db] = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[kb][hh], acc[db]);
-        }
+        for (int db = 0; db < C::DB; ++db)
+          acc[db] = E::mfma(tr_operand(&Vs[buf][(32 * kb + 16 * hh) * C::KLD + 32 * db + tro], C::KLD),
+                            pb[kb][hh], acc[db]);
       }
     }
   };
@@ -262,12 +238,9 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
     auto pv_group = [&](int grp) {
       const int kb = grp >> 1, hh = grp & 1;
 #pragma unroll
-      for (int db = 0; db < C::DB; ++db) {
-        const uint16_t* vrow = &Vt[vbuf][(32 * db + l32) * C::VLD + 32 * kb + 16 * hh + 4 * g];
-        const u32x2 lo = *(const u32x2*)vrow;
-        const u32x2 hi = *(const u32x2*)(vrow + 8);
-        acc[db] = E::mfma(u32x4{lo[0], lo[1], hi[0], hi[1]}, pb[grp], acc[db]);
-      }
+      for (int db = 0; db < C::DB; ++db)
+        acc[db] = E::mfma(tr_operand(&Vs[vbuf][(32 * kb + 16 * hh) * C::KLD + 32 * db + tro], C::KLD),
+                          pb[grp], acc[db]);
     };
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
@@ -303,14 +276,18 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
   };
 
   // ---- prologue: K0, V0, K1 in LDS, K2 and V1 in flight; S for tile 0 ----
-  load_k(0);
-  load_v(0);
-  store_k(0);
-  store_v(0);
-  if (nkv > 1) {
-    load_k(1);
-    store_k(1);
-    load_v(1);
+  // K0, V0 and K1 are requested together (one memory round trip).
+  {
+    u32x4 k1reg[C::KCH];
+    load_k(0);
+    load_v(0);
+    if (nkv > 1) load_into(kp, a.k.ss, koff, 1, k1reg);
+    store_k(0);
+    store_v(0);
+    if (nkv > 1) {
+      store_from(Ks[1], k1reg);
+      load_v(1);
+    }
   }
   if (nkv > 2) load_k(2);
   __syncthreads();
