@@ -46,20 +46,37 @@ template <int D>
 struct FwdCfg {
   static constexpr int BQ = 128;
   static constexpr int BKV = 64;
-  static constexpr int NT = 256;                   // 4 waves x 32 query rows
-  static constexpr int KLD = D + 8;             // K / V tile row stride in LDS (elements)
-  static constexpr int KS = D / 16;             // MFMA k-steps of K Q^T
-  static constexpr int DB = D / 32;             // 32-row blocks of O^T
-  static constexpr int KCH = BKV * D / 8 / NT;  // 16-byte chunks per thread of a K or V tile
+  static constexpr int NT = 256;                     // 4 waves x 32 query rows
+  static constexpr int KS = D / 16;                  // MFMA k-steps of K Q^T
+  static constexpr int DB = D / 32;                  // 32-row blocks of O^T
+  static constexpr int TILE = BKV * D;               // elements of a staged K or V tile
+  static constexpr int CPR = D / 8;                  // 16-byte chunks per row
+  static constexpr int RPS = 64 / CPR;               // rows per 1 KB slice (one wave instruction)
+  static constexpr int SPW = TILE * 2 / 1024 / 4;    // slices per wave per tile
 };
+
+// LDS layout of a staged tile: BKV rows of D elements, no padding; the
+// 16-byte chunk c of row r sits at chunk position c ^ swz(r).
+//   K: swz = r & 7        the A-operand reads of K Q^T (each lane a 16-byte
+//                         chunk, eight consecutive rows per LDS cycle) land
+//                         on eight different chunk positions;
+//   V: swz = 2 * (r & 3)  the transposing reads of V^T (16-lane groups over
+//                         four consecutive rows and two adjacent chunks)
+//                         likewise.
+__device__ __forceinline__ int swz_k(int r) { return r & 7; }
+__device__ __forceinline__ int swz_v(int r) { return (r & 3) << 1; }
 
 constexpr float kRescaleSlack = 8.f;  // log2 units: probabilities stay <= 2^8
 
 template <typename E, int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qtiles) {
   using C = FwdCfg<D>;
-  __shared__ __attribute__((aligned(16))) uint16_t Ks[2][C::BKV * C::KLD];
-  __shared__ __attribute__((aligned(16))) uint16_t Vs[2][C::BKV * C::KLD];
+  // One array per buffer, so that the compiler can see that a direct load
+  // into one buffer never aliases the reads of the other.
+  __shared__ __attribute__((aligned(16))) uint16_t K0[C::TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t K1[C::TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t V0[C::TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t V1[C::TILE];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -84,7 +101,6 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
   const int qw = q0 + 32 * wave;       // first query row of this wave (SGPR)
   const bool wave_valid = qw < S;      // S % 64 == 0: 32-row blocks are all-or-nothing
   const int qrow = qw + l32;
-  const int tro = tr_lane_offset(lane, C::KLD);
 
   u32x4 qf[C::KS];
 #pragma unroll
@@ -95,35 +111,42 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
   const int kv_end = CAUSAL ? min(q0 + C::BQ, S) : S;
   const int nkv = kv_end / C::BKV;
 
-  // ---- staging (global -> registers -> LDS) ----
-  // Buffer loads: one descriptor per tile, rebased with scalar arithmetic; the
-  // per-lane byte offsets inside a tile are fixed.  K and V use the same
-  // 16-byte chunk layout.
-  u32x4 kreg[C::KCH], vreg[C::KCH];
-  uint32_t koff[C::KCH], voff[C::KCH];
-  int soff[C::KCH];  // LDS element offset of each chunk
+  // ---- staging: direct global -> LDS loads ----
+  // A tile is 1 KB slices; wave w fills slices w, w + 4, ...  Lane i of slice
+  // s writes the 16 bytes at row s*RPS + i/CPR, chunk position i%CPR, so it
+  // fetches chunk (i%CPR) ^ swz(row) of that row.  One buffer descriptor per
+  // tile, fixed per-lane byte offsets; completion is tracked by vmcnt and the
+  // barrier that ends each step.
+  uint32_t kdo[C::SPW], vdo[C::SPW];
 #pragma unroll
-  for (int i = 0; i < C::KCH; ++i) {
-    const int ci = tid + C::NT * i;
-    const int row = ci / (D / 8), col = (ci % (D / 8)) * 8;
-    koff[i] = (uint32_t)((row * a.k.ss + col) * 2);
-    voff[i] = (uint32_t)((row * a.v.ss + col) * 2);
-    soff[i] = row * C::KLD + col;
+  for (int m = 0; m < C::SPW; ++m) {
+    const int r = (wave + 4 * m) * C::RPS + lane / C::CPR;
+    const int pos = lane % C::CPR;
+    kdo[m] = (uint32_t)((r * a.k.ss + ((pos ^ swz_k(r)) << 3)) * 2);
+    vdo[m] = (uint32_t)((r * a.v.ss + ((pos ^ swz_v(r)) << 3)) * 2);
   }
-  auto load_into = [&](const uint16_t* base, int64_t ss, const uint32_t(&off)[C::KCH], int t,
-                       u32x4(&dst)[C::KCH]) {
+  auto dma = [&](const uint16_t* base, int64_t ss, const uint32_t(&off)[C::SPW], int t,
+                 uint16_t* tile) {
     const auto rs = tile_rsrc(base + (int64_t)t * C::BKV * ss);
 #pragma unroll
-    for (int i = 0; i < C::KCH; ++i) dst[i] = __builtin_amdgcn_raw_buffer_load_b128(rs, off[i], 0, 0);
+    for (int m = 0; m < C::SPW; ++m)
+      buffer_load_lds16(rs, off[m], tile + (wave + 4 * m) * 512);
   };
-  auto store_from = [&](uint16_t* tile, const u32x4(&src)[C::KCH]) {
+
+  // Per-lane LDS offsets of the MFMA operands.
+  //   K Q^T A operand, k-step ks: row l32 (+32 per key block), chunk 2ks + g;
+  //   V^T operand of P V (transposing read), O^T block db: row 4g + (lane%16)/4
+  //   (+16 per half-block, +8 for the second read), column 32db +
+  //   16((lane/16)%2) + 4(lane%4).
+  int kro[C::KS], vro[C::DB];
 #pragma unroll
-    for (int i = 0; i < C::KCH; ++i) *(u32x4*)(&tile[soff[i]]) = src[i];
-  };
-  auto load_k = [&](int t) { load_into(kp, a.k.ss, koff, t, kreg); };
-  auto load_v = [&](int t) { load_into(vp, a.v.ss, voff, t, vreg); };
-  auto store_k = [&](int buf) { store_from(Ks[buf], kreg); };
-  auto store_v = [&](int buf) { store_from(Vs[buf], vreg); };
+  for (int ks = 0; ks < C::KS; ++ks) kro[ks] = l32 * D + (((2 * ks + g) ^ swz_k(l32)) << 3);
+#pragma unroll
+  for (int db = 0; db < C::DB; ++db) {
+    const int r = 4 * g + ((lane & 15) >> 2);
+    const int ch = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    vro[db] = r * D + ((ch ^ swz_v(r)) << 3) + 4 * (lane & 1);
+  }
 
   // ---- per-wave compute pieces ----
   f32x16 acc[C::DB];
@@ -133,13 +156,13 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
   float l_run = 0.f;        // running sum over this lane's half of the keys
   const float c = a.scale_log2;
 
-  // S^T for one key tile (two 32-key blocks) from LDS buffer `buf`.
-  auto qk = [&](int buf, f32x16(&s)[2]) {
+  // S^T for one key tile (two 32-key blocks).
+  auto qk = [&](const uint16_t* kt, f32x16(&s)[2]) {
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const u32x4 kf = *(const u32x4*)(&Ks[buf][(32 * kb + l32) * C::KLD + 16 * ks + 8 * g]);
+        const u32x4 kf = *(const u32x4*)(&kt[32 * kb * D + kro[ks]]);
         s[kb] = E::mfma(kf, qf[ks], ks == 0 ? f32x16{} : s[kb]);
       }
     }
@@ -186,18 +209,16 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
     }
     l_run += psum;
   };
-  // O^T += V^T P^T with V^T from LDS buffer `buf`.
-  auto pv = [&](int buf, const u32x4(&pb)[2][2]) {
+  // O^T += V^T P^T.
+  auto pv = [&](const uint16_t* vt, const u32x4(&pb)[2][2]) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
+      for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int db = 0; db < C::DB; ++db)
-          acc[db] = E::mfma(tr_operand(&Vs[buf][(32 * kb + 16 * hh) * C::KLD + 32 * db + tro], C::KLD),
-                            pb[kb][hh], acc[db]);
-      }
-    }
+          acc[db] = E::mfma(tr_operand(&vt[(32 * kb + 16 * hh) * D + vro[db]], D), pb[kb][hh],
+                            acc[db]);
   };
 
   // Mask-free tile with the matrix-core work woven into the softmax.  The 32
@@ -206,7 +227,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
   // probabilities, and issues the P V MFMAs of group g-1, so that every MFMA
   // has ~7 VALU instructions behind it to overlap with.  sched_barrier keeps
   // the compiler from clustering the MFMAs back together.
-  auto hot = [&](int kbuf, int vbuf, f32x16(&s)[2], f32x16(&sn)[2]) {
+  auto hot = [&](const uint16_t* kt, const uint16_t* vt, f32x16(&s)[2], f32x16(&sn)[2]) {
     constexpr int KPG = C::KS / 4;  // k-steps of the next tile's S per group
     // K fragments of group g+1 are read while group g computes.
     u32x4 kf[2][KPG][2];
@@ -215,8 +236,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
       for (int kk = 0; kk < KPG; ++kk)
 #pragma unroll
         for (int nb = 0; nb < 2; ++nb)
-          dst[kk][nb] = *(const u32x4*)(&Ks[kbuf][(32 * nb + l32) * C::KLD +
-                                                  16 * (KPG * grp + kk) + 8 * g]);
+          dst[kk][nb] = *(const u32x4*)(&kt[32 * nb * D + kro[KPG * grp + kk]]);
     };
     read_k(0, kf[0]);
 
@@ -239,8 +259,8 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
       const int kb = grp >> 1, hh = grp & 1;
 #pragma unroll
       for (int db = 0; db < C::DB; ++db)
-        acc[db] = E::mfma(tr_operand(&Vs[vbuf][(32 * kb + 16 * hh) * C::KLD + 32 * db + tro], C::KLD),
-                          pb[grp], acc[db]);
+        acc[db] = E::mfma(tr_operand(&vt[(32 * kb + 16 * hh) * D + vro[db]], D), pb[grp],
+                          acc[db]);
     };
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
@@ -275,73 +295,62 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
     l_run += psum;
   };
 
-  // ---- prologue: K0, V0, K1 in LDS, K2 and V1 in flight; S for tile 0 ----
-  // K0, V0 and K1 are requested together (one memory round trip).
-  {
-    u32x4 k1reg[C::KCH];
-    load_k(0);
-    load_v(0);
-    if (nkv > 1) load_into(kp, a.k.ss, koff, 1, k1reg);
-    store_k(0);
-    store_v(0);
-    if (nkv > 1) {
-      store_from(Ks[1], k1reg);
-      load_v(1);
-    }
-  }
-  if (nkv > 2) load_k(2);
+  // ---- prologue: K0, V0, K1 into LDS; S for tile 0 ----
+  dma(kp, a.k.ss, kdo, 0, K0);
+  dma(vp, a.v.ss, vdo, 0, V0);
+  if (nkv > 1) dma(kp, a.k.ss, kdo, 1, K1);
   __syncthreads();
 
   f32x16 sA[2], sB[2];
-  if (wave_valid) qk(0, sA);
-  // Step 0 overwrites K buffer 0 (K_2 lands where K_0 was): every wave must
-  // be done reading it.
+  if (wave_valid) qk(K0, sA);
+  // Step 0 loads K_2 into K0: every wave must be done reading it.
   __syncthreads();
 
-  // Tile j.  LDS writes first: K_{j+2} into K_j's buffer and V_{j+1} into
-  // V_{j-1}'s buffer (both were last read before the previous barrier); then
-  // the loads of K_{j+3} and V_{j+2} go out, with a whole tile of compute to
-  // land.  S_{j+1} runs on the matrix cores while the VALU turns S_j into P_j;
-  // then O += P_j V_j.
-  auto step = [&](int j, f32x16(&scur)[2], f32x16(&snext)[2], auto masked_tag) {
+  // Tile j (parity P = j & 1, a compile-time tag).  K_{j+2} goes into K_j's
+  // buffer and V_{j+1} into V_{j-1}'s (both last read before the previous
+  // barrier); the loads complete under this step's compute and the barrier
+  // at its end.  S_{j+1} runs on the matrix cores while the VALU turns S_j
+  // into P_j; then O += P_j V_j.
+  auto step = [&](int j, f32x16(&scur)[2], f32x16(&snext)[2], auto masked_tag, auto parity) {
     constexpr bool MASKED = decltype(masked_tag)::value;
+    constexpr int P = decltype(parity)::value;
+    uint16_t* const kfree = P ? K1 : K0;  // K_j's buffer -> K_{j+2}
+    uint16_t* const knext = P ? K0 : K1;  // K_{j+1}
+    uint16_t* const vcur = P ? V1 : V0;   // V_j
+    uint16_t* const vfree = P ? V0 : V1;  // V_{j-1}'s buffer -> V_{j+1}
     const int kv0 = j * C::BKV;
-    if (j + 2 < nkv) store_k(j & 1);
-    if (j + 1 < nkv) store_v((j + 1) & 1);
-    if (j + 3 < nkv) load_k(j + 3);
-    if (j + 2 < nkv) load_v(j + 2);
+    if (j + 2 < nkv) dma(kp, a.k.ss, kdo, j + 2, kfree);
+    if (j + 1 < nkv) dma(vp, a.v.ss, vdo, j + 1, vfree);
     u32x4 pb[2][2];
     if (!MASKED) {
-      hot((j + 1) & 1, j & 1, scur, snext);
+      hot(knext, vcur, scur, snext);
     } else if (wave_valid) {
-      if (j + 1 < nkv && (!CAUSAL || (j + 1) * C::BKV <= qw + 31)) qk((j + 1) & 1, snext);
+      if (j + 1 < nkv && (!CAUSAL || (j + 1) * C::BKV <= qw + 31)) qk(knext, snext);
       if (!CAUSAL || kv0 <= qw + 31) {
         softmax(scur, pb, kv0, CAUSAL && kv0 + C::BKV - 1 > qw);
-        pv(j & 1, pb);
+        pv(vcur, pb);
       }
     }
     __syncthreads();
   };
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
 
   // Branch-free body: tile j lies below the diagonal for every wave of the
-  // workgroup and tile j+1 exists and is visible to every wave.
-  const int n_main = wave_valid ? (CAUSAL ? min(q0 / C::BKV, nkv - 1) : nkv - 1) : 0;
+  // workgroup and tile j+1 exists and is visible to every wave.  An even
+  // count keeps the buffer parity of each call site fixed.
+  const int n_main =
+      (wave_valid ? (CAUSAL ? min(q0 / C::BKV, nkv - 1) : nkv - 1) : 0) & ~1;
   int j = 0;
-  for (; j + 1 < n_main; j += 2) {
-    step(j, sA, sB, std::false_type{});
-    step(j + 1, sB, sA, std::false_type{});
-  }
-  if (j < n_main) {
-    step(j, sA, sB, std::false_type{});
-    ++j;
-    sA[0] = sB[0];
-    sA[1] = sB[1];
+  for (; j < n_main; j += 2) {
+    step(j, sA, sB, std::false_type{}, P0{});
+    step(j + 1, sB, sA, std::false_type{}, P1{});
   }
   for (; j + 1 < nkv; j += 2) {
-    step(j, sA, sB, std::true_type{});
-    step(j + 1, sB, sA, std::true_type{});
+    step(j, sA, sB, std::true_type{}, P0{});
+    step(j + 1, sB, sA, std::true_type{}, P1{});
   }
-  if (j < nkv) step(j, sA, sB, std::true_type{});
+  if (j < nkv) step(j, sA, sB, std::true_type{}, P0{});
 
   if (!wave_valid) return;
   const float l_tot = sum_halves(l_run);

@@ -208,6 +208,15 @@ __device__ __forceinline__ int tr_lane_offset(int lane, int ld) {
   return (4 * (lane >> 5) + ((lane & 15) >> 2)) * ld + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 }
 
+// 16 bytes per lane from a buffer straight into LDS (no VGPRs): lane i's data
+// lands at lds + 16*i bytes; `lds` must be wave-uniform.  Completion is
+// counted by vmcnt.
+__device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rs, uint32_t voffset,
+                                                  uint16_t* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(lds), 16,
+                                           voffset, 0, 0, 0);
+}
+
 __device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t* p) {
   typedef __attribute__((ext_vector_type(4))) short s16x4;
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
