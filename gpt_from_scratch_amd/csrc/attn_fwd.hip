@@ -53,6 +53,10 @@ struct FwdCfg {
   static constexpr int CPR = D / 8;                  // 16-byte chunks per row
   static constexpr int RPS = 64 / CPR;               // rows per 1 KB slice (one wave instruction)
   static constexpr int SPW = TILE * 2 / 1024 / 4;    // slices per wave per tile
+  // LDS buffers per tensor.  Steps run in phases of NBUF/2 tiles with one
+  // barrier per phase; D = 128 tiles are twice as large, so two buffers.
+  static constexpr int NBUF = (D == 64) ? 4 : 2;
+  static constexpr int L = NBUF / 2;  // tiles per phase
 };
 
 // LDS layout of a staged tile: BKV rows of D elements, no padding; the
@@ -72,11 +76,30 @@ template <typename E, int D, bool CAUSAL>
 __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qtiles) {
   using C = FwdCfg<D>;
   // One array per buffer, so that the compiler can see that a direct load
-  // into one buffer never aliases the reads of the other.
+  // into one buffer never aliases the reads of another.
+  constexpr int T23 = C::NBUF == 4 ? C::TILE : 8;
   __shared__ __attribute__((aligned(16))) uint16_t K0[C::TILE];
   __shared__ __attribute__((aligned(16))) uint16_t K1[C::TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t K2[T23];
+  __shared__ __attribute__((aligned(16))) uint16_t K3[T23];
   __shared__ __attribute__((aligned(16))) uint16_t V0[C::TILE];
   __shared__ __attribute__((aligned(16))) uint16_t V1[C::TILE];
+  __shared__ __attribute__((aligned(16))) uint16_t V2[T23];
+  __shared__ __attribute__((aligned(16))) uint16_t V3[T23];
+  auto kbuf = [&](auto i) __attribute__((always_inline)) -> uint16_t* {
+    constexpr int I = decltype(i)::value;
+    if constexpr (I == 0) return K0;
+    else if constexpr (I == 1) return K1;
+    else if constexpr (I == 2) return K2;
+    else return K3;
+  };
+  auto vbuf = [&](auto i) __attribute__((always_inline)) -> uint16_t* {
+    constexpr int I = decltype(i)::value;
+    if constexpr (I == 0) return V0;
+    else if constexpr (I == 1) return V1;
+    else if constexpr (I == 2) return V2;
+    else return V3;
+  };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -126,7 +149,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
     vdo[m] = (uint32_t)((r * a.v.ss + ((pos ^ swz_v(r)) << 3)) * 2);
   }
   auto dma = [&](const uint16_t* base, int64_t ss, const uint32_t(&off)[C::SPW], int t,
-                 uint16_t* tile) {
+                 uint16_t* tile) __attribute__((always_inline)) {
     const auto rs = tile_rsrc(base + (int64_t)t * C::BKV * ss);
 #pragma unroll
     for (int m = 0; m < C::SPW; ++m)
@@ -157,7 +180,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
   const float c = a.scale_log2;
 
   // S^T for one key tile (two 32-key blocks).
-  auto qk = [&](const uint16_t* kt, f32x16(&s)[2]) {
+  auto qk = [&](const uint16_t* kt, f32x16(&s)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int ks = 0; ks < C::KS; ++ks) {
 #pragma unroll
@@ -168,7 +191,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
     }
   };
   // Softmax of S^T in place, probabilities packed into pb; key tile starts at kv0.
-  auto softmax = [&](f32x16(&s)[2], u32x4(&pb)[2][2], int kv0, bool masked) {
+  auto softmax = [&](f32x16(&s)[2], u32x4(&pb)[2][2], int kv0, bool masked) __attribute__((always_inline)) {
     if (masked) {
       const int rel = qrow - kv0 - 4 * g;  // visible iff (kv - kv0 - 4g) <= rel
 #pragma unroll
@@ -210,7 +233,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
     l_run += psum;
   };
   // O^T += V^T P^T.
-  auto pv = [&](const uint16_t* vt, const u32x4(&pb)[2][2]) {
+  auto pv = [&](const uint16_t* vt, const u32x4(&pb)[2][2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -227,11 +250,11 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
   // probabilities, and issues the P V MFMAs of group g-1, so that every MFMA
   // has ~7 VALU instructions behind it to overlap with.  sched_barrier keeps
   // the compiler from clustering the MFMAs back together.
-  auto hot = [&](const uint16_t* kt, const uint16_t* vt, f32x16(&s)[2], f32x16(&sn)[2]) {
+  auto hot = [&](const uint16_t* kt, const uint16_t* vt, f32x16(&s)[2], f32x16(&sn)[2]) __attribute__((always_inline)) {
     constexpr int KPG = C::KS / 4;  // k-steps of the next tile's S per group
     // K fragments of group g+1 are read while group g computes.
     u32x4 kf[2][KPG][2];
-    auto read_k = [&](int grp, u32x4(&dst)[KPG][2]) {
+    auto read_k = [&](int grp, u32x4(&dst)[KPG][2]) __attribute__((always_inline)) {
 #pragma unroll
       for (int kk = 0; kk < KPG; ++kk)
 #pragma unroll
@@ -255,7 +278,7 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
     const float mref = m_run;
     float psum = 0.f;
     u32x4 pb[4];
-    auto pv_group = [&](int grp) {
+    auto pv_group = [&](int grp) __attribute__((always_inline)) {
       const int kb = grp >> 1, hh = grp & 1;
 #pragma unroll
       for (int db = 0; db < C::DB; ++db)
@@ -295,32 +318,33 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
     l_run += psum;
   };
 
-  // ---- prologue: K0, V0, K1 into LDS; S for tile 0 ----
+  // ---- prologue: K_0..K_L and V_0..V_{L-1} into LDS; S for tile 0 ----
+  using I0_ = std::integral_constant<int, 0>;
+  using I1_ = std::integral_constant<int, 1>;
+  using I2_ = std::integral_constant<int, 2>;
   dma(kp, a.k.ss, kdo, 0, K0);
   dma(vp, a.v.ss, vdo, 0, V0);
   if (nkv > 1) dma(kp, a.k.ss, kdo, 1, K1);
+  if constexpr (C::L == 2) {
+    if (nkv > 1) dma(vp, a.v.ss, vdo, 1, V1);
+    if (nkv > 2) dma(kp, a.k.ss, kdo, 2, K2);
+  }
   __syncthreads();
 
   f32x16 sA[2], sB[2];
   if (wave_valid) qk(K0, sA);
-  // Step 0 loads K_2 into K0: every wave must be done reading it.
+  // The first phase loads a tile into K0: every wave must be done reading it.
   __syncthreads();
 
-  // Tile j (parity P = j & 1, a compile-time tag).  K_{j+2} goes into K_j's
-  // buffer and V_{j+1} into V_{j-1}'s (both last read before the previous
-  // barrier); the loads complete under this step's compute and the barrier
-  // at its end.  S_{j+1} runs on the matrix cores while the VALU turns S_j
-  // into P_j; then O += P_j V_j.
-  auto step = [&](int j, f32x16(&scur)[2], f32x16(&snext)[2], auto masked_tag, auto parity) {
+  // Tile j in buffer slot I = j % NBUF (a compile-time tag): S_{j+1} from K
+  // slot I+1 runs on the matrix cores while the VALU turns S_j into P_j; then
+  // O += P_j V_j from V slot I.
+  auto step = [&](int j, f32x16(&scur)[2], f32x16(&snext)[2], auto masked_tag, auto slot) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
-    constexpr int P = decltype(parity)::value;
-    uint16_t* const kfree = P ? K1 : K0;  // K_j's buffer -> K_{j+2}
-    uint16_t* const knext = P ? K0 : K1;  // K_{j+1}
-    uint16_t* const vcur = P ? V1 : V0;   // V_j
-    uint16_t* const vfree = P ? V0 : V1;  // V_{j-1}'s buffer -> V_{j+1}
+    constexpr int I = decltype(slot)::value;
+    const uint16_t* const knext = kbuf(std::integral_constant<int, (I + 1) % C::NBUF>{});
+    const uint16_t* const vcur = vbuf(std::integral_constant<int, I>{});
     const int kv0 = j * C::BKV;
-    if (j + 2 < nkv) dma(kp, a.k.ss, kdo, j + 2, kfree);
-    if (j + 1 < nkv) dma(vp, a.v.ss, vdo, j + 1, vfree);
     u32x4 pb[2][2];
     if (!MASKED) {
       hot(knext, vcur, scur, snext);
@@ -331,26 +355,65 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
         pv(vcur, pb);
       }
     }
+  };
+  // Phase starting at tile j (slot I0 = j % NBUF): loads K_{j+L+1..j+2L} and
+  // V_{j+L..j+2L-1} into the slots the previous phase finished reading, runs
+  // its L tiles and ends with the one barrier, by which the loads have landed.
+  auto phase = [&](int j, auto masked_tag, auto slot0) __attribute__((always_inline)) {
+    constexpr int I0 = decltype(slot0)::value;
+    if (j + C::L + 1 < nkv)
+      dma(kp, a.k.ss, kdo, j + C::L + 1, kbuf(std::integral_constant<int, (I0 + C::L + 1) % C::NBUF>{}));
+    if (j + C::L < nkv)
+      dma(vp, a.v.ss, vdo, j + C::L, vbuf(std::integral_constant<int, (I0 + C::L) % C::NBUF>{}));
+    if constexpr (C::L == 2) {
+      if (j + 4 < nkv) dma(kp, a.k.ss, kdo, j + 4, kbuf(std::integral_constant<int, I0>{}));
+      if (j + 3 < nkv) dma(vp, a.v.ss, vdo, j + 3, vbuf(std::integral_constant<int, (I0 + 3) % 4>{}));
+      step(j, sA, sB, masked_tag, std::integral_constant<int, I0>{});
+      if (j + 1 < nkv) step(j + 1, sB, sA, masked_tag, std::integral_constant<int, I0 + 1>{});
+    } else {
+      // one tile per phase: scur alternates with the slot
+      if constexpr (I0 == 0)
+        step(j, sA, sB, masked_tag, I0_{});
+      else
+        step(j, sB, sA, masked_tag, I1_{});
+    }
     __syncthreads();
   };
-  using P0 = std::integral_constant<int, 0>;
-  using P1 = std::integral_constant<int, 1>;
 
   // Branch-free body: tile j lies below the diagonal for every wave of the
-  // workgroup and tile j+1 exists and is visible to every wave.  An even
-  // count keeps the buffer parity of each call site fixed.
+  // workgroup and tile j+1 exists and is visible to every wave.  Phases hold
+  // two tiles each (an even count keeps S_j in sA for even j).
   const int n_main =
       (wave_valid ? (CAUSAL ? min(q0 / C::BKV, nkv - 1) : nkv - 1) : 0) & ~1;
   int j = 0;
-  for (; j < n_main; j += 2) {
-    step(j, sA, sB, std::false_type{}, P0{});
-    step(j + 1, sB, sA, std::false_type{}, P1{});
-  }
-  for (; j + 1 < nkv; j += 2) {
-    step(j, sA, sB, std::true_type{}, P0{});
-    step(j + 1, sB, sA, std::true_type{}, P1{});
-  }
-  if (j < nkv) step(j, sA, sB, std::true_type{}, P0{});
+  auto run = [&](int j_end, auto masked_tag) __attribute__((always_inline)) {
+    // phases over [j, j_end) with j even; slot pattern repeats every NBUF tiles
+    if constexpr (C::L == 2) {
+      if ((j & 3) == 2 && j < j_end) {
+        phase(j, masked_tag, I2_{});
+        j += 2;
+      }
+      for (; j + 2 < j_end; j += 4) {
+        phase(j, masked_tag, I0_{});
+        phase(j + 2, masked_tag, I2_{});
+      }
+      if (j < j_end) {
+        phase(j, masked_tag, I0_{});
+        j += 2;
+      }
+    } else {
+      for (; j + 1 < j_end; j += 2) {
+        phase(j, masked_tag, I0_{});
+        phase(j + 1, masked_tag, I1_{});
+      }
+      if (j < j_end) {
+        phase(j, masked_tag, I0_{});
+        ++j;
+      }
+    }
+  };
+  run(n_main, std::false_type{});
+  run(nkv, std::true_type{});
 
   if (!wave_valid) return;
   const float l_tot = sum_halves(l_run);
