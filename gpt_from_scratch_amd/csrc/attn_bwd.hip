@@ -71,26 +71,34 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(AttnArgs a, FastDiv div
 //          over query tiles, with K and V rows of its keys in registers;
 //   kind 1 (dQ, `_attn_bwd_LoopKV`):   OWN queries of one head; the item loops
 //          over key tiles, with Q and dO rows of its queries in registers.
-// Both stream TILE-row tiles of the other two tensors through LDS (double
-// buffered) and keep the same register layout: two resident row sets (B
-// operands) and one staged tile, so one launch can run both kinds.
+// Both stream TILE-row tiles of the other two tensors into LDS with direct
+// global -> LDS loads (double buffered, no registers, no LDS store
+// instructions) and keep the same register layout (two resident row sets,
+// the B operands), so one launch can run both kinds.
 // ---------------------------------------------------------------------------
 template <int D>
 struct BwdCfg {
   static constexpr int OWN = 128;                   // rows owned by an item
   static constexpr int TILE = (D == 64) ? 64 : 32;  // rows of a streamed tile
   static constexpr int NT = 256;
-  static constexpr int RLD = D + 8;  // row stride of the row-major LDS tiles (elements)
   static constexpr int KS = D / 16;
   static constexpr int DB = D / 32;
-  static constexpr int TB = TILE / 32;  // 32-row blocks per streamed tile
-  static constexpr int CG = D / 4;      // loader column groups (4 columns each)
-  static constexpr int RG = TILE / 4;   // loader row groups (4 rows each)
-  static_assert(CG * RG == NT, "loader covers the tile with 4x4 blocks");
-  static constexpr int BUF = 2 * TILE * RLD;  // uint16 per LDS buffer: both streamed tensors
-  // two buffers, then lse*log2e and -delta of each buffer's query rows (dK/dV kind)
-  static constexpr int LDS_BYTES = 2 * BUF * 2 + 2 * 2 * TILE * 4;
+  static constexpr int TB = TILE / 32;             // 32-row blocks per streamed tile
+  static constexpr int ELEMS = TILE * D;           // elements of one streamed tile
+  static constexpr int CPR = D / 8;                // 16-byte chunks per row
+  static constexpr int RPS = 64 / CPR;             // rows per 1 KB slice (one wave instruction)
+  static constexpr int SPW = ELEMS * 2 / 1024 / 4; // slices per wave per tile
+  static_assert(SPW >= 1 && TILE <= 64, "tile layout");
 };
+
+// LDS layout of a streamed tile: TILE rows of D elements, no padding; the
+// 16-byte chunk c of row r sits at chunk position c ^ swz(r), with
+//   swz(r) = 2*(r & 3) + ((r >> 2) & 1).
+// The tiles are read two ways and the swizzle suits both: 16-byte row reads
+// (eight consecutive rows, one chunk each: swz takes eight distinct values)
+// and transposing reads (16-lane groups over four consecutive rows and two
+// adjacent chunks: swz >> 1 takes four distinct values there).
+__device__ __forceinline__ int bwd_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
 struct BwdItem {
   int kind;  // 0: dK/dV, 1: dQ
@@ -100,23 +108,27 @@ struct BwdItem {
 
 template <int D>
 struct Resident {
-  u32x4 r[2][D / 16];  // kind 0: K, V rows; kind 1: Q, dO rows (lane: row l%32, 8 columns)
+  u32x4 r[2][D / 16];  // kind 0: K, -V rows; kind 1: Q, dO rows (lane: row l%32, 8 columns)
   float lse2, dl;      // kind 1: lse*log2e and delta of this lane's query row
 };
 
-struct Staged {
-  u32x2 t[2][4];  // one streamed tile: 4 rows x 4 columns of each tensor per thread
-  float s0, s1;   // kind 0: lse*log2e and -delta of query row `tid` (tid < TILE)
+// One LDS staging buffer: the two streamed tiles and, for the dK/dV kind,
+// lse and delta of the tile's query rows (as stored in memory).
+struct BwdBuf {
+  uint16_t* t0;
+  uint16_t* t1;
+  float* sl;
 };
 
-// Where an item's streamed tiles come from: head bases, strides and this
-// thread's fixed byte offset inside a tile (buffer loads, so that advancing
-// a tile is scalar arithmetic).
+// Where an item's streamed tiles come from: head bases and strides, and this
+// lane's byte offsets inside a tile for its slices (buffer loads, so that
+// advancing a tile is scalar arithmetic).
+template <int D>
 struct StageSrc {
   const uint16_t* p0;
   const uint16_t* p1;
   int64_t ss0, ss1;
-  uint32_t off0, off1;
+  uint32_t off0[BwdCfg<D>::SPW], off1[BwdCfg<D>::SPW];
   const float* lse;
   const float* delta;
 };
@@ -146,10 +158,12 @@ __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& 
     const auto r1 = tile_rsrc(head_ptr(t1, b, h) + (int64_t)w0 * t1.ss);
     const uint32_t o0 = (uint32_t)(((lane & 31) * t0.ss + 8 * (lane >> 5)) * 2);
     const uint32_t o1 = (uint32_t)(((lane & 31) * t1.ss + 8 * (lane >> 5)) * 2);
+    // kind 0 keeps V negated (sign bits of both 16-bit halves flipped)
+    const uint32_t neg = it.kind ? 0u : 0x80008000u;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
       res.r[0][ks] = __builtin_amdgcn_raw_buffer_load_b128(r0, o0 + 32 * ks, 0, 0);
-      res.r[1][ks] = __builtin_amdgcn_raw_buffer_load_b128(r1, o1 + 32 * ks, 0, 0);
+      res.r[1][ks] = __builtin_amdgcn_raw_buffer_load_b128(r1, o1 + 32 * ks, 0, 0) ^ neg;
     }
     if (it.kind) {
       const int64_t o = (int64_t)it.bh * a.S + w0;
@@ -170,64 +184,53 @@ __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& 
 }
 
 template <int D>
-__device__ __forceinline__ StageSrc stage_src(const AttnArgs& a, const BwdItem& it) {
+__device__ __forceinline__ StageSrc<D> stage_src(const AttnArgs& a, const BwdItem& it) {
   using C = BwdCfg<D>;
-  const int tid = threadIdx.x;
-  const int rg = tid / C::CG;
-  const int cg = tid % C::CG;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int b = it.bh / a.H;
   const int h = it.bh % a.H;
   const TensorArg& t0 = it.kind ? a.k : a.q;
   const TensorArg& t1 = it.kind ? a.v : a.dout;
-  StageSrc s;
+  StageSrc<D> s;
   s.p0 = head_ptr(t0, b, h);
   s.p1 = head_ptr(t1, b, h);
   s.ss0 = t0.ss;
   s.ss1 = t1.ss;
-  s.off0 = (uint32_t)((4 * rg * t0.ss + 4 * cg) * 2);
-  s.off1 = (uint32_t)((4 * rg * t1.ss + 4 * cg) * 2);
+  // Slice m of this wave covers rows (wave + 4m)*RPS ..; lane i writes chunk
+  // position i%CPR of row (wave + 4m)*RPS + i/CPR, i.e. fetches chunk
+  // (i%CPR) ^ swz(row).
+#pragma unroll
+  for (int m = 0; m < C::SPW; ++m) {
+    const int r = (wave + 4 * m) * C::RPS + lane / C::CPR;
+    const int col = ((lane % C::CPR) ^ bwd_swz(r)) << 3;
+    s.off0[m] = (uint32_t)((r * t0.ss + col) * 2);
+    s.off1[m] = (uint32_t)((r * t1.ss + col) * 2);
+  }
   s.lse = a.lse + (int64_t)it.bh * a.S;
   s.delta = a.delta + (int64_t)it.bh * a.S;
   return s;
 }
 
-// Streamed tile starting at row `row0` into registers.
+// Streamed tile starting at row `row0` straight into LDS buffer `dst`;
+// completion is tracked by vmcnt and the barrier that ends the step.
 template <int D>
-__device__ __forceinline__ void load_stage(const StageSrc& s, int kind, int row0, Staged& st) {
+__device__ __forceinline__ void dma_stage(const StageSrc<D>& s, int kind, int row0,
+                                          const BwdBuf& dst) {
+  using C = BwdCfg<D>;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const auto r0 = tile_rsrc(s.p0 + (int64_t)row0 * s.ss0);
   const auto r1 = tile_rsrc(s.p1 + (int64_t)row0 * s.ss1);
-  const uint32_t rb0 = (uint32_t)(s.ss0 * 2), rb1 = (uint32_t)(s.ss1 * 2);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    st.t[0][r] = __builtin_amdgcn_raw_buffer_load_b64(r0, s.off0, r * rb0, 0);
-    st.t[1][r] = __builtin_amdgcn_raw_buffer_load_b64(r1, s.off1, r * rb1, 0);
+  for (int m = 0; m < C::SPW; ++m) {
+    buffer_load_lds16(r0, s.off0[m], dst.t0 + (wave + 4 * m) * 512);
+    buffer_load_lds16(r1, s.off1[m], dst.t1 + (wave + 4 * m) * 512);
   }
-  const int tid = threadIdx.x;
-  if (kind == 0 && tid < BwdCfg<D>::TILE) {
-    const uint32_t lo = __builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(s.lse + row0), tid * 4, 0, 0);
-    const uint32_t dl = __builtin_amdgcn_raw_buffer_load_b32(tile_rsrc(s.delta + row0), tid * 4, 0, 0);
-    st.s0 = __builtin_bit_cast(float, lo) * kLog2e;
-    st.s1 = -__builtin_bit_cast(float, dl);  // dP accumulators start at -delta
-  }
-}
-
-// Staged tile into one LDS buffer (row-major, both tensors) and, for the
-// dK/dV kind, its query rows' lse and -delta.
-template <int D>
-__device__ __forceinline__ void store_stage(const Staged& st, int kind, uint16_t* buf, float* slb) {
-  using C = BwdCfg<D>;
-  const int tid = threadIdx.x;
-  const int rg = tid / C::CG;
-  const int cg = tid % C::CG;
-  uint16_t* t1 = buf + C::TILE * C::RLD;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    *(u32x2*)(&buf[(4 * rg + r) * C::RLD + 4 * cg]) = st.t[0][r];
-    *(u32x2*)(&t1[(4 * rg + r) * C::RLD + 4 * cg]) = st.t[1][r];
-  }
-  if (kind == 0 && tid < C::TILE) {
-    slb[tid] = st.s0;
-    slb[C::TILE + tid] = st.s1;
+  if (kind == 0 && wave >= 2 && lane < C::TILE) {
+    // waves 2 and 3: lse and delta of the tile's query rows (4 bytes per lane)
+    const float* src = (wave == 2 ? s.lse : s.delta) + row0;
+    buffer_load_lds4(tile_rsrc(src), lane * 4, dst.sl + (wave - 2) * C::TILE);
   }
 }
 
@@ -235,14 +238,13 @@ __device__ __forceinline__ void store_stage(const Staged& st, int kind, uint16_t
 // dK / dV item.  Wave w owns keys [kv0 + 32w, +32).  S = Q K^T and
 // dP = dO V^T are computed with keys along the lane index, so P and dS leave
 // the accumulators in B-operand form for dV^T = dO^T P and dK^T = Q^T dS; the
-// dO^T and Q^T A operands are read transposed from the row-major tiles.
-// `stg` holds the item's first query tile on entry.
+// dO^T and Q^T A operands are read transposed from the same tiles.
+// The dP accumulators start at +delta and the V rows are negated once per
+// item, so they hold delta - dO V^T and dS = -P * acc.
 // ---------------------------------------------------------------------------
 template <typename E, int D, bool CAUSAL>
 __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
-                                          const Resident<D>& res, Staged& stg,
-                                          uint16_t (*smem)[BwdCfg<D>::BUF],
-                                          float (*sl)[2 * BwdCfg<D>::TILE]) {
+                                          const Resident<D>& res, const BwdBuf (&bufs)[2]) {
   using C = BwdCfg<D>;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
@@ -254,13 +256,24 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
   const int kw = kv0 + 32 * wave;
   const bool wave_valid = kw < S;
   const int krow = kw + l32;
-  const int tro = tr_lane_offset(lane, C::RLD);
   const u32x4(&kf)[C::KS] = res.r[0];
-  const u32x4(&vf)[C::KS] = res.r[1];
+  const u32x4(&vn)[C::KS] = res.r[1];  // -V
+
+  // per-lane LDS offsets: 16-byte row reads (row l32, chunk 2ks + g) and
+  // transposing reads (row 4g + (lane%16)/4, column 32db + 16((lane/16)%2) + 4(lane%4))
+  int rro[C::KS], tro[C::DB];
+#pragma unroll
+  for (int ks = 0; ks < C::KS; ++ks) rro[ks] = l32 * D + (((2 * ks + g) ^ bwd_swz(l32)) << 3);
+#pragma unroll
+  for (int db = 0; db < C::DB; ++db) {
+    const int r = 4 * g + ((lane & 15) >> 2);
+    const int ch = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    tro[db] = r * D + ((ch ^ bwd_swz(r)) << 3) + 4 * (lane & 1);
+  }
 
   const int q_begin = first_row<D, CAUSAL>(it);
   const int nq = (S - q_begin) / C::TILE;
-  const StageSrc src = stage_src<D>(a, it);
+  const StageSrc<D> src = stage_src<D>(a, it);
 
   f32x16 dk[C::DB], dv[C::DB];
 #pragma unroll
@@ -270,61 +283,60 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
   }
   const float c = a.scale_log2;
 
-  store_stage<D>(stg, 0, smem[0], sl[0]);
+  dma_stage<D>(src, 0, q_begin, bufs[0]);
   __syncthreads();
 
-  // Query tile j.  MASKED steps are the ones that straddle this item's keys
-  // (causal only): there a 32-row block entirely before a wave's keys is
-  // skipped and the block on the wave's diagonal (qbs == kw, everything is
-  // 32-aligned) is masked with the fixed triangle key > query.  All later
-  // tiles see every key of the item and run the branch-free body.
-  auto step = [&](int j, auto masked_tag, auto last_tag) {
+  // Query tile j in buffer P = j & 1 (a compile-time tag); the next tile goes
+  // into the other buffer.  MASKED steps are the ones that straddle this
+  // item's keys (causal only): there a 32-row block entirely before a wave's
+  // keys is skipped and the block on the wave's diagonal (qbs == kw,
+  // everything is 32-aligned) is masked with the fixed triangle key > query.
+  auto step = [&](int j, auto masked_tag, auto last_tag, auto parity) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     constexpr bool LAST = decltype(last_tag)::value;
-    const int buf = j & 1;
+    constexpr int P = decltype(parity)::value;
     const int q0 = q_begin + j * C::TILE;
-    if (!LAST) load_stage<D>(src, 0, q0 + C::TILE, stg);
+    if (!LAST) dma_stage<D>(src, 0, q0 + C::TILE, bufs[P ^ 1]);
 
-    const bool active = wave_valid && (!MASKED || q0 + C::TILE - 1 >= kw);
-    const uint16_t* Qs = smem[buf];
-    const uint16_t* dOs = Qs + C::TILE * C::RLD;
-    u32x4 pb[C::TB][2], sb[C::TB][2];
-    bool live[C::TB];
-    if (active) {
+    if (wave_valid && (!MASKED || q0 + C::TILE - 1 >= kw)) {
+      const uint16_t* Qs = bufs[P].t0;
+      const uint16_t* dOs = bufs[P].t1;
+      const float* sl = bufs[P].sl;
+      u32x4 pb[C::TB][2], sb[C::TB][2];
+      bool live[C::TB];
 #pragma unroll
       for (int qb = 0; qb < C::TB; ++qb) {
         const int qbs = q0 + 32 * qb;
         live[qb] = !MASKED || (qbs + 31 >= kw);
         if (!live[qb]) continue;
-        // dP starts at -delta (row = query), so the MFMAs leave dP - delta.
         f32x16 s = f32x16{}, dp;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const f32x4 d4 = *(const f32x4*)(&sl[buf][C::TILE + 32 * qb + 8 * jj + 4 * g]);
+          const f32x4 d4 = *(const f32x4*)(&sl[C::TILE + 32 * qb + 8 * jj + 4 * g]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) dp[4 * jj + i] = d4[i];
         }
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
-          const u32x4 qa = *(const u32x4*)(&Qs[(32 * qb + l32) * C::RLD + 16 * ks + 8 * g]);
+          const u32x4 qa = *(const u32x4*)(&Qs[32 * qb * D + rro[ks]]);
           s = E::mfma(qa, kf[ks], s);
         }
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
-          const u32x4 da = *(const u32x4*)(&dOs[(32 * qb + l32) * C::RLD + 16 * ks + 8 * g]);
-          dp = E::mfma(da, vf[ks], dp);
+          const u32x4 da = *(const u32x4*)(&dOs[32 * qb * D + rro[ks]]);
+          dp = E::mfma(da, vn[ks], dp);
         }
         const bool diag = MASKED && qbs == kw;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const f32x4 l4 = *(const f32x4*)(&sl[buf][32 * qb + 8 * jj + 4 * g]);
+          const f32x4 l4 = *(const f32x4*)(&sl[32 * qb + 8 * jj + 4 * g]);
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * jj + i;
-            float p = fast_exp2(__builtin_fmaf(s[r], c, -l4[i]));
+            float p = fast_exp2(__builtin_fmaf(s[r], c, l4[i] * -kLog2e));
             if (MASKED && diag && l32 > 8 * jj + 4 * g + i) p = 0.f;
             s[r] = p;
-            dp[r] = p * dp[r];
+            dp[r] = -(p * dp[r]);
           }
         }
 #pragma unroll
@@ -335,8 +347,6 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
             sb[qb][hh][w] = E::pack2(dp[8 * hh + 2 * w], dp[8 * hh + 2 * w + 1]);
           }
       }
-    }
-    if (active) {
 #pragma unroll
       for (int qb = 0; qb < C::TB; ++qb) {
         if (!live[qb]) continue;
@@ -344,28 +354,40 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
           for (int db = 0; db < C::DB; ++db) {
-            const int off = (32 * qb + 16 * hh) * C::RLD + 32 * db + tro;
-            dv[db] = E::mfma(tr_operand(&dOs[off], C::RLD), pb[qb][hh], dv[db]);
-            dk[db] = E::mfma(tr_operand(&Qs[off], C::RLD), sb[qb][hh], dk[db]);
+            const int off = (32 * qb + 16 * hh) * D + tro[db];
+            dv[db] = E::mfma(tr_operand(&dOs[off], D), pb[qb][hh], dv[db]);
+            dk[db] = E::mfma(tr_operand(&Qs[off], D), sb[qb][hh], dk[db]);
           }
         }
       }
     }
-
-    if (!LAST) store_stage<D>(stg, 0, smem[buf ^ 1], sl[buf ^ 1]);
     __syncthreads();
   };
 
-  // nq >= 1: the matrix-core path needs S % 64 == 0.
-  const int n_diag = CAUSAL ? min(nq, C::OWN / C::TILE) : 0;
+  // Steps [j, j_end) with the buffer parity fixed per call site.
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
   int j = 0;
-  if constexpr (CAUSAL)
-    for (; j < n_diag && j + 1 < nq; ++j) step(j, std::true_type{}, std::false_type{});
-  for (; j + 1 < nq; ++j) step(j, std::false_type{}, std::false_type{});
-  if (CAUSAL && j < n_diag)
-    step(j, std::true_type{}, std::true_type{});
-  else
-    step(j, std::false_type{}, std::true_type{});
+  auto run = [&](int j_end, auto masked_tag) __attribute__((always_inline)) {
+    if ((j & 1) && j < j_end) step(j++, masked_tag, std::false_type{}, P1{});
+    for (; j + 1 < j_end; j += 2) {
+      step(j, masked_tag, std::false_type{}, P0{});
+      step(j + 1, masked_tag, std::false_type{}, P1{});
+    }
+    if (j < j_end) step(j++, masked_tag, std::false_type{}, P0{});
+  };
+  // nq >= 1: the matrix-core path needs S % 64 == 0.
+  const int n_diag = CAUSAL ? min(nq - 1, C::OWN / C::TILE) : 0;
+  if constexpr (CAUSAL) run(n_diag, std::true_type{});
+  run(nq - 1, std::false_type{});
+  const bool last_masked = CAUSAL && nq - 1 < C::OWN / C::TILE;
+  if (last_masked) {
+    if (j & 1) step(j, std::true_type{}, std::true_type{}, P1{});
+    else step(j, std::true_type{}, std::true_type{}, P0{});
+  } else {
+    if (j & 1) step(j, std::false_type{}, std::true_type{}, P1{});
+    else step(j, std::false_type{}, std::true_type{}, P0{});
+  }
 
   if (!wave_valid) return;
   const int b = it.bh / a.H;
@@ -392,12 +414,11 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
 // dQ item.  Wave w owns queries [q0 + 32w, +32).  S^T = K Q^T and
 // dP^T = V dO^T put queries along the lane index, so lse and delta are
 // per-lane scalars and dS^T feeds dQ^T = K^T dS^T directly (K^T read
-// transposed from the row-major K tile).
+// transposed from the K tile).
 // ---------------------------------------------------------------------------
 template <typename E, int D, bool CAUSAL>
 __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
-                                        const Resident<D>& res, Staged& stg,
-                                        uint16_t (*smem)[BwdCfg<D>::BUF]) {
+                                        const Resident<D>& res, const BwdBuf (&bufs)[2]) {
   using C = BwdCfg<D>;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
@@ -409,41 +430,49 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   const int qw = q0 + 32 * wave;
   const bool wave_valid = qw < S;
   const int qrow = qw + l32;
-  const int tro = tr_lane_offset(lane, C::RLD);
   const u32x4(&qf)[C::KS] = res.r[0];
   const u32x4(&df)[C::KS] = res.r[1];
   const float lse2 = res.lse2;
   const float dl = res.dl;
 
+  int rro[C::KS], tro[C::DB];
+#pragma unroll
+  for (int ks = 0; ks < C::KS; ++ks) rro[ks] = l32 * D + (((2 * ks + g) ^ bwd_swz(l32)) << 3);
+#pragma unroll
+  for (int db = 0; db < C::DB; ++db) {
+    const int r = 4 * g + ((lane & 15) >> 2);
+    const int ch = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    tro[db] = r * D + ((ch ^ bwd_swz(r)) << 3) + 4 * (lane & 1);
+  }
+
   const int kv_end = CAUSAL ? min(q0 + C::OWN, S) : S;
   const int nkv = kv_end / C::TILE;
-  const StageSrc src = stage_src<D>(a, it);
+  const StageSrc<D> src = stage_src<D>(a, it);
 
   f32x16 acc[C::DB];
 #pragma unroll
   for (int i = 0; i < C::DB; ++i) acc[i] = f32x16{};
   const float c = a.scale_log2;
 
-  store_stage<D>(stg, 1, smem[0], nullptr);
+  dma_stage<D>(src, 1, 0, bufs[0]);
   __syncthreads();
 
-  // Key tile j.  MASKED steps are the causal ones that straddle this item's
-  // queries: a 32-key block after a wave's queries is skipped and the block on
-  // the wave's diagonal (kvb == qw) gets the fixed triangle mask.  Earlier
-  // tiles are visible to every query and run the branch-free body.
-  auto step = [&](int j, auto masked_tag, auto last_tag) {
+  // Key tile j in buffer P = j & 1.  MASKED steps are the causal ones that
+  // straddle this item's queries: a 32-key block after a wave's queries is
+  // skipped and the block on the wave's diagonal (kvb == qw) gets the fixed
+  // triangle mask.  Earlier tiles are visible to every query.
+  auto step = [&](int j, auto masked_tag, auto last_tag, auto parity) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     constexpr bool LAST = decltype(last_tag)::value;
-    const int buf = j & 1;
+    constexpr int P = decltype(parity)::value;
     const int kv0 = j * C::TILE;
-    if (!LAST) load_stage<D>(src, 1, kv0 + C::TILE, stg);
+    if (!LAST) dma_stage<D>(src, 1, kv0 + C::TILE, bufs[P ^ 1]);
 
-    const bool active = wave_valid && (!MASKED || kv0 <= qw + 31);
-    const uint16_t* Ks = smem[buf];
-    const uint16_t* Vs = Ks + C::TILE * C::RLD;
-    u32x4 sb[C::TB][2];
-    bool live[C::TB];
-    if (active) {
+    if (wave_valid && (!MASKED || kv0 <= qw + 31)) {
+      const uint16_t* Ks = bufs[P].t0;
+      const uint16_t* Vs = bufs[P].t1;
+      u32x4 sb[C::TB][2];
+      bool live[C::TB];
 #pragma unroll
       for (int kb = 0; kb < C::TB; ++kb) {
         const int kvb = kv0 + 32 * kb;
@@ -452,12 +481,12 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
         f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
-          const u32x4 ka = *(const u32x4*)(&Ks[(32 * kb + l32) * C::RLD + 16 * ks + 8 * g]);
+          const u32x4 ka = *(const u32x4*)(&Ks[32 * kb * D + rro[ks]]);
           s = E::mfma(ka, qf[ks], s);
         }
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
-          const u32x4 va = *(const u32x4*)(&Vs[(32 * kb + l32) * C::RLD + 16 * ks + 8 * g]);
+          const u32x4 va = *(const u32x4*)(&Vs[32 * kb * D + rro[ks]]);
           dp = E::mfma(va, df[ks], dp);
         }
         const bool diag = MASKED && kvb == qw;
@@ -473,8 +502,6 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
           for (int w = 0; w < 4; ++w)
             sb[kb][hh][w] = E::pack2(dp[8 * hh + 2 * w], dp[8 * hh + 2 * w + 1]);
       }
-    }
-    if (active) {
 #pragma unroll
       for (int kb = 0; kb < C::TB; ++kb) {
         if (!live[kb]) continue;
@@ -482,27 +509,38 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
           for (int db = 0; db < C::DB; ++db) {
-            const int off = (32 * kb + 16 * hh) * C::RLD + 32 * db + tro;
-            acc[db] = E::mfma(tr_operand(&Ks[off], C::RLD), sb[kb][hh], acc[db]);
+            const int off = (32 * kb + 16 * hh) * D + tro[db];
+            acc[db] = E::mfma(tr_operand(&Ks[off], D), sb[kb][hh], acc[db]);
           }
         }
       }
     }
-
-    if (!LAST) store_stage<D>(stg, 1, smem[buf ^ 1], nullptr);
     __syncthreads();
   };
 
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  int j = 0;
+  auto run = [&](int j_end, auto masked_tag) __attribute__((always_inline)) {
+    if ((j & 1) && j < j_end) step(j++, masked_tag, std::false_type{}, P1{});
+    for (; j + 1 < j_end; j += 2) {
+      step(j, masked_tag, std::false_type{}, P0{});
+      step(j + 1, masked_tag, std::false_type{}, P1{});
+    }
+    if (j < j_end) step(j++, masked_tag, std::false_type{}, P0{});
+  };
   // nkv >= 1: the matrix-core path needs S % 64 == 0.
   const int n_main = CAUSAL ? max(0, nkv - C::OWN / C::TILE) : nkv;
-  int j = 0;
-  for (; j < n_main && j + 1 < nkv; ++j) step(j, std::false_type{}, std::false_type{});
-  if constexpr (CAUSAL)
-    for (; j + 1 < nkv; ++j) step(j, std::true_type{}, std::false_type{});
-  if (!CAUSAL || j < n_main)
-    step(j, std::false_type{}, std::true_type{});
-  else
-    step(j, std::true_type{}, std::true_type{});
+  run(min(n_main, nkv - 1), std::false_type{});
+  if constexpr (CAUSAL) run(nkv - 1, std::true_type{});
+  const bool last_masked = CAUSAL && nkv - 1 >= n_main;
+  if (last_masked) {
+    if (j & 1) step(j, std::true_type{}, std::true_type{}, P1{});
+    else step(j, std::true_type{}, std::true_type{}, P0{});
+  } else {
+    if (j & 1) step(j, std::false_type{}, std::true_type{}, P1{});
+    else step(j, std::false_type{}, std::true_type{}, P0{});
+  }
 
   if (!wave_valid) return;
   const int b = it.bh / a.H;
@@ -521,32 +559,36 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   }
 }
 
-// One item per workgroup.
+// One item per workgroup.  One LDS array per buffer and tensor, so that the
+// compiler can see that a direct load into one buffer never aliases the
+// reads of the other.
 template <typename E, int D, bool CAUSAL>
 __device__ __forceinline__ void run_item(const AttnArgs& a, const BwdItem it) {
   using C = BwdCfg<D>;
-  __shared__ __attribute__((aligned(16))) unsigned char lds[C::LDS_BYTES];
-  auto smem = (uint16_t(*)[C::BUF])lds;
-  auto sl = (float(*)[2 * C::TILE])(lds + 2 * C::BUF * 2);
+  __shared__ __attribute__((aligned(16))) uint16_t A0[C::ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t A1[C::ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t B0[C::ELEMS];
+  __shared__ __attribute__((aligned(16))) uint16_t B1[C::ELEMS];
+  __shared__ __attribute__((aligned(16))) float SA[2 * C::TILE];
+  __shared__ __attribute__((aligned(16))) float SB[2 * C::TILE];
+  const BwdBuf bufs[2] = {{A0, A1, SA}, {B0, B1, SB}};
   Resident<D> res;
-  Staged stg;
   load_resident<D>(a, it, res);
-  load_stage<D>(stage_src<D>(a, it), it.kind, first_row<D, CAUSAL>(it), stg);
   if (it.kind)
-    dq_item<E, D, CAUSAL>(a, it, res, stg, smem);
+    dq_item<E, D, CAUSAL>(a, it, res, bufs);
   else
-    dkdv_item<E, D, CAUSAL>(a, it, res, stg, smem, sl);
+    dkdv_item<E, D, CAUSAL>(a, it, res, bufs);
 }
 
 template <typename E, int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_bwd_dkdv_kernel(AttnArgs a) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(AttnArgs a) {
   // key tile 0 sees the most query tiles: dispatched first
   const int BH = a.B * a.H;
   run_item<E, D, CAUSAL>(a, BwdItem{0, (int)(blockIdx.x / BH), (int)(blockIdx.x % BH)});
 }
 
 template <typename E, int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a, int n_qtiles) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a, int n_qtiles) {
   const int BH = a.B * a.H;
   run_item<E, D, CAUSAL>(
       a, BwdItem{1, n_qtiles - 1 - (int)(blockIdx.x / BH), (int)(blockIdx.x % BH)});
@@ -558,7 +600,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(AttnArgs a, int n_qtil
 // masking), so the short tails of both kinds overlap the long heads of the
 // other and the launch keeps the whole chip busy.
 template <typename E, int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_bwd_kernel(AttnArgs a, int n_tiles) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_kernel(AttnArgs a, int n_tiles) {
   const int BH = a.B * a.H;
   const int rank = blockIdx.x / BH;
   const int kind = rank & 1;

@@ -217,6 +217,13 @@ __device__ __forceinline__ void buffer_load_lds16(__amdgpu_buffer_rsrc_t rs, uin
                                            voffset, 0, 0, 0);
 }
 
+// The same with 4 bytes per lane (lane i's word lands at lds + 4*i bytes).
+__device__ __forceinline__ void buffer_load_lds4(__amdgpu_buffer_rsrc_t rs, uint32_t voffset,
+                                                 float* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(lds), 4,
+                                           voffset, 0, 0, 0);
+}
+
 __device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t* p) {
   typedef __attribute__((ext_vector_type(4))) short s16x4;
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
