@@ -186,20 +186,27 @@ def main():
         step()
     torch.cuda.synchronize()
 
-    # Timed region: exactly K steps between two events on the launch stream,
-    # with events around every launch for the per-kernel durations.
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(calls) + 1)]
-           for _ in range(args.steps)]
+    # Timed region: exactly K steps between two events on the launch stream
+    # and nothing else in the stream.
     t_start = torch.cuda.Event(enable_timing=True)
     t_end = torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t_start.record(stream)
-    for s in range(args.steps):
-        step(evs[s])
+    for _ in range(args.steps):
+        step()
     t_end.record(stream)
     torch.cuda.synchronize()
     ms_per_step = t_start.elapsed_time(t_end) / args.steps
 
+    # Second timed pass of K steps with an event before every launch, for the
+    # per-kernel durations (each interval also holds the launch gap before the
+    # next kernel; the events themselves are kept out of the first pass).
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(calls) + 1)]
+           for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    for s in range(args.steps):
+        step(evs[s])
+    torch.cuda.synchronize()
     per_kernel_us = {}
     for i, (name, _, _) in enumerate(calls):
         per_kernel_us[name] = statistics.mean(e[i].elapsed_time(e[i + 1]) for e in evs) * 1e3
