@@ -9,10 +9,11 @@ through the C ABI (include/mi_attn.h) with pre-built argument lists so the
 host keeps the GPU queue full.
 
 Printed: ONE JSON line with the metric of BASELINE.json (algorithmic TFLOP/s of
-fwd+bwd, causal counted as half of dense: 7*B*H*S^2*D flops per step), the
-per-kernel durations from HIP events recorded around every launch in the
-timed region, the roofline of the dominant kernel, the RoPE bandwidth, and
-the CPU baseline (the oracle's fp32 eager attention on the host cores).
+fwd+bwd, causal counted as half of dense: 7*B*H*S^2*D flops per step) from a
+timed pass of K steps with events only at its ends, the per-kernel durations
+from a second timed pass of K steps with an event before every launch, the
+roofline of the dominant kernel, the RoPE bandwidth, and the CPU baseline (the
+oracle's fp32 eager attention on the host cores).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -226,15 +227,21 @@ def main():
                 "algorithmic_flop_per_launch": kflops[dom], "traffic": read_traffic(dom)}
 
     # RoPE (q and k in one launch, the model's strided layout) — HBM-bound.
+    # Called through the C ABI with a pre-built argument list, like the
+    # attention calls, so that the timed loop is not bound by Python.
     rq, rk = torch.empty_like(qr), torch.empty_like(kr)
+    ST2 = lambda t: (ctypes.c_int64 * 2)(*t.stride())
+    rope_args = (_lib.dtype_code(q), _lib.dtype_code(cos), S, B, H, D, 0, P(q), ST(q), P(k),
+                 ST(k), P(cos), ST2(cos), P(sin), ST2(sin), P(rq), ST(rq), P(rk), ST(rk), sp)
     for _ in range(10):
-        _lib.rope_qk(q, k, cos, sin, rq, rk, inverse=False)
+        if lib.mi_rope_qk(*rope_args) != 0:
+            raise RuntimeError(f"rope_qk: {lib.mi_last_error().decode()}")
     torch.cuda.synchronize()
     r0, r1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     n_rope = 200
     r0.record(stream)
     for _ in range(n_rope):
-        _lib.rope_qk(q, k, cos, sin, rq, rk, inverse=False)
+        lib.mi_rope_qk(*rope_args)
     r1.record(stream)
     torch.cuda.synchronize()
     rope_us = r0.elapsed_time(r1) / n_rope * 1e3

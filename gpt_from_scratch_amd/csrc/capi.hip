@@ -329,7 +329,13 @@ static mi_status rope_common(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B,
   a.inverse = inverse ? 1 : 0;
   const int esz = elem_size(x_dtype);
   const int vecn = 16 / esz;
-  bool vec = (D % vecn == 0) && a.cs_i == 1 && a.ss_i == 1;
+  // the vector path also reads vecn/2 consecutive angles of a table row with
+  // one aligned load
+  const int np = vecn / 2;
+  const int abytes = np * elem_size(tab_dtype);
+  bool vec = (D % vecn == 0) && a.cs_i == 1 && a.ss_i == 1 && a.cs_s % np == 0 &&
+             a.ss_s % np == 0 && ((uintptr_t)cos_tab) % abytes == 0 &&
+             ((uintptr_t)sin_tab) % abytes == 0;
   for (int t = 0; t < nt; ++t) {
     if (!ins[t] || !outs[t] || !in_st[t] || !out_st[t])
       return fail(MI_ERR_INVALID_ARGUMENT, "rope tensor %d: null pointer", t);
