@@ -89,6 +89,42 @@ def test_odd_layouts(gpu, dtype):
     assert float(((y.cpu().float() - ref).abs() - ref.abs() * tol).max()) <= 1e-5
 
 
+def test_table_layouts_vector_x(gpu):
+    """x that qualifies for the 16-byte vector path with angle tables that do and do not:
+    contiguous tables, tables whose rows are padded to an odd stride, and tables whose base
+    is not aligned to the angle vector (the last two take the pair path).  All three compute
+    the same fp32 rotation with one rounding, so they must agree bit for bit, and match the
+    oracle to one bf16 rounding."""
+    from gpt_from_scratch_amd import apply_rope_qk
+    S, B, H, D = 64, 2, 3, 64
+    qkv = seeded((S, B, 3, H, D), 21, dtype=torch.bfloat16).to(gpu)
+    q, k, _ = qkv.unbind(2)
+    cos, sin = (t.to(torch.bfloat16).to(gpu) for t in rope_tables(D, S))
+    variants = {"contiguous": (cos, sin)}
+    padded = []
+    for t in (cos, sin):
+        buf = torch.zeros(S, D // 2 + 1, dtype=torch.bfloat16, device=gpu)
+        buf[:, : D // 2] = t
+        padded.append(buf[:, : D // 2])
+    variants["padded rows"] = tuple(padded)
+    shifted = []
+    for t in (cos, sin):
+        buf = torch.zeros(S * (D // 2) + 1, dtype=torch.bfloat16, device=gpu)
+        buf[1:] = t.reshape(-1)
+        shifted.append(buf[1:].view(S, D // 2))
+    variants["unaligned base"] = tuple(shifted)
+    assert variants["padded rows"][0].stride(0) == D // 2 + 1
+    assert variants["unaligned base"][0].data_ptr() % 8 != 0
+
+    outs = {name: apply_rope_qk(q, k, c, s) for name, (c, s) in variants.items()}
+    for name in ("padded rows", "unaligned base"):
+        for got, want in zip(outs[name], outs["contiguous"]):
+            assert torch.equal(got, want), name
+    for got, x in zip(outs["contiguous"], (q, k)):
+        assert _bf16_ulp_ok(got, rope_apply(x.cpu(), cos.cpu().float(), sin.cpu().float(),
+                                            dtype=torch.float32))
+
+
 def test_long_sequence_invariants(gpu):
     """C4 shape: inverse(forward(x)) == x to rounding, per-pair norms preserved."""
     from gpt_from_scratch_amd import apply_rope
