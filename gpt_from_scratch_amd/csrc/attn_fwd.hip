@@ -14,14 +14,15 @@
 //     statistics are per-lane scalars (one v_permlane32_swap for the max) and
 //     the probabilities feed the P V product as a B operand without any
 //     register shuffle;
-//   * K/V tiles of BKV = 64 keys are staged row-major through LDS; the K
-//     operand is a contiguous 16-byte read, the V^T operand of P V comes from
-//     the same row-major V tile through the transposing LDS read
-//     (ds_read_b64_tr_b16);
-//   * software pipeline: while the VALU runs the softmax of tile j, the matrix
-//     cores already compute S for tile j+1, then P V for tile j.  K is staged
-//     two tiles ahead and V one tile ahead (double buffers for each), so one
-//     barrier per tile suffices;
+//   * K/V tiles of BKV = 64 keys are staged row-major through LDS by direct
+//     global->LDS loads; the K operand is a contiguous 16-byte read, the V^T
+//     operand of P V comes from the same row-major V tile through the
+//     transposing LDS read (ds_read_b64_tr_b16);
+//   * one tile per step (S, softmax, P V) with double buffers: the loads of
+//     tile j+1 run under step j, one barrier per step.  Only one S tile is live,
+//     so D = 64 fits 128 VGPRs and four waves per SIMD (three workgroups per CU
+//     at once), which hides the step's latency better than pipelining S_{j+1}
+//     under softmax_j inside a wave at half the occupancy;
 //   * key tiles below the diagonal run a branch-free body; the diagonal tiles
 //     run a masked body that also skips tiles a wave cannot see;
 //   * the running max is only moved (and O, l rescaled) when a new score
@@ -32,7 +33,9 @@
 //     sequence (which see the most keys under causal masking) are dispatched
 //     first, and all tiles of one head land on the same XCD (workgroups go
 //     round-robin over the 8 XCDs and the index stride between tiles of one
-//     head is B*H).
+//     head is B*H).  Workgroups w and w + #CU share a CU, so every odd round
+//     of #CU workgroups is taken in reverse (XCD kept): a CU's co-resident
+//     tiles pair heavy with light.
 #include <type_traits>
 
 #include "mi_device.h"
@@ -53,10 +56,8 @@ struct FwdCfg {
   static constexpr int CPR = D / 8;                  // 16-byte chunks per row
   static constexpr int RPS = 64 / CPR;               // rows per 1 KB slice (one wave instruction)
   static constexpr int SPW = TILE * 2 / 1024 / 4;    // slices per wave per tile
-  // LDS buffers per tensor.  Steps run in phases of NBUF/2 tiles with one
-  // barrier per phase; D = 128 tiles are twice as large, so two buffers.
-  static constexpr int NBUF = (D == 64) ? 4 : 2;
-  static constexpr int L = NBUF / 2;  // tiles per phase
+  // Waves per SIMD the register budget is held to: D = 64 fits 128 VGPRs.
+  static constexpr int WAVES_PER_EU = D == 64 ? 4 : 2;
 };
 
 // LDS layout of a staged tile: BKV rows of D elements, no padding; the
@@ -73,33 +74,14 @@ __device__ __forceinline__ int swz_v(int r) { return (r & 3) << 1; }
 constexpr float kRescaleSlack = 8.f;  // log2 units: probabilities stay <= 2^8
 
 template <typename E, int D, bool CAUSAL>
-__global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qtiles) {
+__global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_kernel(AttnArgs a, int n_qtiles, int n_cu) {
   using C = FwdCfg<D>;
   // One array per buffer, so that the compiler can see that a direct load
   // into one buffer never aliases the reads of another.
-  constexpr int T23 = C::NBUF == 4 ? C::TILE : 8;
   __shared__ __attribute__((aligned(16))) uint16_t K0[C::TILE];
   __shared__ __attribute__((aligned(16))) uint16_t K1[C::TILE];
-  __shared__ __attribute__((aligned(16))) uint16_t K2[T23];
-  __shared__ __attribute__((aligned(16))) uint16_t K3[T23];
   __shared__ __attribute__((aligned(16))) uint16_t V0[C::TILE];
   __shared__ __attribute__((aligned(16))) uint16_t V1[C::TILE];
-  __shared__ __attribute__((aligned(16))) uint16_t V2[T23];
-  __shared__ __attribute__((aligned(16))) uint16_t V3[T23];
-  auto kbuf = [&](auto i) __attribute__((always_inline)) -> uint16_t* {
-    constexpr int I = decltype(i)::value;
-    if constexpr (I == 0) return K0;
-    else if constexpr (I == 1) return K1;
-    else if constexpr (I == 2) return K2;
-    else return K3;
-  };
-  auto vbuf = [&](auto i) __attribute__((always_inline)) -> uint16_t* {
-    constexpr int I = decltype(i)::value;
-    if constexpr (I == 0) return V0;
-    else if constexpr (I == 1) return V1;
-    else if constexpr (I == 2) return V2;
-    else return V3;
-  };
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -108,7 +90,14 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
   const int g = lane >> 5;
 
   const int BH = a.B * a.H;
-  const int bid = blockIdx.x;
+  int bid = blockIdx.x;
+  {
+    // Heaviest query tiles first; odd rounds of #CU workgroups reversed
+    // (within each XCD), so a CU's co-resident tiles pair heavy with light.
+    const int R = bid / n_cu, c = bid % n_cu;
+    const int cnt = min(n_cu, (int)gridDim.x - R * n_cu);
+    if ((R & 1) && cnt % 8 == 0) bid = R * n_cu + 8 * (cnt / 8 - 1 - c / 8) + (c & 7);
+  }
   const int qt = n_qtiles - 1 - bid / BH;
   const int bh = bid % BH;
   const int b = bh / a.H;
@@ -133,13 +122,14 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
 
   const int kv_end = CAUSAL ? min(q0 + C::BQ, S) : S;
   const int nkv = kv_end / C::BKV;
+  const int jdiag = CAUSAL ? q0 / C::BKV : nkv;   // first tile that may need a mask
 
   // ---- staging: direct global -> LDS loads ----
-  // A tile is 1 KB slices; wave w fills slices w, w + 4, ...  Lane i of slice
-  // s writes the 16 bytes at row s*RPS + i/CPR, chunk position i%CPR, so it
-  // fetches chunk (i%CPR) ^ swz(row) of that row.  One buffer descriptor per
-  // tile, fixed per-lane byte offsets; completion is tracked by vmcnt and the
-  // barrier that ends each step.
+  // A tile is 1 KB slices; wave w fills slices w, w + 4, ...
+  // Lane i of slice s writes the 16 bytes at row s*RPS + i/CPR, chunk position
+  // i%CPR, so it fetches chunk (i%CPR) ^ swz(row) of that row.  One buffer
+  // descriptor per tile, fixed per-lane byte offsets; completion is tracked by
+  // vmcnt and the barrier that ends each step.
   uint32_t kdo[C::SPW], vdo[C::SPW];
 #pragma unroll
   for (int m = 0; m < C::SPW; ++m) {
@@ -244,176 +234,46 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
                             acc[db]);
   };
 
-  // Mask-free tile with the matrix-core work woven into the softmax.  The 32
-  // scores per lane form 4 groups of 8 (one B operand of P V each).  Group g
-  // issues 1/4 of the next tile's K Q^T MFMAs, turns its 8 scores into
-  // probabilities, and issues the P V MFMAs of group g-1, so that every MFMA
-  // has ~7 VALU instructions behind it to overlap with.  sched_barrier keeps
-  // the compiler from clustering the MFMAs back together.
-  auto hot = [&](const uint16_t* kt, const uint16_t* vt, f32x16(&s)[2], f32x16(&sn)[2]) __attribute__((always_inline)) {
-    constexpr int KPG = C::KS / 4;  // k-steps of the next tile's S per group
-    // K fragments of group g+1 are read while group g computes.
-    u32x4 kf[2][KPG][2];
-    auto read_k = [&](int grp, u32x4(&dst)[KPG][2]) __attribute__((always_inline)) {
-#pragma unroll
-      for (int kk = 0; kk < KPG; ++kk)
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-          dst[kk][nb] = *(const u32x4*)(&kt[32 * nb * D + kro[KPG * grp + kk]]);
-    };
-    read_k(0, kf[0]);
-
-    float mx = vmax(s[0][0], s[0][1]);
-#pragma unroll
-    for (int i = 2; i < 32; i += 2) mx = vmax(vmax(mx, s[i >> 4][i & 15]), s[i >> 4][(i & 15) + 1]);
-    mx = max_halves(mx) * c;
-    if (__any(mx > m_run + kRescaleSlack)) {
-      const float m_new = fmaxf(m_run, mx);
-      const float alpha = fast_exp2(m_run - m_new);
-      m_run = m_new;
-      l_run *= alpha;
-#pragma unroll
-      for (int db = 0; db < C::DB; ++db) acc[db] *= alpha;
-    }
-    const float mref = m_run;
-    float psum = 0.f;
-    u32x4 pb[4];
-    auto pv_group = [&](int grp) __attribute__((always_inline)) {
-      const int kb = grp >> 1, hh = grp & 1;
-#pragma unroll
-      for (int db = 0; db < C::DB; ++db)
-        acc[db] = E::mfma(tr_operand(&vt[(32 * kb + 16 * hh) * D + vro[db]], D), pb[grp],
-                          acc[db]);
-    };
-#pragma unroll
-    for (int grp = 0; grp < 4; ++grp) {
-      __builtin_amdgcn_sched_barrier(0);
-      const int kb = grp >> 1, hh = grp & 1;
-      if (grp < 3) read_k(grp + 1, kf[(grp + 1) & 1]);
-#pragma unroll
-      for (int kk = 0; kk < KPG; ++kk) {
-        const int ks = KPG * grp + kk;
-#pragma unroll
-        for (int nb = 0; nb < 2; ++nb)
-          sn[nb] = E::mfma(kf[grp & 1][kk][nb], qf[ks], ks == 0 ? f32x16{} : sn[nb]);
-      }
-      float p[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        p[i] = fast_exp2(__builtin_fmaf(s[kb][8 * hh + i], c, -mref));
-        psum += p[i];
-      }
-#pragma unroll
-      for (int w = 0; w < 4; ++w) pb[grp][w] = E::pack2(p[2 * w], p[2 * w + 1]);
-      if (grp > 0) pv_group(grp - 1);
-      // 2*KPG + DB MFMAs against ~28 VALU ops: one MFMA, then a run of VALU.
-#pragma unroll
-      for (int m = 0; m < 2 * KPG + (grp > 0 ? C::DB : 0); ++m) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    pv_group(3);
-    l_run += psum;
-  };
-
-  // ---- prologue: K_0..K_L and V_0..V_{L-1} into LDS; S for tile 0 ----
-  using I0_ = std::integral_constant<int, 0>;
-  using I1_ = std::integral_constant<int, 1>;
-  using I2_ = std::integral_constant<int, 2>;
+  // ---- steps over key tiles [0, nkv) ----
+  // Step j works on tile j from buffer j & 1 while the direct loads of tile
+  // j + 1 fill the other buffer; the barrier that ends step j also ends those
+  // loads (vmcnt) and every read of buffer j & 1.
   dma(kp, a.k.ss, kdo, 0, K0);
   dma(vp, a.v.ss, vdo, 0, V0);
-  if (nkv > 1) dma(kp, a.k.ss, kdo, 1, K1);
-  if constexpr (C::L == 2) {
-    if (nkv > 1) dma(vp, a.v.ss, vdo, 1, V1);
-    if (nkv > 2) dma(kp, a.k.ss, kdo, 2, K2);
-  }
   __syncthreads();
-
-  f32x16 sA[2], sB[2];
-  if (wave_valid) qk(K0, sA);
-  // The first phase loads a tile into K0: every wave must be done reading it.
-  __syncthreads();
-
-  // Tile j in buffer slot I = j % NBUF (a compile-time tag): S_{j+1} from K
-  // slot I+1 runs on the matrix cores while the VALU turns S_j into P_j; then
-  // O += P_j V_j from V slot I.
-  auto step = [&](int j, f32x16(&scur)[2], f32x16(&snext)[2], auto masked_tag, auto slot) __attribute__((always_inline)) {
+  auto step = [&](int j, auto masked_tag, auto slot) __attribute__((always_inline)) {
     constexpr bool MASKED = decltype(masked_tag)::value;
     constexpr int I = decltype(slot)::value;
-    const uint16_t* const knext = kbuf(std::integral_constant<int, (I + 1) % C::NBUF>{});
-    const uint16_t* const vcur = vbuf(std::integral_constant<int, I>{});
-    const int kv0 = j * C::BKV;
-    u32x4 pb[2][2];
-    if (!MASKED) {
-      hot(knext, vcur, scur, snext);
-    } else if (wave_valid) {
-      if (j + 1 < nkv && (!CAUSAL || (j + 1) * C::BKV <= qw + 31)) qk(knext, snext);
-      if (!CAUSAL || kv0 <= qw + 31) {
-        softmax(scur, pb, kv0, CAUSAL && kv0 + C::BKV - 1 > qw);
-        pv(vcur, pb);
-      }
+    const uint16_t* kt = I ? K1 : K0;
+    const uint16_t* vt = I ? V1 : V0;
+    if (j + 1 < nkv) {
+      dma(kp, a.k.ss, kdo, j + 1, I ? K0 : K1);
+      dma(vp, a.v.ss, vdo, j + 1, I ? V0 : V1);
     }
-  };
-  // Phase starting at tile j (slot I0 = j % NBUF): loads K_{j+L+1..j+2L} and
-  // V_{j+L..j+2L-1} into the slots the previous phase finished reading, runs
-  // its L tiles and ends with the one barrier, by which the loads have landed.
-  auto phase = [&](int j, auto masked_tag, auto slot0) __attribute__((always_inline)) {
-    constexpr int I0 = decltype(slot0)::value;
-    if (j + C::L + 1 < nkv)
-      dma(kp, a.k.ss, kdo, j + C::L + 1, kbuf(std::integral_constant<int, (I0 + C::L + 1) % C::NBUF>{}));
-    if (j + C::L < nkv)
-      dma(vp, a.v.ss, vdo, j + C::L, vbuf(std::integral_constant<int, (I0 + C::L) % C::NBUF>{}));
-    if constexpr (C::L == 2) {
-      if (j + 4 < nkv) dma(kp, a.k.ss, kdo, j + 4, kbuf(std::integral_constant<int, I0>{}));
-      if (j + 3 < nkv) dma(vp, a.v.ss, vdo, j + 3, vbuf(std::integral_constant<int, (I0 + 3) % 4>{}));
-      step(j, sA, sB, masked_tag, std::integral_constant<int, I0>{});
-      if (j + 1 < nkv) step(j + 1, sB, sA, masked_tag, std::integral_constant<int, I0 + 1>{});
-    } else {
-      // one tile per phase: scur alternates with the slot
-      if constexpr (I0 == 0)
-        step(j, sA, sB, masked_tag, I0_{});
-      else
-        step(j, sB, sA, masked_tag, I1_{});
+    const int kv0 = j * C::BKV;
+    if (wave_valid && (!MASKED || !CAUSAL || kv0 <= qw + 31)) {
+      f32x16 s[2];
+      qk(kt, s);
+      u32x4 pb[2][2];
+      softmax(s, pb, kv0, MASKED && CAUSAL && kv0 + C::BKV - 1 > qw);
+      pv(vt, pb);
     }
     __syncthreads();
   };
-
-  // Branch-free body: tile j lies below the diagonal for every wave of the
-  // workgroup and tile j+1 exists and is visible to every wave.  Phases hold
-  // two tiles each (an even count keeps S_j in sA for even j).
-  const int n_main =
-      (wave_valid ? (CAUSAL ? min(q0 / C::BKV, nkv - 1) : nkv - 1) : 0) & ~1;
+  using I0_ = std::integral_constant<int, 0>;
+  using I1_ = std::integral_constant<int, 1>;
+  // Branch-free pairs below the diagonal, then masked steps.
+  const int n_main = wave_valid ? (min(jdiag, nkv) & ~1) : 0;
   int j = 0;
-  auto run = [&](int j_end, auto masked_tag) __attribute__((always_inline)) {
-    // phases over [j, j_end) with j even; slot pattern repeats every NBUF tiles
-    if constexpr (C::L == 2) {
-      if ((j & 3) == 2 && j < j_end) {
-        phase(j, masked_tag, I2_{});
-        j += 2;
-      }
-      for (; j + 2 < j_end; j += 4) {
-        phase(j, masked_tag, I0_{});
-        phase(j + 2, masked_tag, I2_{});
-      }
-      if (j < j_end) {
-        phase(j, masked_tag, I0_{});
-        j += 2;
-      }
-    } else {
-      for (; j + 1 < j_end; j += 2) {
-        phase(j, masked_tag, I0_{});
-        phase(j + 1, masked_tag, I1_{});
-      }
-      if (j < j_end) {
-        phase(j, masked_tag, I0_{});
-        ++j;
-      }
-    }
-  };
-  run(n_main, std::false_type{});
-  run(nkv, std::true_type{});
+  for (; j < n_main; j += 2) {
+    step(j, std::false_type{}, I0_{});
+    step(j + 1, std::false_type{}, I1_{});
+  }
+  for (; j + 1 < nkv; j += 2) {
+    step(j, std::true_type{}, I0_{});
+    step(j + 1, std::true_type{}, I1_{});
+  }
+  if (j < nkv) step(j, std::true_type{}, I0_{});
 
   if (!wave_valid) return;
   const float l_tot = sum_halves(l_run);
@@ -432,14 +292,30 @@ __global__ __launch_bounds__(256) void attn_fwd_mfma_kernel(AttnArgs a, int n_qt
   if (g == 0) a.lse[(int64_t)bh * S + qrow] = (m_run + fast_log2(l_tot)) * kLn2;
 }
 
+// Compute units of the current device (cached), the size of one dispatch
+// round of the grid ordering; 0 when unknown or not a multiple of the 8 XCDs.
+int cu_count() {
+  static int cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    cache[dev] = (n > 0 && n % 8 == 0) ? n : -1;
+  }
+  return cache[dev] > 0 ? cache[dev] : 0;
+}
+
 template <typename E, int D>
 hipError_t launch_fwd_d(const AttnArgs& a, hipStream_t st) {
   const int n_qtiles = (a.S + FwdCfg<D>::BQ - 1) / FwdCfg<D>::BQ;
+  int n_cu = cu_count();
+  if (n_cu == 0) n_cu = 1 << 30;  // one round: no reversal
   dim3 grid(n_qtiles * a.B * a.H), block(FwdCfg<D>::NT);
   if (a.causal)
-    hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, true>), grid, block, 0, st, a, n_qtiles);
+    hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, true>), grid, block, 0, st, a, n_qtiles, n_cu);
   else
-    hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, false>), grid, block, 0, st, a, n_qtiles);
+    hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, false>), grid, block, 0, st, a, n_qtiles, n_cu);
   return hipGetLastError();
 }
 
