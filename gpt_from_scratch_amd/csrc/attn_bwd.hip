@@ -89,6 +89,7 @@ struct BwdCfg {
   static constexpr int RPS = 64 / CPR;             // rows per 1 KB slice (one wave instruction)
   static constexpr int SPW = ELEMS * 2 / 1024 / 4; // slices per wave per tile
   static_assert(SPW >= 1 && TILE <= 64, "tile layout");
+  static_assert(ELEMS >= 32 * D, "a tile buffer stages one wave's 32 output rows");
 };
 
 // LDS layout of a streamed tile: TILE rows of D elements, no padding; the
@@ -119,6 +120,15 @@ struct BwdBuf {
   uint16_t* t1;
   float* sl;
 };
+
+// Tile buffer w of the four (ELEMS elements each, at least 32*D): the output
+// staging area of wave w once the steps are over.
+__device__ __forceinline__ uint16_t* wave_stage_buf(const BwdBuf (&bufs)[2], int wave) {
+  // selects, not an index: a runtime index would put `bufs` in scratch memory
+  uint16_t* const b0 = (wave & 1) ? bufs[0].t1 : bufs[0].t0;
+  uint16_t* const b1 = (wave & 1) ? bufs[1].t1 : bufs[1].t0;
+  return (wave & 2) ? b1 : b0;
+}
 
 // Where an item's streamed tiles come from: head bases and strides, and this
 // lane's byte offsets inside a tile for its slices (buffer loads, so that
@@ -244,7 +254,7 @@ __device__ __forceinline__ void dma_stage(const StageSrc<D>& s, int kind, int ro
 // ---------------------------------------------------------------------------
 template <typename E, int D, bool CAUSAL>
 __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
-                                          const Resident<D>& res, const BwdBuf (&bufs)[2]) {
+                                          const BwdBuf (&bufs)[2]) {
   using C = BwdCfg<D>;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
@@ -255,9 +265,6 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
   const int kv0 = it.tile * C::OWN;
   const int kw = kv0 + 32 * wave;
   const bool wave_valid = kw < S;
-  const int krow = kw + l32;
-  const u32x4(&kf)[C::KS] = res.r[0];
-  const u32x4(&vn)[C::KS] = res.r[1];  // -V
 
   // per-lane LDS offsets: 16-byte row reads (row l32, chunk 2ks + g) and
   // transposing reads (row 4g + (lane%16)/4, column 32db + 16((lane/16)%2) + 4(lane%4))
@@ -283,7 +290,13 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
   }
   const float c = a.scale_log2;
 
+  // First tile's loads before the resident rows: one memory round trip for
+  // both (the V negation waits for its rows, not for the tile).
   dma_stage<D>(src, 0, q_begin, bufs[0]);
+  Resident<D> res;
+  load_resident<D>(a, it, res);
+  const u32x4(&kf)[C::KS] = res.r[0];
+  const u32x4(&vn)[C::KS] = res.r[1];  // -V
   __syncthreads();
 
   // Query tile j in buffer P = j & 1 (a compile-time tag); the next tile goes
@@ -392,21 +405,30 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
   if (!wave_valid) return;
   const int b = it.bh / a.H;
   const int h = it.bh % a.H;
-  uint16_t* dkrow = (uint16_t*)a.dk.ptr + b * a.dk.sb + h * a.dk.sh + (int64_t)krow * a.dk.ss;
-  uint16_t* dvrow = (uint16_t*)a.dv.ptr + b * a.dv.sb + h * a.dv.sh + (int64_t)krow * a.dv.ss;
-  const float sc = a.scale;
+  uint16_t* const dk_rows = (uint16_t*)a.dk.ptr + b * a.dk.sb + h * a.dk.sh + (int64_t)kw * a.dk.ss;
+  uint16_t* const dv_rows = (uint16_t*)a.dv.ptr + b * a.dv.sb + h * a.dv.sh + (int64_t)kw * a.dv.ss;
+  if constexpr (D == 64) {
+    // The staging buffers are idle after the last step's barrier: wave w
+    // stages its rows (dK, then dV) through tile buffer w.
+    uint16_t* stage = wave_stage_buf(bufs, wave);
+    store_block_rows<E, D>(dk, a.scale, stage, dk_rows, a.dk.ss);
+    store_block_rows<E, D>(dv, 1.f, stage, dv_rows, a.dv.ss);
+  } else {
+    // D = 128 runs at the register limit; the staged store measured slower
+    // there, so the accumulators go out directly (8 bytes per lane and row).
+    const int l32 = lane & 31;
 #pragma unroll
-  for (int db = 0; db < C::DB; ++db) {
+    for (int db = 0; db < C::DB; ++db)
 #pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      u32x2 wk, wv;
-      wk[0] = E::pack2(dk[db][4 * jj + 0] * sc, dk[db][4 * jj + 1] * sc);
-      wk[1] = E::pack2(dk[db][4 * jj + 2] * sc, dk[db][4 * jj + 3] * sc);
-      wv[0] = E::pack2(dv[db][4 * jj + 0], dv[db][4 * jj + 1]);
-      wv[1] = E::pack2(dv[db][4 * jj + 2], dv[db][4 * jj + 3]);
-      *(u32x2*)(dkrow + 32 * db + 8 * jj + 4 * g) = wk;
-      *(u32x2*)(dvrow + 32 * db + 8 * jj + 4 * g) = wv;
-    }
+      for (int jj = 0; jj < 4; ++jj) {
+        u32x2 wk, wv;
+        wk[0] = E::pack2(dk[db][4 * jj + 0] * a.scale, dk[db][4 * jj + 1] * a.scale);
+        wk[1] = E::pack2(dk[db][4 * jj + 2] * a.scale, dk[db][4 * jj + 3] * a.scale);
+        wv[0] = E::pack2(dv[db][4 * jj + 0], dv[db][4 * jj + 1]);
+        wv[1] = E::pack2(dv[db][4 * jj + 2], dv[db][4 * jj + 3]);
+        *(u32x2*)(dk_rows + (int64_t)l32 * a.dk.ss + 32 * db + 8 * jj + 4 * g) = wk;
+        *(u32x2*)(dv_rows + (int64_t)l32 * a.dv.ss + 32 * db + 8 * jj + 4 * g) = wv;
+      }
   }
 }
 
@@ -418,7 +440,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
 // ---------------------------------------------------------------------------
 template <typename E, int D, bool CAUSAL>
 __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
-                                        const Resident<D>& res, const BwdBuf (&bufs)[2]) {
+                                        const BwdBuf (&bufs)[2]) {
   using C = BwdCfg<D>;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
@@ -429,11 +451,6 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   const int q0 = it.tile * C::OWN;
   const int qw = q0 + 32 * wave;
   const bool wave_valid = qw < S;
-  const int qrow = qw + l32;
-  const u32x4(&qf)[C::KS] = res.r[0];
-  const u32x4(&df)[C::KS] = res.r[1];
-  const float lse2 = res.lse2;
-  const float dl = res.dl;
 
   int rro[C::KS], tro[C::DB];
 #pragma unroll
@@ -454,7 +471,14 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   for (int i = 0; i < C::DB; ++i) acc[i] = f32x16{};
   const float c = a.scale_log2;
 
+  // First tile's loads before the resident rows (one round trip for both).
   dma_stage<D>(src, 1, 0, bufs[0]);
+  Resident<D> res;
+  load_resident<D>(a, it, res);
+  const u32x4(&qf)[C::KS] = res.r[0];
+  const u32x4(&df)[C::KS] = res.r[1];
+  const float lse2 = res.lse2;
+  const float dl = res.dl;
   __syncthreads();
 
   // Key tile j in buffer P = j & 1.  MASKED steps are the causal ones that
@@ -545,18 +569,9 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   if (!wave_valid) return;
   const int b = it.bh / a.H;
   const int h = it.bh % a.H;
-  uint16_t* dqrow = (uint16_t*)a.dq.ptr + b * a.dq.sb + h * a.dq.sh + (int64_t)qrow * a.dq.ss;
-  const float sc = a.scale;
-#pragma unroll
-  for (int db = 0; db < C::DB; ++db) {
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      u32x2 w;
-      w[0] = E::pack2(acc[db][4 * jj + 0] * sc, acc[db][4 * jj + 1] * sc);
-      w[1] = E::pack2(acc[db][4 * jj + 2] * sc, acc[db][4 * jj + 3] * sc);
-      *(u32x2*)(dqrow + 32 * db + 8 * jj + 4 * g) = w;
-    }
-  }
+  store_block_rows<E, D>(acc, a.scale, wave_stage_buf(bufs, wave),
+                         (uint16_t*)a.dq.ptr + b * a.dq.sb + h * a.dq.sh + (int64_t)qw * a.dq.ss,
+                         a.dq.ss);
 }
 
 // One item per workgroup.  One LDS array per buffer and tensor, so that the
@@ -572,12 +587,10 @@ __device__ __forceinline__ void run_item(const AttnArgs& a, const BwdItem it) {
   __shared__ __attribute__((aligned(16))) float SA[2 * C::TILE];
   __shared__ __attribute__((aligned(16))) float SB[2 * C::TILE];
   const BwdBuf bufs[2] = {{A0, A1, SA}, {B0, B1, SB}};
-  Resident<D> res;
-  load_resident<D>(a, it, res);
   if (it.kind)
-    dq_item<E, D, CAUSAL>(a, it, res, bufs);
+    dq_item<E, D, CAUSAL>(a, it, bufs);
   else
-    dkdv_item<E, D, CAUSAL>(a, it, res, bufs);
+    dkdv_item<E, D, CAUSAL>(a, it, bufs);
 }
 
 template <typename E, int D, bool CAUSAL>

@@ -277,18 +277,10 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
 
   if (!wave_valid) return;
   const float l_tot = sum_halves(l_run);
-  const float inv_l = 1.f / l_tot;
-  uint16_t* orow = op + (int64_t)qrow * a.o.ss;
-#pragma unroll
-  for (int db = 0; db < C::DB; ++db) {
-#pragma unroll
-    for (int jj = 0; jj < 4; ++jj) {
-      u32x2 w;
-      w[0] = E::pack2(acc[db][4 * jj + 0] * inv_l, acc[db][4 * jj + 1] * inv_l);
-      w[1] = E::pack2(acc[db][4 * jj + 2] * inv_l, acc[db][4 * jj + 3] * inv_l);
-      *(u32x2*)(orow + 32 * db + 8 * jj + 4 * g) = w;
-    }
-  }
+  // Every buffer is idle after the last step's barrier: wave w stages its O
+  // rows through buffer w.
+  uint16_t* stage = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? V0 : V1;
+  store_block_rows<E, D>(acc, 1.f / l_tot, stage, op + (int64_t)qw * a.o.ss, a.o.ss);
   if (g == 0) a.lse[(int64_t)bh * S + qrow] = (m_run + fast_log2(l_tot)) * kLn2;
 }
 

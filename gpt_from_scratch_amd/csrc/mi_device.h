@@ -239,4 +239,40 @@ __device__ __forceinline__ u32x4 tr_operand(const uint16_t* p, int ld) {
   return u32x4{lo[0], lo[1], hi[0], hi[1]};
 }
 
+// Stores one wave's 32 x D output block, held transposed in 32x32 MFMA
+// accumulators (block db covers columns [32db, 32db+32); lane l holds row l%32
+// and, per register group jj, columns 32db + 8jj + 4(l/32) + {0..3}), times a
+// per-lane (per-row) factor `sc`, rounded to E.  Written straight out, every
+// store instruction would touch 32 rows with 8 bytes each; staged through the
+// wave's own LDS region `lds` (32*D elements, idle at this point) each lane
+// stores 16 contiguous bytes and one instruction covers 64/(D/8) whole rows.
+// `grow` points at row 0 of the block, `ss` is the row stride in elements.
+// Row r of the staging keeps 16-byte chunk c at position c ^ (r & 7).
+template <typename E, int D>
+__device__ __forceinline__ void store_block_rows(const f32x16 (&acc)[D / 32], float sc,
+                                                 uint16_t* lds, uint16_t* grow, int64_t ss) {
+  constexpr int CPR = D / 8;     // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;  // rows per store instruction
+  const int lane = threadIdx.x & 63;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int c = 4 * db + jj;
+      u32x2 w;
+      w[0] = E::pack2(acc[db][4 * jj + 0] * sc, acc[db][4 * jj + 1] * sc);
+      w[1] = E::pack2(acc[db][4 * jj + 2] * sc, acc[db][4 * jj + 3] * sc);
+      *(u32x2*)(lds + l32 * D + ((c ^ (l32 & 7)) << 3) + 4 * g) = w;
+    }
+#pragma unroll
+  for (int p = 0; p < 32 / RPI; ++p) {
+    const int r = p * RPI + lane / CPR;
+    const int c = lane % CPR;
+    const u32x4 v = *(const u32x4*)(lds + r * D + ((c ^ (r & 7)) << 3));
+    *(u32x4*)(grow + (int64_t)r * ss + 8 * c) = v;
+  }
+}
+
 }  // namespace mi
