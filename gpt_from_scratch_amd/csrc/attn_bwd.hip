@@ -65,6 +65,55 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(AttnArgs a, FastDiv div
   if (row < nrows && sub == 0) a.delta[row] = acc;
 }
 
+// The same for 16-bit O and dO with 16-byte aligned rows and D = 64 * NCH:
+// lane l of a group of eight loads bytes [16(l%8), 16(l%8)+16) of each
+// 128-byte chunk, so one wave instruction reads eight whole rows; every lane
+// takes R rows (32 apart) and issues all its loads before the first use.
+template <int DT, int NCH, int R>
+__global__ __launch_bounds__(256) void attn_delta_v16_kernel(AttnArgs a, FastDiv divS,
+                                                             FastDiv divH, uint32_t nrows) {
+  const int sub = threadIdx.x & 7;
+  const uint32_t rbase = blockIdx.x * (32 * R) + (threadIdx.x >> 3);
+  u32x4 ov[R][NCH], dv[R][NCH];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const uint32_t row = rbase + 32 * r;
+    if (row < nrows) {
+      const uint32_t bh = fdiv(row, divS);
+      const uint32_t s = row - bh * divS.d;
+      const uint32_t b = fdiv(bh, divH);
+      const uint32_t h = bh - b * divH.d;
+      const uint16_t* o = (const uint16_t*)a.o.ptr + b * a.o.sb + h * a.o.sh + s * a.o.ss;
+      const uint16_t* d = (const uint16_t*)a.dout.ptr + b * a.dout.sb + h * a.dout.sh + s * a.dout.ss;
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) {
+        ov[r][k] = *(const u32x4*)(o + 64 * k + 8 * sub);
+        dv[r][k] = *(const u32x4*)(d + 64 * k + 8 * sub);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < NCH; ++k) ov[r][k] = dv[r][k] = u32x4{0, 0, 0, 0};
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    float acc = 0.f;
+#pragma unroll
+    for (int k = 0; k < NCH; ++k)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t x = ov[r][k][w], y = dv[r][k][w];
+        acc += Store<DT>::ld((const uint16_t*)&x, 0) * Store<DT>::ld((const uint16_t*)&y, 0);
+        acc += Store<DT>::ld((const uint16_t*)&x, 1) * Store<DT>::ld((const uint16_t*)&y, 1);
+      }
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    acc += __shfl_xor(acc, 4, 64);
+    const uint32_t row = rbase + 32 * r;
+    if (row < nrows && sub == 0) a.delta[row] = acc;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Work items.  The gradients are produced by items of two kinds:
 //   kind 0 (dK/dV, `_attn_bwd_LoopQ`): OWN keys of one head; the item loops
@@ -684,6 +733,20 @@ hipError_t launch_delta_t(const AttnArgs& a, hipStream_t st) {
   const FastDiv dS = make_fastdiv(a.S), dH = make_fastdiv(a.H);
   const dim3 grid((nrows * 8 + 255) / 256);
   constexpr int V16 = (DT == 0) ? 4 : 8;
+  if constexpr (DT != 0) {
+    auto a16 = [](const TensorArg& t) {
+      return ((uintptr_t)t.ptr % 16 == 0) && t.sb % 8 == 0 && t.sh % 8 == 0 && t.ss % 8 == 0;
+    };
+    constexpr int R = 4;
+    const dim3 g4((nrows + 32 * R - 1) / (32 * R));
+    if (a16(a.o) && a16(a.dout) && (a.D == 64 || a.D == 128)) {
+      if (a.D == 64)
+        hipLaunchKernelGGL((attn_delta_v16_kernel<DT, 1, R>), g4, dim3(256), 0, st, a, dS, dH, nrows);
+      else
+        hipLaunchKernelGGL((attn_delta_v16_kernel<DT, 2, R>), g4, dim3(256), 0, st, a, dS, dH, nrows);
+      return hipGetLastError();
+    }
+  }
   if (a.D % (8 * V16) == 0)
     hipLaunchKernelGGL((attn_delta_kernel<DT, V16>), grid, dim3(256), 0, st, a, dS, dH, nrows);
   else
