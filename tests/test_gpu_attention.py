@@ -187,6 +187,31 @@ def test_backward_with_strided_grad(gpu):
         assert_close_bf16(name, got, ref[name])
 
 
+@pytest.mark.parametrize("D,extra", [(64, 1), (64, 8), (128, 1), (128, 8), (32, 8)])
+def test_preprocess_row_pitch(gpu, D, extra):
+    """delta = rowsum(dO * O) through the C ABI with dO rows at a pitch of
+    D + extra elements: an odd pitch leaves rows unaligned (scalar path), a
+    pitch of D + 8 keeps them 16-byte aligned (vector path for D = 64, 128).
+    Against the float64 row sums of the same bf16 values, to fp32 rounding."""
+    import ctypes
+    from gpt_from_scratch_amd import _lib
+    B, H, S = 2, 3, 160
+    o = seeded((B, H, S, D), 70 + D).to(gpu)
+    do = seeded((B, H, S, D + extra), 71 + D).to(gpu)[..., :D]
+    assert do.stride(2) == D + extra
+    delta = torch.empty(B, H, S, device=gpu)
+    lib = _lib.lib()
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    rc = lib.mi_attn_bwd_preprocess(2, B, H, S, D, ctypes.c_void_p(o.data_ptr()),
+                                    _lib._strides(o, 4), ctypes.c_void_p(do.data_ptr()),
+                                    _lib._strides(do, 4), ctypes.c_void_p(delta.data_ptr()), st)
+    assert rc == 0, lib.mi_last_error()
+    # delta as defined by `_attn_bwd_precompute` (core/myFlashAttn.py:787)
+    want = (do.cpu().double() * o.cpu().double()).sum(-1)
+    err = (delta.cpu().double() - want).abs() / want.abs().clamp_min(1.0)
+    assert float(err.max()) < 1e-5
+
+
 def test_errors_surface_as_exceptions(gpu):
     from gpt_from_scratch_amd import apply_flash_attn
     q = torch.randn(1, 1, 64, 48, device=gpu, dtype=torch.bfloat16)
