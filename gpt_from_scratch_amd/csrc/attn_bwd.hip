@@ -528,6 +528,11 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   const u32x4(&df)[C::KS] = res.r[1];
   const float lse2 = res.lse2;
   const float dl = res.dl;
+  // The dP^T accumulators start at -delta (a per-lane constant here), so they
+  // end at dP - delta and dS = P * acc is one multiply.
+  f32x16 ndl;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) ndl[r] = -dl;
   __syncthreads();
 
   // Key tile j in buffer P = j & 1.  MASKED steps are the causal ones that
@@ -551,7 +556,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
         const int kvb = kv0 + 32 * kb;
         live[kb] = !MASKED || (kvb <= qw + 31);
         if (!live[kb]) continue;
-        f32x16 s = f32x16{}, dp = f32x16{};
+        f32x16 s = f32x16{}, dp = ndl;
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
           const u32x4 ka = *(const u32x4*)(&Ks[32 * kb * D + rro[ks]]);
@@ -567,7 +572,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
         for (int r = 0; r < 16; ++r) {
           float p = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
           if (MASKED && diag && 8 * (r >> 2) + 4 * g + (r & 3) > l32) p = 0.f;
-          dp[r] = p * (dp[r] - dl);
+          dp[r] = p * dp[r];
         }
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh)
