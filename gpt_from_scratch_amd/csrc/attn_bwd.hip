@@ -65,6 +65,13 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(AttnArgs a, FastDiv div
   if (row < nrows && sub == 0) a.delta[row] = acc;
 }
 
+// One 16-bit value (bf16 or fp16, per DT) held in the low bits of x, as fp32.
+template <int DT>
+__device__ __forceinline__ float half_f32(uint32_t x) {
+  if constexpr (DT == 2) return __uint_as_float(x << 16);
+  else return (float)__builtin_bit_cast(_Float16, (uint16_t)x);
+}
+
 // The same for 16-bit O and dO with 16-byte aligned rows and D = 64 * NCH:
 // lane l of a group of eight loads bytes [16(l%8), 16(l%8)+16) of each
 // 128-byte chunk, so one wave instruction reads eight whole rows; every lane
@@ -103,8 +110,8 @@ __global__ __launch_bounds__(256) void attn_delta_v16_kernel(AttnArgs a, FastDiv
 #pragma unroll
       for (int w = 0; w < 4; ++w) {
         const uint32_t x = ov[r][k][w], y = dv[r][k][w];
-        acc += Store<DT>::ld((const uint16_t*)&x, 0) * Store<DT>::ld((const uint16_t*)&y, 0);
-        acc += Store<DT>::ld((const uint16_t*)&x, 1) * Store<DT>::ld((const uint16_t*)&y, 1);
+        acc += half_f32<DT>(x & 0xffffu) * half_f32<DT>(y & 0xffffu);
+        acc += half_f32<DT>(x >> 16) * half_f32<DT>(y >> 16);
       }
     acc += __shfl_xor(acc, 1, 64);
     acc += __shfl_xor(acc, 2, 64);

@@ -148,6 +148,22 @@ def test_noncausal(gpu):
     _config_check(gpu, 1, 2, 256, 128, seed=12, std=0.5, causal=False)
 
 
+def test_noncausal_identical_keys(gpu):
+    """Every key equal: each row's scores tie, so O is the mean of V over the
+    sequence and LSE = s + ln S (s the common scaled score) — closed forms, no
+    oracle run.  Long enough to cross many key tiles of both head dims."""
+    from gpt_from_scratch_amd import flash_attn_forward
+    for S, D in ((512, 64), (256, 128)):
+        q = seeded((1, 2, S, D), 80 + D).to(gpu)
+        k = seeded((1, 2, 1, D), 81 + D).expand(1, 2, S, D).contiguous().to(gpu)
+        v = seeded((1, 2, S, D), 82 + D).to(gpu)
+        o, lse = flash_attn_forward(q, k, v, False)
+        want = v.float().mean(2, keepdim=True).expand(1, 2, S, D).cpu()
+        assert float((o.float().cpu() - want).abs().max()) < 2e-2
+        s = (q.float().cpu() * k[:, :, :1].float().cpu()).sum(-1) / math.sqrt(D)
+        assert float((lse.cpu() - (s + math.log(S))).abs().max()) < 1e-3
+
+
 def test_fp16(gpu):
     _config_check(gpu, 2, 4, 512, 64, seed=13, std=1.0, dtype=torch.float16)
     _config_check(gpu, 1, 2, 256, 128, seed=14, std=1.0, dtype=torch.float16)
@@ -187,18 +203,25 @@ def test_backward_with_strided_grad(gpu):
         assert_close_bf16(name, got, ref[name])
 
 
+@pytest.mark.parametrize("layout", ["bhsd", "sbhd"])
 @pytest.mark.parametrize("D,extra", [(64, 1), (64, 8), (128, 1), (128, 8), (32, 8)])
-def test_preprocess_row_pitch(gpu, D, extra):
+def test_preprocess_row_pitch(gpu, D, extra, layout):
     """delta = rowsum(dO * O) through the C ABI with dO rows at a pitch of
     D + extra elements: an odd pitch leaves rows unaligned (scalar path), a
-    pitch of D + 8 keeps them 16-byte aligned (vector path for D = 64, 128).
+    pitch of D + 8 keeps them 16-byte aligned (vector paths for D = 64, 128).
+    dO is [B,H,S,*] or a permuted view of [S,B,H,*] (position-major, as the
+    model's gradient arrives).
     Against the float64 row sums of the same bf16 values, to fp32 rounding."""
     import ctypes
     from gpt_from_scratch_amd import _lib
-    B, H, S = 2, 3, 160
+    B, H, S = 2, 3, 150
     o = seeded((B, H, S, D), 70 + D).to(gpu)
-    do = seeded((B, H, S, D + extra), 71 + D).to(gpu)[..., :D]
-    assert do.stride(2) == D + extra
+    if layout == "bhsd":
+        do = seeded((B, H, S, D + extra), 71 + D).to(gpu)[..., :D]
+    else:
+        do = seeded((S, B, H, D + extra), 71 + D).to(gpu)[..., :D].permute(1, 2, 0, 3)
+        assert do.stride(2) > do.stride(0)
+    assert do.stride(3) == 1 and (do.stride(2) - D if layout == "bhsd" else do.stride(1) - D) == extra
     delta = torch.empty(B, H, S, device=gpu)
     lib = _lib.lib()
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)

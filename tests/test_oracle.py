@@ -81,6 +81,19 @@ def test_dominant_key_selects_its_value():
         assert torch.allclose(oc[i], v[: i + 1].mean(0), atol=1e-12)
 
 
+def test_identical_keys_average_the_values():
+    """Non-causal with every key equal: all scores of a row tie, so each output
+    row is the plain mean of V and LSE = s + ln(S) for the common score s."""
+    S, D = 10, 8
+    q = _randn(S, D, seed=13)
+    k = _randn(1, D, seed=14).expand(S, D).clone()
+    v = _randn(S, D, seed=15)
+    o, lse = attention_forward(q, k, v, False)
+    assert torch.allclose(o, v.mean(0).expand(S, D), atol=1e-12)
+    s = (q @ k[0]) / math.sqrt(D)
+    assert torch.allclose(lse, s + math.log(S), atol=1e-12)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 def test_closed_form_backward_matches_autograd(causal):
     q, k, v = (_randn(2, 2, 13, 8, seed=s).requires_grad_() for s in (13, 14, 15))
