@@ -38,6 +38,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from ..attention_block import attention_block
 from ..flash_attn import apply_flash_attn
 from ..position_embeddings import RotaryEmbedding
 from ..rope import apply_rope_qk
@@ -86,9 +87,16 @@ class Attention(nn.Module):
                                       device=device)
         self.attention = attention or apply_flash_attn
         self.rope = rope or apply_rope_qk
+        # With the HIP kernels on both sides, the block runs fused: no relayout
+        # copies of q/k/v, O or the qkv gradient.
+        self.fused = attention is None and rope is None
 
     def forward(self, x):  # x: [S, B, H]
         S, B, _ = x.shape
+        if self.fused:
+            cos, sin = self.rotary(x, seq_len=S)
+            return F.linear(attention_block(F.linear(x, self.qkv), cos, sin, self.heads),
+                            self.out)
         qkv = F.linear(x, self.qkv).view(S, B, 3, self.heads, self.head_dim)
         q, k, v = qkv.unbind(2)
         cos, sin = self.rotary(q, seq_len=S)

@@ -105,6 +105,19 @@ def test_python_api_shape_errors():
         apply_rope(torch.randn(4, 1, 1, 7), torch.ones(4, 3), torch.ones(4, 3))
 
 
+def test_attention_block_shape_errors():
+    """The fused block checks its [S, B, 3*H*D] input before any launch."""
+    import torch
+    from gpt_from_scratch_amd import attention_block
+    cos, sin = torch.ones(8, 2), torch.ones(8, 2)
+    with pytest.raises(ValueError, match="3 \\* heads"):
+        attention_block(torch.randn(8, 2, 10), cos, sin, 2)
+    with pytest.raises(ValueError):
+        attention_block(torch.randn(8, 30), cos, sin, 2)
+    with pytest.raises(AssertionError, match="even"):
+        attention_block(torch.randn(8, 2, 18), cos, sin, 2)
+
+
 def test_rotary_embedding_tables_cpu():
     import torch
     from gpt_from_scratch_amd import RotaryEmbedding
