@@ -44,6 +44,8 @@ def parse_args():
                     help="approximate CPU time budget of the baseline sample")
     ap.add_argument("--no-gpt", action="store_true",
                     help="skip the config-5 GPT train-step measurement")
+    ap.add_argument("--no-model-ops", action="store_true",
+                    help="skip the config-5 cross-entropy kernel measurement")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run a plain elementwise kernel that reads and "
                          "writes 256 MiB each (reference point for HBM byte counters)")
@@ -56,10 +58,10 @@ def attn_flops(B, H, S, D):
             "total": 7 * unit}
 
 
-def read_traffic(kernel):
-    """HBM bytes per launch for `kernel` from the committed rocprofv3 PMC summary,
+def read_traffic(kernel, fname="traffic_c2.txt"):
+    """HBM bytes per launch for `kernel` from a committed rocprofv3 PMC summary,
     or None when it has not been measured."""
-    path = os.path.join(ROOT, "profiles", "traffic_c2.txt")
+    path = os.path.join(ROOT, "profiles", fname)
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -99,13 +101,71 @@ def cpu_baseline(B, H, S, D, budget_s):
                       f"fwd+bwd on the CPU, median of {reps} runs ({t:.2f} s each)"}
 
 
+def _time_calls(stream, fn, args, n, what):
+    """Average µs per call of `fn(*args)` over n back-to-back launches on `stream`."""
+    import torch
+    for _ in range(3):
+        if fn(*args) != 0:
+            raise RuntimeError(what)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(n):
+        fn(*args)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n * 1e3
+
+
+def model_ops_bench(dev, lib):
+    """The train step's fused bandwidth-bound kernels at config 5's shapes, each
+    against the HBM peak with its algorithmic bytes (every input read once,
+    every output written once):
+      * cross entropy over logits [S*B = 8192, V = 50257] bf16
+        (core/tensor_parallel/loss.py:9-72): forward reads the logits and the
+        int64 targets, writes the bf16 loss and the fp32 lse; backward reads the
+        logits, targets, lse and dloss and writes the bf16 gradient."""
+    import torch
+    from gpt_from_scratch_amd import _lib
+
+    S, B, V = 1024, 8, 50257
+    rows = S * B
+    g = torch.Generator(device=dev).manual_seed(3)
+    z = (torch.randn(S, B, V, generator=g, device=dev) * 2).to(torch.bfloat16)
+    t = torch.randint(0, V, (S, B), generator=g, device=dev)
+    loss = torch.empty(S, B, dtype=torch.bfloat16, device=dev)
+    lse = torch.empty(S, B, dtype=torch.float32, device=dev)
+    dl = torch.full((S, B), 1.0 / rows, dtype=torch.bfloat16, device=dev)
+    grad = torch.empty_like(z)
+    stream = torch.cuda.current_stream(dev)
+    sp = ctypes.c_void_p(stream.cuda_stream)
+    P = lambda x: ctypes.c_void_p(x.data_ptr())
+    dt = _lib.dtype_code(z)
+    fwd = (dt, rows, V, P(z), V, P(t), P(loss), P(lse), sp)
+    bwd = (dt, rows, V, P(z), V, P(t), P(lse), P(dl), P(grad), V, sp)
+    out = {}
+    for name, fn, a, nbytes in (
+            ("xent_fwd", lib.mi_xent_fwd, fwd, rows * V * 2 + rows * (8 + 2 + 4)),
+            ("xent_bwd", lib.mi_xent_bwd, bwd, 2 * rows * V * 2 + rows * (8 + 4 + 2))):
+        us = _time_calls(stream, fn, a, 30, name)
+        gbps = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"bound": "hbm", "avg_us": round(us, 2), "achieved": round(gbps, 1),
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                     "algorithmic_bytes": nbytes, "shape": f"[{rows}, {V}] bf16",
+                     "traffic": read_traffic(name, "traffic_xent_c5.txt")}
+    del z, grad
+    torch.cuda.empty_cache()
+    return out
+
+
 def gpt_train(dev, steps=20, warmup=3):
     """Config 5: GPT train step (12L / 768 / 12 heads / SwiGLU 3072 / RMSNorm /
     vocab 50257, B=8, S=1024, TP=1, DP=1) with attention and RoPE on the HIP
     kernels; tokens/s = B*S*steps / wall time (train.py:196-198), beside the
-    same step with attention done by plain PyTorch matmul/softmax (fp32 math)."""
+    same step with attention done by plain PyTorch matmul/softmax (fp32 math)
+    and the loss by eager torch ops."""
     import torch
-    from gpt_from_scratch_amd.harness import GPTConfig, train
+    from gpt_from_scratch_amd.harness import GPTConfig, SoftmaxCrossEntropy, train
 
     def eager_attention(q, k, v):
         S, Dh = q.shape[-2], q.shape[-1]
@@ -117,12 +177,13 @@ def gpt_train(dev, steps=20, warmup=3):
     cfg = GPTConfig()
     losses, tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup)
     _, eager_tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup,
-                         attention=eager_attention)
+                         attention=eager_attention, loss_fn=SoftmaxCrossEntropy.apply)
     return {"workload": "config 5: 12L/768/12H SwiGLU RMSNorm vocab 50257, B8 S1024, bf16 params "
                         "+ fp32 AdamW master, TP=1 DP=1, synthetic uint16 ids",
             "steps": steps, "tokens_per_s": round(tps, 1),
             "ms_per_step": round(8 * 1024 / tps * 1e3, 3),
-            "tokens_per_s_eager_attention": round(eager_tps, 1),
+            "tokens_per_s_eager": round(eager_tps, 1),
+            "eager": "attention as torch matmul/softmax (fp32 math), loss as eager torch ops",
             "loss_first": round(losses[0], 4), "loss_last": round(losses[-1], 4)}
 
 
@@ -248,6 +309,8 @@ def main():
     rope_bytes = 4 * B * S * H * D * 2 + 2 * S * (D // 2) * 2
     rope_gbps = rope_bytes / (rope_us * 1e-6) / 1e9
 
+    model_ops = {} if args.no_model_ops else model_ops_bench(dev, lib)
+
     if args.calibrate_copy:
         # 64 Mi fp32 elements: exactly 256 MiB read and 256 MiB written by one
         # elementwise kernel; its byte counters scale the attention kernels'.
@@ -275,6 +338,8 @@ def main():
                  "frac": round(rope_gbps / PEAK_HBM_GBPS, 4), "algorithmic_bytes": rope_bytes,
                  "traffic": read_traffic("rope_qk")},
     }
+    if model_ops:
+        out["model_ops"] = model_ops
     if not args.no_gpt:
         out["gpt_train"] = gpt_train(dev)
     if not args.no_cpu_baseline:

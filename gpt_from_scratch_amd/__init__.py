@@ -1,10 +1,13 @@
 """MI355X-native attention hot path of gpt_from_scratch.
 
 Drop-ins for the reference's kernels (core/myFlashAttn.py, core/rope_triton.py,
-core/position_embeddings.py), backed by hand-written gfx950 HIP kernels in
+core/position_embeddings.py) and its vocabulary cross entropy
+(core/tensor_parallel/loss.py), backed by hand-written gfx950 HIP kernels in
 libmi_attn.so behind the C ABI of include/mi_attn.h.
 """
 from .attention_block import AttentionBlock, attention_block
+from .cross_entropy import (VocabParallelCrossEntropy, _VocabParallelCrossEntropy,
+                            vocab_parallel_cross_entropy)
 from .flash_attn import FlashAttn, apply_flash_attn, flash_attn_backward, flash_attn_forward
 from .position_embeddings import RotaryEmbedding
 from .rope import RoPE, RoPEQK, TritonRoPE, apply_rope, apply_rope_qk
@@ -13,4 +16,5 @@ __all__ = [
     "FlashAttn", "apply_flash_attn", "flash_attn_forward", "flash_attn_backward",
     "RotaryEmbedding", "RoPE", "RoPEQK", "TritonRoPE", "apply_rope", "apply_rope_qk",
     "AttentionBlock", "attention_block",
+    "VocabParallelCrossEntropy", "_VocabParallelCrossEntropy", "vocab_parallel_cross_entropy",
 ]

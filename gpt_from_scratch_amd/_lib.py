@@ -24,8 +24,7 @@ _DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 # Every function declared in include/mi_attn.h.
 EXPORTED = ("mi_version", "mi_status_str", "mi_last_error", "mi_attn_fwd", "mi_attn_bwd",
             "mi_attn_bwd_preprocess", "mi_attn_bwd_grads", "mi_attn_bwd_dkdv", "mi_attn_bwd_dq",
-            "mi_rope",
-            "mi_rope_qk")
+            "mi_rope", "mi_rope_qk", "mi_xent_fwd", "mi_xent_bwd")
 
 _lib = None
 
@@ -68,6 +67,11 @@ def _declare(lib):
     lib.mi_rope_qk.restype = i
     lib.mi_rope_qk.argtypes = [i, i, i, i, i, i, i, p, i64p, p, i64p, p, i64p, p, i64p,
                                p, i64p, p, i64p, p]
+    i64 = ctypes.c_int64
+    lib.mi_xent_fwd.restype = i
+    lib.mi_xent_fwd.argtypes = [i, i64, i64, p, i64, p, p, p, p]
+    lib.mi_xent_bwd.restype = i
+    lib.mi_xent_bwd.argtypes = [i, i64, i64, p, i64, p, p, p, p, i64, p]
 
 
 def lib():
@@ -166,3 +170,44 @@ def rope_qk(q, k, cos, sin, q_out, k_out, inverse: bool):
                           _ptr(q_out), _strides(q_out, 4), _ptr(k_out), _strides(k_out, 4),
                           _stream(q))
     _check(st, "mi_rope_qk")
+
+
+def _rows(t: torch.Tensor):
+    """(rows, row stride) of t viewed as rows over its last dim (unit stride)."""
+    if t.stride(-1) != 1:
+        raise ValueError("the vocabulary dim must have unit stride")
+    lead = t.shape[:-1]
+    rows = 1
+    for n in lead:
+        rows *= n
+    if t.dim() == 1:
+        return 1, t.shape[-1]
+    # the leading dims must collapse into one row index with a single stride
+    rs = t.stride(-2)
+    expect = rs
+    for d in range(t.dim() - 2, -1, -1):
+        if t.shape[d] != 1 and t.stride(d) != expect:
+            raise ValueError(f"leading dims of {tuple(t.shape)} / {t.stride()} are not one row axis")
+        expect *= t.shape[d]
+    return rows, rs
+
+
+def xent_fwd(logits, target, loss, lse):
+    """Enqueue the cross-entropy forward: loss [rows] (logits dtype), lse [rows] fp32."""
+    _require_gpu(logits, target, loss, lse)
+    rows, rs = _rows(logits)
+    st = lib().mi_xent_fwd(dtype_code(logits), rows, logits.shape[-1], _ptr(logits), rs,
+                           _ptr(target), _ptr(loss), _ptr(lse), _stream(logits))
+    _check(st, "mi_xent_fwd")
+
+
+def xent_bwd(logits, target, lse, grad_loss, grad):
+    """Enqueue the cross-entropy backward into grad (may be logits itself)."""
+    _require_gpu(logits, target, lse, grad_loss, grad)
+    rows, rs = _rows(logits)
+    grows, grs = _rows(grad)
+    assert grows == rows
+    st = lib().mi_xent_bwd(dtype_code(logits), rows, logits.shape[-1], _ptr(logits), rs,
+                           _ptr(target), _ptr(lse), _ptr(grad_loss), _ptr(grad), grs,
+                           _stream(logits))
+    _check(st, "mi_xent_bwd")

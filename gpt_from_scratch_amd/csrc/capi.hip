@@ -378,4 +378,62 @@ mi_status mi_rope_qk(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, 
                      cos_strides, sin_tab, sin_strides, stream);
 }
 
+static mi_status xent_common(mi_dtype dtype, int64_t rows, int64_t vocab, const void* logits,
+                             int64_t row_stride, const int64_t* target, mi::XentArgs& a) {
+  if (!dtype_ok(dtype)) return fail(MI_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+  if (rows <= 0 || vocab <= 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "sizes must be positive (rows=%lld vocab=%lld)",
+                (long long)rows, (long long)vocab);
+  if (rows >= (1ll << 31)) return fail(MI_ERR_UNSUPPORTED, "rows = %lld exceeds 2^31", (long long)rows);
+  if (row_stride < vocab)
+    return fail(MI_ERR_INVALID_ARGUMENT, "row_stride %lld < vocab %lld", (long long)row_stride,
+                (long long)vocab);
+  if (!logits || !target) return fail(MI_ERR_INVALID_ARGUMENT, "logits / target: null pointer");
+  if (((uintptr_t)logits) % elem_size(dtype) || ((uintptr_t)target) % 8)
+    return fail(MI_ERR_INVALID_ARGUMENT, "logits / target: misaligned");
+  a = {};
+  a.logits = logits;
+  a.rows = rows;
+  a.vocab = vocab;
+  a.row_stride = row_stride;
+  a.target = target;
+  return MI_OK;
+}
+
+mi_status mi_xent_fwd(mi_dtype dtype, int64_t rows, int64_t vocab, const void* logits,
+                      int64_t row_stride, const int64_t* target, void* loss, float* lse,
+                      void* stream) {
+  mi::XentArgs a;
+  if (mi_status st = xent_common(dtype, rows, vocab, logits, row_stride, target, a)) return st;
+  if (!loss || !lse) return fail(MI_ERR_INVALID_ARGUMENT, "loss / lse: null pointer");
+  if (((uintptr_t)loss) % elem_size(dtype) || ((uintptr_t)lse) % 4)
+    return fail(MI_ERR_INVALID_ARGUMENT, "loss / lse: misaligned");
+  a.loss = loss;
+  a.lse = lse;
+  return launched(mi::launch_xent_fwd(dtype, a, (hipStream_t)stream), "xent_fwd");
+}
+
+mi_status mi_xent_bwd(mi_dtype dtype, int64_t rows, int64_t vocab, const void* logits,
+                      int64_t row_stride, const int64_t* target, const float* lse,
+                      const void* grad_loss, void* grad_logits, int64_t grad_row_stride,
+                      void* stream) {
+  mi::XentArgs a;
+  if (mi_status st = xent_common(dtype, rows, vocab, logits, row_stride, target, a)) return st;
+  if (!lse || !grad_loss || !grad_logits)
+    return fail(MI_ERR_INVALID_ARGUMENT, "lse / grad_loss / grad_logits: null pointer");
+  if (((uintptr_t)lse) % 4 || ((uintptr_t)grad_loss) % elem_size(dtype) ||
+      ((uintptr_t)grad_logits) % elem_size(dtype))
+    return fail(MI_ERR_INVALID_ARGUMENT, "lse / grad_loss / grad_logits: misaligned");
+  if (grad_row_stride < vocab)
+    return fail(MI_ERR_INVALID_ARGUMENT, "grad_row_stride %lld < vocab %lld",
+                (long long)grad_row_stride, (long long)vocab);
+  if (grad_logits == logits && grad_row_stride != row_stride)
+    return fail(MI_ERR_INVALID_ARGUMENT, "in-place backward needs grad_row_stride == row_stride");
+  a.lse = (float*)lse;
+  a.grad_loss = grad_loss;
+  a.grad = grad_logits;
+  a.grad_row_stride = grad_row_stride;
+  return launched(mi::launch_xent_bwd(dtype, a, (hipStream_t)stream), "xent_bwd");
+}
+
 }  // extern "C"

@@ -60,4 +60,20 @@ struct RopeArgs {
 hipError_t launch_rope(int x_dtype, int tab_dtype, const RopeArgs& a, bool vector_ok,
                        hipStream_t st);
 
+// Softmax cross entropy over the vocabulary (model_ops.hip).  One row per
+// token; logits / grad rows are `row_stride` / `grad_row_stride` elements apart.
+struct XentArgs {
+  const void* logits;
+  int64_t rows, vocab, row_stride;
+  const int64_t* target;
+  void* loss;           // [rows], logits dtype (forward)
+  float* lse;           // [rows] fp32, written by forward, read by backward
+  const void* grad_loss;  // [rows], logits dtype (backward)
+  void* grad;           // backward output
+  int64_t grad_row_stride;
+};
+
+hipError_t launch_xent_fwd(int dtype, const XentArgs& a, hipStream_t st);
+hipError_t launch_xent_bwd(int dtype, const XentArgs& a, hipStream_t st);
+
 }  // namespace mi

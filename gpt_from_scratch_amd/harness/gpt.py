@@ -18,7 +18,9 @@ kernels run inside a real train step:
 * RMSNorm: fp32 mean square, rsqrt(ms + eps), cast back, times the weight
   (core/normalization.py:13-25);
 * loss: softmax cross entropy on the (bf16) logits, mean over [S, B]
-  (core/tensor_parallel/loss.py:9-72 at one rank; train.py:179-181);
+  (core/tensor_parallel/loss.py:9-72 at one rank; train.py:179-181), by
+  default the fused HIP kernels (`loss_fn` injectable, e.g. the eager
+  `SoftmaxCrossEntropy.apply` below);
 * optimizer (core/optimizer.py:6-104 at one rank): parameters and gradients
   live in flat bf16 buffers the model computes in, an fp32 master copy takes
   the AdamW step, gradients are clipped by their global norm first, and the
@@ -26,7 +28,7 @@ kernels run inside a real train step:
 * init: xavier-uniform for every projection and the embedding
   (core/tensor_parallel/layers.py:31,66,112), RMSNorm weights 1.
 
-Everything here is ordinary PyTorch except the attention path.
+Everything here is ordinary PyTorch except the attention path and the loss.
 """
 from __future__ import annotations
 
@@ -39,6 +41,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from ..attention_block import attention_block
+from ..cross_entropy import vocab_parallel_cross_entropy
 from ..flash_attn import apply_flash_attn
 from ..position_embeddings import RotaryEmbedding
 from ..rope import apply_rope_qk
@@ -222,10 +225,12 @@ def synthetic_batch(batch, seq, vocab, seed, device):
 
 
 def train(cfg: GPTConfig, batch=8, seq=1024, steps=20, seed=5, device="cuda", attention=None,
-          rope=None, warmup=0):
+          rope=None, warmup=0, loss_fn=None):
     """Build the model and optimizer from `seed`, run `warmup` untimed then
     `steps` timed train steps on one fixed synthetic batch.  Returns
-    (losses, tokens_per_second)."""
+    (losses, tokens_per_second).  `loss_fn(logits, target)` -> per-token loss
+    defaults to the HIP cross entropy."""
+    loss_fn = loss_fn or vocab_parallel_cross_entropy
     torch.manual_seed(seed)
     model = GPT(cfg, device, attention, rope)
     opt = MixedPrecisionAdamW(model)
@@ -235,7 +240,7 @@ def train(cfg: GPTConfig, batch=8, seq=1024, steps=20, seed=5, device="cuda", at
     def one_step():
         opt.zero_grad()
         logits = model(inputs)
-        per_token = SoftmaxCrossEntropy.apply(logits, labels_t)
+        per_token = loss_fn(logits, labels_t)
         per_token.mean().backward()  # mean in the logits' dtype, as the reference does
         opt.step()
         return per_token.detach().float().mean()  # logged in fp32 for resolution

@@ -171,6 +171,34 @@ mi_status mi_rope_qk(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, 
                      void* k_out, const int64_t k_out_strides[4],
                      void* stream);
 
+/*
+ * Softmax cross entropy of each logits row against an integer target, at one
+ * tensor-parallel rank (the whole vocabulary on this GPU).  Replaces the
+ * forward of _VocabParallelCrossEntropy, core/tensor_parallel/loss.py:9-57:
+ *   loss[r] = log sum_j exp(z_rj - m_r) - (z_r,t - m_r),  m_r = max_j z_rj,
+ * where a target outside [0, vocab) is masked: its shifted logit counts as 0
+ * (:33-41).  Instead of the normalised softmax (:54-56) it saves
+ * lse[r] = m_r + log sum_j exp(z_rj - m_r), fp32, for mi_xent_bwd.
+ * logits: rows of `vocab` elements, `row_stride` elements apart (any alignment);
+ * target: int64 [rows]; loss: [rows] in the logits dtype.  Row statistics are
+ * fp32.
+ */
+mi_status mi_xent_fwd(mi_dtype dtype, int64_t rows, int64_t vocab, const void* logits,
+                      int64_t row_stride, const int64_t* target, void* loss, float* lse,
+                      void* stream);
+
+/*
+ * Gradient of mi_xent_fwd: grad[r, j] = (exp(z_rj - lse[r]) - [j == t_r]) *
+ * grad_loss[r], with no -1 for a masked target.  Replaces
+ * _VocabParallelCrossEntropy.backward, core/tensor_parallel/loss.py:59-72.
+ * grad_logits may be the logits buffer itself (same row stride): each element
+ * is read before it is overwritten.  Any other overlap is undefined.
+ */
+mi_status mi_xent_bwd(mi_dtype dtype, int64_t rows, int64_t vocab, const void* logits,
+                      int64_t row_stride, const int64_t* target, const float* lse,
+                      const void* grad_loss, void* grad_logits, int64_t grad_row_stride,
+                      void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -128,3 +128,36 @@ def test_rotary_embedding_tables_cpu():
     c, s = rope_tables(64, 40)
     assert cos.dtype == torch.bfloat16 and cos.shape == (40, 32)
     assert torch.equal(cos, c.to(torch.bfloat16)) and torch.equal(sin, s.to(torch.bfloat16))
+
+
+def test_xent_rejects_bad_arguments_before_launch():
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(16)
+    V = 50257
+    # rows <= 0, vocab <= 0
+    assert lib.mi_xent_fwd(2, 0, V, fake, V, fake, fake, fake, None) == 1
+    assert lib.mi_xent_fwd(2, 4, 0, fake, V, fake, fake, fake, None) == 1
+    # row stride shorter than a row
+    assert lib.mi_xent_fwd(2, 4, V, fake, V - 1, fake, fake, fake, None) == 1
+    assert b"row_stride" in lib.mi_last_error()
+    # null / misaligned pointers
+    assert lib.mi_xent_fwd(2, 4, V, None, V, fake, fake, fake, None) == 1
+    assert lib.mi_xent_fwd(2, 4, V, ctypes.c_void_p(17), V, fake, fake, fake, None) == 1
+    assert b"misaligned" in lib.mi_last_error()
+    assert lib.mi_xent_fwd(9, 4, V, fake, V, fake, fake, fake, None) == 1
+    # backward: in-place needs the same row stride
+    assert lib.mi_xent_bwd(2, 4, V, fake, V + 3, fake, fake, fake, fake, V, None) == 1
+    assert b"in-place" in lib.mi_last_error()
+    assert lib.mi_xent_bwd(2, 4, V, fake, V, fake, fake, None, fake, V, None) == 1
+
+
+def test_cross_entropy_python_checks():
+    import torch
+    from gpt_from_scratch_amd import vocab_parallel_cross_entropy
+    z = torch.randn(4, 3, 10)
+    with pytest.raises(ValueError, match="target shape"):
+        vocab_parallel_cross_entropy(z, torch.zeros(4, dtype=torch.int64))
+    with pytest.raises(TypeError, match="integer"):
+        vocab_parallel_cross_entropy(z, torch.zeros(4, 3))
+    with pytest.raises(RuntimeError, match="ROCm GPUs only"):
+        vocab_parallel_cross_entropy(z, torch.zeros(4, 3, dtype=torch.int64))

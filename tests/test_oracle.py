@@ -209,3 +209,66 @@ def test_rope_gradient_is_inverse_rotation():
     g = _randn(S, B, H, D, seed=34)
     (gx,) = torch.autograd.grad(rope_apply(x, c, s), x, g)
     assert torch.allclose(gx, rope_apply(g, c, s, inverse=True), atol=1e-12)
+
+
+# ---- vocabulary cross entropy (oracle/cross_entropy.py) ----
+
+def _xent_inputs(rows=12, V=37, seed=3):
+    rng = np.random.default_rng(seed)
+    z = rng.normal(0.0, 3.0, size=(rows, V))
+    t = rng.integers(0, V, size=rows)
+    return z, t
+
+
+def test_xent_matches_scipy_logsumexp():
+    from scipy.special import logsumexp
+    from oracle import cross_entropy_forward
+    z, t = _xent_inputs()
+    loss, lse = cross_entropy_forward(z, t)
+    ref_lse = logsumexp(z, axis=-1)
+    np.testing.assert_allclose(lse, ref_lse, rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(loss, ref_lse - z[np.arange(len(t)), t], rtol=1e-12, atol=1e-12)
+
+
+def test_xent_uniform_logits_give_log_vocab_and_shift_invariance():
+    from oracle import cross_entropy_forward
+    V = 50257
+    loss, _ = cross_entropy_forward(np.full((3, V), 7.25), np.array([0, 5, V - 1]))
+    np.testing.assert_allclose(loss, math.log(V), rtol=1e-13)
+    z, t = _xent_inputs()
+    shift = np.linspace(-1e3, 1e3, z.shape[0])[:, None]
+    np.testing.assert_allclose(cross_entropy_forward(z + shift, t)[0],
+                               cross_entropy_forward(z, t)[0], rtol=1e-9, atol=1e-9)
+
+
+def test_xent_masked_target_semantics():
+    """loss.py:33-41: an out-of-range target contributes a shifted logit of 0,
+    so the loss is log(sum exp(z - max)) = lse - max, and the gradient is the
+    plain softmax."""
+    from oracle import cross_entropy_backward, cross_entropy_forward
+    z, t = _xent_inputs(rows=4)
+    t = np.array([-1, 37, -100, 2])
+    loss, lse = cross_entropy_forward(z, t)
+    np.testing.assert_allclose(loss[:3], (lse - z.max(-1))[:3], rtol=1e-13)
+    g = cross_entropy_backward(z, t, np.ones(4))
+    p = np.exp(z - lse[:, None])
+    np.testing.assert_allclose(g[:3], p[:3], rtol=1e-12, atol=1e-15)
+    assert abs(g[3].sum()) < 1e-12 and g[3, 2] < 0
+
+
+def test_xent_gradient_is_finite_difference():
+    from oracle import cross_entropy_backward, cross_entropy_forward
+    z, t = _xent_inputs(rows=3, V=11)
+    w = np.array([0.5, -1.25, 2.0])  # d(sum_r w_r loss_r) / dz
+    g = cross_entropy_backward(z, t, w)
+    eps = 1e-6
+    fd = np.zeros_like(z)
+    for r in range(z.shape[0]):
+        for j in range(z.shape[1]):
+            zp, zm = z.copy(), z.copy()
+            zp[r, j] += eps
+            zm[r, j] -= eps
+            fd[r, j] = (w @ cross_entropy_forward(zp, t)[0] - w @ cross_entropy_forward(zm, t)[0]) / (2 * eps)
+    np.testing.assert_allclose(g, fd, rtol=1e-6, atol=1e-8)
+    # rows with an in-range target sum to zero
+    np.testing.assert_allclose(g.sum(-1), 0.0, atol=1e-12)
