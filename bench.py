@@ -117,6 +117,22 @@ def _time_calls(stream, fn, args, n, what):
     return e0.elapsed_time(e1) / n * 1e3
 
 
+def _time_rotating(stream, fn, arglist, n, what):
+    """Average µs per call over n back-to-back launches cycling through arglist."""
+    import torch
+    for a in arglist[:3]:
+        if fn(*a) != 0:
+            raise RuntimeError(what)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(n):
+        fn(*arglist[i % len(arglist)])
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n * 1e3
+
+
 def model_ops_bench(dev, lib):
     """The train step's fused bandwidth-bound kernels at config 5's shapes, each
     against the HBM peak with its algorithmic bytes (every input read once,
@@ -124,7 +140,11 @@ def model_ops_bench(dev, lib):
       * cross entropy over logits [S*B = 8192, V = 50257] bf16
         (core/tensor_parallel/loss.py:9-72): forward reads the logits and the
         int64 targets, writes the bf16 loss and the fp32 lse; backward reads the
-        logits, targets, lse and dloss and writes the bf16 gradient."""
+        logits, targets, lse and dloss and writes the bf16 gradient;
+      * RMSNorm over [8192, 768] bf16 (core/normalization.py:13-25): forward
+        reads x and w, writes y and the fp32 rstd; backward reads x, dy, w and
+        rstd, writes dx and dw (its [parts, 768] fp32 partials stay in cache
+        and are not counted)."""
     import torch
     from gpt_from_scratch_amd import _lib
 
@@ -152,8 +172,38 @@ def model_ops_bench(dev, lib):
         out[name] = {"bound": "hbm", "avg_us": round(us, 2), "achieved": round(gbps, 1),
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
                      "algorithmic_bytes": nbytes, "shape": f"[{rows}, {V}] bf16",
-                     "traffic": read_traffic(name, "traffic_xent_c5.txt")}
+                     "traffic": read_traffic(name, "traffic_model_ops_c5.txt")}
     del z, grad
+    torch.cuda.empty_cache()
+
+    # RMSNorm over the residual stream [S, B, 768] bf16 with a bf16 weight (the
+    # model's after the optimizer takes its parameters), core/normalization.py:13-25.
+    # Inputs cycle through NC copies (NC * 12.6 MB > the 256 MB Infinity Cache),
+    # so every launch reads HBM.
+    H, NC = 768, 24
+    gen = torch.Generator(device=dev).manual_seed(4)
+    xs = [torch.randn(rows, H, generator=gen, device=dev).to(torch.bfloat16) for _ in range(NC)]
+    dys = [torch.randn(rows, H, generator=gen, device=dev).to(torch.bfloat16) for _ in range(NC)]
+    outs = [torch.empty(rows, H, dtype=torch.bfloat16, device=dev) for _ in range(NC)]
+    w = (1 + 0.1 * torch.randn(H, generator=gen, device=dev)).to(torch.bfloat16)
+    dw = torch.empty_like(w)
+    rstd = torch.empty(rows, dtype=torch.float32, device=dev)
+    ws = torch.empty(_lib.rmsnorm_workspace(rows, H), dtype=torch.float32, device=dev)
+    fwd_args = [(dt, dt, rows, H, 1e-6, P(xs[i]), H, P(w), P(outs[i]), H, P(rstd), sp)
+                for i in range(NC)]
+    bwd_args = [(dt, dt, rows, H, P(xs[i]), H, P(w), P(rstd), P(dys[i]), H, P(outs[i]), H, P(dw),
+                 P(ws), ws.numel(), sp) for i in range(NC)]
+    for name, fn, arglist, nbytes in (
+            ("rmsnorm_fwd", lib.mi_rmsnorm_fwd, fwd_args, 2 * rows * H * 2 + rows * 4 + H * 2),
+            ("rmsnorm_bwd", lib.mi_rmsnorm_bwd, bwd_args,
+             3 * rows * H * 2 + rows * 4 + 2 * H * 2)):
+        us = _time_rotating(stream, fn, arglist, 4 * NC, name)
+        gbps = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"bound": "hbm", "avg_us": round(us, 2), "achieved": round(gbps, 1),
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                     "algorithmic_bytes": nbytes, "shape": f"[{rows}, {H}] bf16",
+                     "traffic": read_traffic(name, "traffic_model_ops_c5.txt")}
+    del xs, dys, outs
     torch.cuda.empty_cache()
     return out
 
@@ -163,7 +213,7 @@ def gpt_train(dev, steps=20, warmup=3):
     vocab 50257, B=8, S=1024, TP=1, DP=1) with attention and RoPE on the HIP
     kernels; tokens/s = B*S*steps / wall time (train.py:196-198), beside the
     same step with attention done by plain PyTorch matmul/softmax (fp32 math)
-    and the loss by eager torch ops."""
+    and the loss and RMSNorm by the reference's eager torch ops."""
     import torch
     from gpt_from_scratch_amd.harness import GPTConfig, SoftmaxCrossEntropy, train
 
@@ -177,13 +227,15 @@ def gpt_train(dev, steps=20, warmup=3):
     cfg = GPTConfig()
     losses, tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup)
     _, eager_tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup,
-                         attention=eager_attention, loss_fn=SoftmaxCrossEntropy.apply)
+                         attention=eager_attention, loss_fn=SoftmaxCrossEntropy.apply,
+                         eager_ops=True)
     return {"workload": "config 5: 12L/768/12H SwiGLU RMSNorm vocab 50257, B8 S1024, bf16 params "
                         "+ fp32 AdamW master, TP=1 DP=1, synthetic uint16 ids",
             "steps": steps, "tokens_per_s": round(tps, 1),
             "ms_per_step": round(8 * 1024 / tps * 1e3, 3),
             "tokens_per_s_eager": round(eager_tps, 1),
-            "eager": "attention as torch matmul/softmax (fp32 math), loss as eager torch ops",
+            "eager": "attention as torch matmul/softmax (fp32 math); loss and RMSNorm as the "
+                     "reference's eager torch ops",
             "loss_first": round(losses[0], 4), "loss_last": round(losses[-1], 4)}
 
 
@@ -308,6 +360,20 @@ def main():
     rope_us = r0.elapsed_time(r1) / n_rope * 1e3
     rope_bytes = 4 * B * S * H * D * 2 + 2 * S * (D // 2) * 2
     rope_gbps = rope_bytes / (rope_us * 1e-6) / 1e9
+    # The loop above re-reads one q/k pair, which stays in the 256 MB Infinity
+    # Cache (as the projection's fresh output would in the model).  The same
+    # launch cycling through 12 qkv copies (453 MB) reads HBM:
+    NQ = 12
+    qkvs = [torch.randn(S, B, 3, H, D, generator=g).to(torch.bfloat16).to(dev) for _ in range(NQ)]
+    cold_args = []
+    for t in qkvs:
+        cq, ck, _ = t.unbind(2)
+        cold_args.append((_lib.dtype_code(cq), _lib.dtype_code(cos), S, B, H, D, 0, P(cq), ST(cq),
+                          P(ck), ST(ck), P(cos), ST2(cos), P(sin), ST2(sin), P(rq), ST(rq), P(rk),
+                          ST(rk), sp))
+    rope_cold_us = _time_rotating(stream, lib.mi_rope_qk, cold_args, 8 * NQ, "rope_qk")
+    rope_cold_gbps = rope_bytes / (rope_cold_us * 1e-6) / 1e9
+    del qkvs
 
     model_ops = {} if args.no_model_ops else model_ops_bench(dev, lib)
 
@@ -336,7 +402,10 @@ def main():
         "rope": {"bound": "hbm", "avg_us": round(rope_us, 3), "achieved": round(rope_gbps, 1),
                  "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                  "frac": round(rope_gbps / PEAK_HBM_GBPS, 4), "algorithmic_bytes": rope_bytes,
-                 "traffic": read_traffic("rope_qk")},
+                 "traffic": read_traffic("rope_qk"), "inputs": "one q/k pair (cache-resident)",
+                 "cold": {"avg_us": round(rope_cold_us, 3), "achieved": round(rope_cold_gbps, 1),
+                          "frac": round(rope_cold_gbps / PEAK_HBM_GBPS, 4),
+                          "inputs": "12 rotating qkv copies (HBM)"}},
     }
     if model_ops:
         out["model_ops"] = model_ops

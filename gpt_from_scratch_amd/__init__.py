@@ -1,13 +1,14 @@
 """MI355X-native attention hot path of gpt_from_scratch.
 
 Drop-ins for the reference's kernels (core/myFlashAttn.py, core/rope_triton.py,
-core/position_embeddings.py) and its vocabulary cross entropy
-(core/tensor_parallel/loss.py), backed by hand-written gfx950 HIP kernels in
+core/position_embeddings.py), its vocabulary cross entropy
+(core/tensor_parallel/loss.py) and RMSNorm (core/normalization.py), backed by hand-written gfx950 HIP kernels in
 libmi_attn.so behind the C ABI of include/mi_attn.h.
 """
 from .attention_block import AttentionBlock, attention_block
 from .cross_entropy import (VocabParallelCrossEntropy, _VocabParallelCrossEntropy,
                             vocab_parallel_cross_entropy)
+from .normalization import FusedRMSNorm, RMSNorm, rms_norm
 from .flash_attn import FlashAttn, apply_flash_attn, flash_attn_backward, flash_attn_forward
 from .position_embeddings import RotaryEmbedding
 from .rope import RoPE, RoPEQK, TritonRoPE, apply_rope, apply_rope_qk
@@ -17,4 +18,5 @@ __all__ = [
     "RotaryEmbedding", "RoPE", "RoPEQK", "TritonRoPE", "apply_rope", "apply_rope_qk",
     "AttentionBlock", "attention_block",
     "VocabParallelCrossEntropy", "_VocabParallelCrossEntropy", "vocab_parallel_cross_entropy",
+    "RMSNorm", "FusedRMSNorm", "rms_norm",
 ]

@@ -24,7 +24,8 @@ _DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 # Every function declared in include/mi_attn.h.
 EXPORTED = ("mi_version", "mi_status_str", "mi_last_error", "mi_attn_fwd", "mi_attn_bwd",
             "mi_attn_bwd_preprocess", "mi_attn_bwd_grads", "mi_attn_bwd_dkdv", "mi_attn_bwd_dq",
-            "mi_rope", "mi_rope_qk", "mi_xent_fwd", "mi_xent_bwd")
+            "mi_rope", "mi_rope_qk", "mi_xent_fwd", "mi_xent_bwd", "mi_rmsnorm_fwd",
+            "mi_rmsnorm_bwd_workspace", "mi_rmsnorm_bwd")
 
 _lib = None
 
@@ -72,6 +73,12 @@ def _declare(lib):
     lib.mi_xent_fwd.argtypes = [i, i64, i64, p, i64, p, p, p, p]
     lib.mi_xent_bwd.restype = i
     lib.mi_xent_bwd.argtypes = [i, i64, i64, p, i64, p, p, p, p, i64, p]
+    lib.mi_rmsnorm_fwd.restype = i
+    lib.mi_rmsnorm_fwd.argtypes = [i, i, i64, i64, f, p, i64, p, p, i64, p, p]
+    lib.mi_rmsnorm_bwd_workspace.restype = i64
+    lib.mi_rmsnorm_bwd_workspace.argtypes = [i64, i64]
+    lib.mi_rmsnorm_bwd.restype = i
+    lib.mi_rmsnorm_bwd.argtypes = [i, i, i64, i64, p, i64, p, p, p, i64, p, i64, p, p, i64, p]
 
 
 def lib():
@@ -211,3 +218,29 @@ def xent_bwd(logits, target, lse, grad_loss, grad):
                            _ptr(target), _ptr(lse), _ptr(grad_loss), _ptr(grad), grs,
                            _stream(logits))
     _check(st, "mi_xent_bwd")
+
+
+def rmsnorm_fwd(x, weight, eps: float, y, rstd):
+    """Enqueue the RMSNorm forward over the last dim: y, rstd [rows] fp32."""
+    _require_gpu(x, weight, y, rstd)
+    rows, xs = _rows(x)
+    _, ys = _rows(y)
+    st = lib().mi_rmsnorm_fwd(dtype_code(x), dtype_code(weight), rows, x.shape[-1], float(eps),
+                              _ptr(x), xs, _ptr(weight), _ptr(y), ys, _ptr(rstd), _stream(x))
+    _check(st, "mi_rmsnorm_fwd")
+
+
+def rmsnorm_workspace(rows: int, hidden: int) -> int:
+    return int(lib().mi_rmsnorm_bwd_workspace(rows, hidden))
+
+
+def rmsnorm_bwd(x, weight, rstd, dy, dx, dweight, workspace):
+    """Enqueue the RMSNorm backward: dx (x's shape and dtype), dweight [hidden]."""
+    _require_gpu(x, weight, rstd, dy, dx, dweight, workspace)
+    rows, xs = _rows(x)
+    _, dys = _rows(dy)
+    _, dxs = _rows(dx)
+    st = lib().mi_rmsnorm_bwd(dtype_code(x), dtype_code(weight), rows, x.shape[-1], _ptr(x), xs,
+                              _ptr(weight), _ptr(rstd), _ptr(dy), dys, _ptr(dx), dxs,
+                              _ptr(dweight), _ptr(workspace), workspace.numel(), _stream(x))
+    _check(st, "mi_rmsnorm_bwd")

@@ -5,6 +5,9 @@
 // VALU otherwise) and reports failures as status codes plus a per-thread
 // message.  No allocation, no synchronisation, no global mutable state apart
 // from the thread-local error text.
+#include <cmath>
+#include <initializer_list>
+#include <utility>
 #include <stdarg.h>
 #include <stdio.h>
 #include <string.h>
@@ -434,6 +437,115 @@ mi_status mi_xent_bwd(mi_dtype dtype, int64_t rows, int64_t vocab, const void* l
   a.grad = grad_logits;
   a.grad_row_stride = grad_row_stride;
   return launched(mi::launch_xent_bwd(dtype, a, (hipStream_t)stream), "xent_bwd");
+}
+
+static bool rms_dtypes_ok(int x_dtype, int w_dtype) {
+  return dtype_ok(x_dtype) && (w_dtype == x_dtype || w_dtype == MI_F32);
+}
+
+static mi_status rms_common(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                            const void* x, int64_t x_row_stride, const void* weight,
+                            mi::RmsArgs& a) {
+  if (!rms_dtypes_ok(x_dtype, w_dtype))
+    return fail(MI_ERR_INVALID_ARGUMENT,
+                "dtypes (x %d, weight %d): weight must have x's dtype or be fp32", x_dtype,
+                w_dtype);
+  if (rows <= 0 || hidden <= 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "sizes must be positive (rows=%lld hidden=%lld)",
+                (long long)rows, (long long)hidden);
+  if ((rows + 3) / 4 >= (1ll << 31))
+    return fail(MI_ERR_UNSUPPORTED, "rows = %lld too many for one launch", (long long)rows);
+  if (x_row_stride < hidden)
+    return fail(MI_ERR_INVALID_ARGUMENT, "x row stride %lld < hidden %lld",
+                (long long)x_row_stride, (long long)hidden);
+  if (!x || !weight) return fail(MI_ERR_INVALID_ARGUMENT, "x / weight: null pointer");
+  if (((uintptr_t)x) % elem_size(x_dtype) || ((uintptr_t)weight) % elem_size(w_dtype))
+    return fail(MI_ERR_INVALID_ARGUMENT, "x / weight: misaligned");
+  a = {};
+  a.rows = rows;
+  a.hidden = hidden;
+  a.x = x;
+  a.x_stride = x_row_stride;
+  a.w = weight;
+  return MI_OK;
+}
+
+// 4-element vectors: every row of every tensor starts on a 4-element boundary.
+static bool rms_vec_ok(int64_t hidden, std::initializer_list<std::pair<const void*, int64_t>> rows,
+                       std::initializer_list<std::pair<const void*, int>> bases) {
+  if (hidden % 4) return false;
+  for (auto& b : bases)
+    if (((uintptr_t)b.first) % (4 * b.second)) return false;
+  for (auto& r : rows)
+    if (r.second % 4) return false;
+  return true;
+}
+
+mi_status mi_rmsnorm_fwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                         float eps, const void* x, int64_t x_row_stride, const void* weight,
+                         void* y, int64_t y_row_stride, float* rstd, void* stream) {
+  mi::RmsArgs a;
+  if (mi_status st = rms_common(x_dtype, w_dtype, rows, hidden, x, x_row_stride, weight, a))
+    return st;
+  if (!(eps >= 0.f) || !std::isfinite(eps))
+    return fail(MI_ERR_INVALID_ARGUMENT, "eps must be a finite number >= 0");
+  const int y_dtype = w_dtype == MI_F32 ? MI_F32 : x_dtype;
+  if (!y || !rstd) return fail(MI_ERR_INVALID_ARGUMENT, "y / rstd: null pointer");
+  if (y_row_stride < hidden)
+    return fail(MI_ERR_INVALID_ARGUMENT, "y row stride %lld < hidden %lld",
+                (long long)y_row_stride, (long long)hidden);
+  if (((uintptr_t)y) % elem_size(y_dtype) || ((uintptr_t)rstd) % 4)
+    return fail(MI_ERR_INVALID_ARGUMENT, "y / rstd: misaligned");
+  a.eps = eps;
+  a.y = y;
+  a.y_stride = y_row_stride;
+  a.rstd = rstd;
+  const bool vec = rms_vec_ok(hidden, {{x, x_row_stride}, {y, y_row_stride}},
+                              {{x, elem_size(x_dtype)}, {y, elem_size(y_dtype)},
+                               {weight, elem_size(w_dtype)}});
+  return launched(mi::launch_rmsnorm_fwd(x_dtype, w_dtype, a, vec, (hipStream_t)stream),
+                  "rmsnorm_fwd");
+}
+
+int64_t mi_rmsnorm_bwd_workspace(int64_t rows, int64_t hidden) {
+  if (rows <= 0 || hidden <= 0) return 0;
+  return mi::rmsnorm_parts(rows) * hidden;
+}
+
+mi_status mi_rmsnorm_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                         const void* x, int64_t x_row_stride, const void* weight,
+                         const float* rstd, const void* dy, int64_t dy_row_stride, void* dx,
+                         int64_t dx_row_stride, void* dweight, float* workspace,
+                         int64_t workspace_elems, void* stream) {
+  mi::RmsArgs a;
+  if (mi_status st = rms_common(x_dtype, w_dtype, rows, hidden, x, x_row_stride, weight, a))
+    return st;
+  const int y_dtype = w_dtype == MI_F32 ? MI_F32 : x_dtype;
+  if (!rstd || !dy || !dx || !dweight || !workspace)
+    return fail(MI_ERR_INVALID_ARGUMENT, "rstd / dy / dx / dweight / workspace: null pointer");
+  if (dy_row_stride < hidden || dx_row_stride < hidden)
+    return fail(MI_ERR_INVALID_ARGUMENT, "dy / dx row stride < hidden %lld", (long long)hidden);
+  if (((uintptr_t)rstd) % 4 || ((uintptr_t)workspace) % 4 ||
+      ((uintptr_t)dy) % elem_size(y_dtype) || ((uintptr_t)dx) % elem_size(x_dtype) ||
+      ((uintptr_t)dweight) % elem_size(w_dtype))
+    return fail(MI_ERR_INVALID_ARGUMENT, "rstd / dy / dx / dweight / workspace: misaligned");
+  const int64_t need = mi_rmsnorm_bwd_workspace(rows, hidden);
+  if (workspace_elems < need)
+    return fail(MI_ERR_INVALID_ARGUMENT, "workspace holds %lld floats, %lld needed",
+                (long long)workspace_elems, (long long)need);
+  a.rstd = (float*)rstd;
+  a.dy = dy;
+  a.dy_stride = dy_row_stride;
+  a.dx = dx;
+  a.dx_stride = dx_row_stride;
+  a.dw = dweight;
+  a.partial = workspace;
+  a.parts = (int)mi::rmsnorm_parts(rows);
+  const bool vec = rms_vec_ok(hidden, {{x, x_row_stride}, {dy, dy_row_stride}, {dx, dx_row_stride}},
+                              {{x, elem_size(x_dtype)}, {dy, elem_size(y_dtype)},
+                               {dx, elem_size(x_dtype)}, {weight, elem_size(w_dtype)}});
+  return launched(mi::launch_rmsnorm_bwd(x_dtype, w_dtype, a, vec, (hipStream_t)stream),
+                  "rmsnorm_bwd");
 }
 
 }  // extern "C"

@@ -76,4 +76,30 @@ struct XentArgs {
 hipError_t launch_xent_fwd(int dtype, const XentArgs& a, hipStream_t st);
 hipError_t launch_xent_bwd(int dtype, const XentArgs& a, hipStream_t st);
 
+// RMSNorm over rows of `hidden` elements (model_ops.hip).
+struct RmsArgs {
+  int64_t rows, hidden;
+  float eps;
+  const void* x;
+  int64_t x_stride;
+  const void* w;  // [hidden], x's dtype or fp32
+  void* y;        // forward output, the promoted dtype
+  int64_t y_stride;
+  float* rstd;    // [rows] fp32, written by forward, read by backward
+  const void* dy;
+  int64_t dy_stride;
+  void* dx;
+  int64_t dx_stride;
+  void* dw;        // [hidden], w's dtype
+  float* partial;  // [parts, hidden] fp32 workspace of the backward
+  int parts;
+};
+
+// Number of dw partial rows the backward uses for `rows` rows (<= 256).
+int64_t rmsnorm_parts(int64_t rows);
+hipError_t launch_rmsnorm_fwd(int x_dtype, int w_dtype, const RmsArgs& a, bool vec,
+                              hipStream_t st);
+hipError_t launch_rmsnorm_bwd(int x_dtype, int w_dtype, const RmsArgs& a, bool vec,
+                              hipStream_t st);
+
 }  // namespace mi

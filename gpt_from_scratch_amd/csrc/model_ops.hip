@@ -1,19 +1,21 @@
 // model_ops.hip — the train step's bandwidth-bound operators around the
-// attention path, fused into single passes over HBM.
+// attention path, each fused into the fewest passes over HBM.
 //
 // Softmax cross entropy over the vocabulary (`_VocabParallelCrossEntropy` at one
-// tensor-parallel rank, core/tensor_parallel/loss.py:8-72):
+// tensor-parallel rank, core/tensor_parallel/loss.py:9-72):
 //   forward:  loss[r] = log sum_j exp(z_rj - m_r) - (z_r,t - m_r), m_r = max_j z_rj
-//             (:13-43; a target outside [0, vocab) is masked: its logit counts as
-//             0 after the shift, :29-35); the log-sum-exp lse_r = m_r + log(sum)
-//             is kept for the backward instead of the whole softmax (:47-50);
-//   backward: dz_rj = (exp(z_rj - lse_r) - [j == t_r]) * dloss_r   (:58-72).
+//             (:14-50; a target outside [0, vocab) is masked: its logit counts as
+//             0 after the shift, :33-41); the log-sum-exp lse_r = m_r + log(sum)
+//             is kept for the backward instead of the whole softmax (:54-56);
+//   backward: dz_rj = (exp(z_rj - lse_r) - [j == t_r]) * dloss_r   (:59-72).
 // One workgroup per row.  The reference computes in the logits' dtype; here the
 // row statistics and the softmax are fp32 and only the outputs are rounded.
 //
 // Logits rows of a vocabulary of odd length are not 16-byte aligned, so each
 // row is split into a scalar head up to the first 16-byte boundary, a body of
 // 16-byte vectors and a scalar tail.
+//
+// RMSNorm (core/normalization.py:13-25): further below.
 #include "mi_device.h"
 #include "mi_kernels.h"
 
@@ -233,6 +235,416 @@ hipError_t launch_xent_bwd(int dtype, const XentArgs& a, hipStream_t st) {
     hipLaunchKernelGGL(xent_bwd_kernel<2>, grid, block, 0, st, a.logits, a.row_stride, a.vocab,
                        a.target, a.lse, a.grad_loss, a.grad, a.grad_row_stride, vec_ok);
   return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// RMSNorm over the last dim (RMSNorm.forward, core/normalization.py:13-25):
+//   r_i = rsqrt(mean_j x_ij^2 + eps)              fp32 (:15-21)
+//   y_ij = round_x(x_ij * r_i) * w_j              rounded to x's dtype (:23), then
+//                                                 multiplied in the promoted dtype (:24)
+// The forward saves r (fp32, one per row) for the backward:
+//   dn_ij = dy_ij * w_j
+//   dx_ij = r_i dn_ij - x_ij r_i^3 (sum_j dn_ij x_ij) / H
+//   dw_j  = sum_i dy_ij * round_x(x_ij r_i)
+// dw is reduced deterministically: each backward workgroup writes the partial
+// sum of its rows to a [parts, H] fp32 workspace, and a second kernel sums the
+// parts of each column in a fixed order.  `parts` depends only on the row
+// count, so results are bitwise reproducible across devices.
+//
+// Fast path: H % 4 == 0, rows 4-element aligned, H <= 4096 (forward) or 2048
+// (backward).  One wave per row,
+// 4 consecutive elements per lane and chunk (8-byte loads for 16-bit types),
+// the row cached in registers.  Anything else takes the scalar path.
+// ---------------------------------------------------------------------------
+namespace {
+
+template <int DT>
+__device__ __forceinline__ float round_to(float v) {
+  if constexpr (DT == 0) return v;
+  else if constexpr (DT == 2) return __uint_as_float(((uint32_t)f32_to_bf16(v)) << 16);
+  else return f16_to_f32(f32_to_f16(v));
+}
+
+template <int DT>
+__device__ __forceinline__ void ld4(const void* row, int64_t i, float (&v)[4]) {
+  if constexpr (DT == 0) {
+    const f32x4 q = *(const f32x4*)((const float*)row + i);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = q[e];
+  } else {
+    const u32x2 q = *(const u32x2*)((const uint16_t*)row + i);
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      if constexpr (DT == 2) {
+        v[2 * e] = __uint_as_float(q[e] << 16);
+        v[2 * e + 1] = __uint_as_float(q[e] & 0xffff0000u);
+      } else {
+        v[2 * e] = f16_to_f32((uint16_t)(q[e] & 0xffffu));
+        v[2 * e + 1] = f16_to_f32((uint16_t)(q[e] >> 16));
+      }
+    }
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ void st4(void* row, int64_t i, const float (&v)[4]) {
+  if constexpr (DT == 0) {
+    f32x4 q;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) q[e] = v[e];
+    *(f32x4*)((float*)row + i) = q;
+  } else {
+    u32x2 q;
+    if constexpr (DT == 2) {
+      q[0] = BF16::pack2(v[0], v[1]);
+      q[1] = BF16::pack2(v[2], v[3]);
+    } else {
+      q[0] = F16::pack2(v[0], v[1]);
+      q[1] = F16::pack2(v[2], v[3]);
+    }
+    *(u32x2*)((uint16_t*)row + i) = q;
+  }
+}
+
+template <int DT>
+__device__ __forceinline__ const void* row_ptr(const void* base, int64_t row, int64_t stride) {
+  return (const char*)base + row * stride * (DT == 0 ? 4 : 2);
+}
+template <int DT>
+__device__ __forceinline__ void* row_ptr(void* base, int64_t row, int64_t stride) {
+  return (char*)base + row * stride * (DT == 0 ? 4 : 2);
+}
+
+// Sum over the 64 lanes, the same bits in every lane: DPP butterflies within
+// each row of 16 lanes (xor 1, xor 2, mirror within 8, mirror within 16), then
+// the row pairs (lane ^ 16) and the halves (lane ^ 32) by permlane swaps.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF,
+                                                        false));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  return sum_halves(v);
+}
+
+// y dtype: the promotion of x's dtype and w's dtype (w is x's dtype or fp32)
+template <int DT, int WDT>
+struct RmsTypes {
+  static constexpr int YDT = WDT == 0 ? 0 : DT;
+};
+
+// Waves per backward workgroup: 16 while the row, w and the dw partial fit in
+// 128 registers (C <= 4 chunks), else 8 with w re-read from cache per row.
+constexpr int RMS_PARTS_ROWS = 16;  // rows per dw partial at most, before the cap
+template <int C>
+struct RmsBwdCfg {
+  static constexpr int W = C <= 4 ? 16 : 8;
+  static constexpr bool CACHE_W = C <= 4;
+};
+
+template <int DT, int WDT, int C>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_vec_kernel(RmsArgs a) {
+  constexpr int YDT = RmsTypes<DT, WDT>::YDT;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;  // whole waves only; the kernel has no barrier
+  const int nq = (int)(a.hidden / 4);
+  const void* xr = row_ptr<DT>(a.x, row, a.x_stride);
+  float v[C][4], w[C][4];
+  float ss = 0.f;
+  // x and w requested together: one memory round trip before the reduction
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int q = c * 64 + lane;
+    if (q < nq) {
+      ld4<DT>(xr, 4 * q, v[c]);
+      ld4<WDT>(a.w, 4 * q, w[c]);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int q = c * 64 + lane;
+    if (q < nq) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) ss = __builtin_fmaf(v[c][e], v[c][e], ss);
+    }
+  }
+  ss = wave_sum(ss);
+  const float r = __builtin_amdgcn_rsqf(ss / (float)a.hidden + a.eps);
+  void* yr = row_ptr<YDT>(a.y, row, a.y_stride);
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int q = c * 64 + lane;
+    if (q < nq) {
+      float y[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) y[e] = round_to<DT>(v[c][e] * r) * w[c][e];
+      st4<YDT>(yr, 4 * q, y);
+    }
+  }
+  if (lane == 0) a.rstd[row] = r;
+}
+
+template <int DT, int WDT>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_scalar_kernel(RmsArgs a) {
+  constexpr int YDT = RmsTypes<DT, WDT>::YDT;
+  typedef typename Store<DT>::type T;
+  typedef typename Store<WDT>::type TW;
+  typedef typename Store<YDT>::type TY;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const T* xr = (const T*)a.x + row * a.x_stride;
+  float ss = 0.f;
+  for (int64_t j = lane; j < a.hidden; j += 64) {
+    const float v = Store<DT>::ld(xr, j);
+    ss = __builtin_fmaf(v, v, ss);
+  }
+  ss = wave_sum(ss);
+  const float r = __builtin_amdgcn_rsqf(ss / (float)a.hidden + a.eps);
+  TY* yr = (TY*)a.y + row * a.y_stride;
+  for (int64_t j = lane; j < a.hidden; j += 64)
+    Store<YDT>::st(yr, j, round_to<DT>(Store<DT>::ld(xr, j) * r) * Store<WDT>::ld((const TW*)a.w, j));
+  if (lane == 0) a.rstd[row] = r;
+}
+
+// dx for every row, and this workgroup's partial dw into partial[blockIdx.x].
+template <int DT, int WDT, int C>
+__global__ __launch_bounds__(64 * RmsBwdCfg<C>::W) void rmsnorm_bwd_vec_kernel(RmsArgs a) {
+  constexpr int YDT = RmsTypes<DT, WDT>::YDT;
+  constexpr int W = RmsBwdCfg<C>::W;
+  constexpr bool CACHE_W = RmsBwdCfg<C>::CACHE_W;
+  constexpr int CS = C < 8 ? C : 8;  // chunks per LDS reduction slice
+  __shared__ float red[W][CS * 256];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int nq = (int)(a.hidden / 4);
+  const float inv_h = 1.f / (float)a.hidden;
+  float w[CACHE_W ? C : 1][4], acc[C][4];
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int q = c * 64 + lane;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[c][e] = 0.f;
+    if constexpr (CACHE_W) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) w[c][e] = 0.f;
+      if (q < nq) ld4<WDT>(a.w, 4 * q, w[c]);
+    }
+  }
+  const int64_t stride = (int64_t)gridDim.x * W;
+  for (int64_t row = (int64_t)blockIdx.x * W + wave; row < a.rows; row += stride) {
+    const void* xr = row_ptr<DT>(a.x, row, a.x_stride);
+    const void* dyr = row_ptr<YDT>(a.dy, row, a.dy_stride);
+    float x[C][4], dn[C][4];
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int q = c * 64 + lane;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[c][e] = dn[c][e] = 0.f;
+      if (q < nq) {
+        ld4<DT>(xr, 4 * q, x[c]);
+        ld4<YDT>(dyr, 4 * q, dn[c]);
+      }
+    }
+    const float r = a.rstd[row];
+    float s = 0.f;
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float dy = dn[c][e];
+        acc[c][e] = __builtin_fmaf(dy, round_to<DT>(x[c][e] * r), acc[c][e]);
+        float wv;
+        if constexpr (CACHE_W) {
+          wv = w[c][e];
+        } else {
+          const int64_t j = 4 * (c * 64 + lane) + e;
+          wv = j < a.hidden ? Store<WDT>::ld((const typename Store<WDT>::type*)a.w, j) : 0.f;
+        }
+        dn[c][e] = dy * wv;
+        s = __builtin_fmaf(dn[c][e], x[c][e], s);
+      }
+    s = wave_sum(s);
+    const float k = r * r * r * s * inv_h;
+    void* dxr = row_ptr<DT>(a.dx, row, a.dx_stride);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int q = c * 64 + lane;
+      if (q < nq) {
+        float d[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d[e] = __builtin_fmaf(r, dn[c][e], -x[c][e] * k);
+        st4<DT>(dxr, 4 * q, d);
+      }
+    }
+  }
+  // partial dw of this workgroup: sum the waves in a fixed order
+  float* part = a.partial + (int64_t)blockIdx.x * a.hidden;
+#pragma unroll
+  for (int s0 = 0; s0 < C; s0 += CS) {
+#pragma unroll
+    for (int c = s0; c < s0 + CS && c < C; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) red[wave][4 * ((c - s0) * 64 + lane) + e] = acc[c][e];
+    __syncthreads();
+    for (int j = threadIdx.x; j < CS * 256; j += 64 * W) {
+      const int64_t col = (int64_t)s0 * 256 + j;
+      if (col < a.hidden) {
+        float t = 0.f;
+#pragma unroll
+        for (int v = 0; v < W; ++v) t += red[v][j];
+        part[col] = t;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+template <int DT, int WDT>
+__global__ __launch_bounds__(256) void rmsnorm_bwd_dx_scalar_kernel(RmsArgs a) {
+  constexpr int YDT = RmsTypes<DT, WDT>::YDT;
+  typedef typename Store<DT>::type T;
+  typedef typename Store<WDT>::type TW;
+  typedef typename Store<YDT>::type TY;
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= a.rows) return;
+  const T* xr = (const T*)a.x + row * a.x_stride;
+  const TY* dyr = (const TY*)a.dy + row * a.dy_stride;
+  const TW* wr = (const TW*)a.w;
+  const float r = a.rstd[row];
+  float s = 0.f;
+  for (int64_t j = lane; j < a.hidden; j += 64)
+    s = __builtin_fmaf(Store<YDT>::ld(dyr, j) * Store<WDT>::ld(wr, j), Store<DT>::ld(xr, j), s);
+  s = wave_sum(s);
+  const float k = r * r * r * s / (float)a.hidden;
+  T* dxr = (T*)a.dx + row * a.dx_stride;
+  // every element of the row is read above before any is written below, so
+  // dx may alias dy (same stride)
+  for (int64_t j = lane; j < a.hidden; j += 64) {
+    const float dn = Store<YDT>::ld(dyr, j) * Store<WDT>::ld(wr, j);
+    Store<DT>::st(dxr, j, __builtin_fmaf(r, dn, -Store<DT>::ld(xr, j) * k));
+  }
+}
+
+// partial[p][col] = sum over rows [p*rpp, (p+1)*rpp) of dy * round_x(x r)
+template <int DT, int WDT>
+__global__ __launch_bounds__(256) void rmsnorm_dw_partial_scalar_kernel(RmsArgs a, int64_t rpp) {
+  constexpr int YDT = RmsTypes<DT, WDT>::YDT;
+  typedef typename Store<DT>::type T;
+  typedef typename Store<YDT>::type TY;
+  const int64_t col = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (col >= a.hidden) return;
+  const int64_t r0 = (int64_t)blockIdx.y * rpp;
+  const int64_t r1 = min(r0 + rpp, a.rows);
+  float t = 0.f;
+  for (int64_t row = r0; row < r1; ++row) {
+    const float n = round_to<DT>(Store<DT>::ld((const T*)a.x + row * a.x_stride, col) * a.rstd[row]);
+    t = __builtin_fmaf(Store<YDT>::ld((const TY*)a.dy + row * a.dy_stride, col), n, t);
+  }
+  a.partial[(int64_t)blockIdx.y * a.hidden + col] = t;
+}
+
+// dw[col] = sum_p partial[p][col], p in increasing order within 16 strided
+// groups, then the 16 group sums in order.
+template <int WDT>
+__global__ __launch_bounds__(1024) void rmsnorm_dw_reduce_kernel(RmsArgs a) {
+  typedef typename Store<WDT>::type TW;
+  __shared__ float red[16][65];
+  const int cl = threadIdx.x & 63, g = threadIdx.x >> 6;
+  const int64_t col = (int64_t)blockIdx.x * 64 + cl;
+  float t = 0.f;
+  if (col < a.hidden) {
+#pragma unroll 16
+    for (int p = g; p < a.parts; p += 16) t += a.partial[(int64_t)p * a.hidden + col];
+  }
+  red[g][cl] = t;
+  __syncthreads();
+  if (g == 0 && col < a.hidden) {
+    float u = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) u += red[k][cl];
+    Store<WDT>::st((TW*)a.dw, col, u);
+  }
+}
+
+// The forward's vector path covers H <= 64 * 4 * 16; the backward's, which also
+// holds dy and the dw partial in registers, H <= 64 * 4 * 8 (beyond, it spills).
+constexpr int64_t RMS_VEC_FWD_MAX = 4096, RMS_VEC_BWD_MAX = 2048;
+
+template <int DT, int WDT, int C>
+void launch_rms_vec(bool fwd, const RmsArgs& a, hipStream_t st) {
+  if (fwd)
+    hipLaunchKernelGGL((rmsnorm_fwd_vec_kernel<DT, WDT, C>), dim3((unsigned)((a.rows + 3) / 4)),
+                       dim3(256), 0, st, a);
+  else if constexpr (C <= 8)
+    hipLaunchKernelGGL((rmsnorm_bwd_vec_kernel<DT, WDT, C>), dim3((unsigned)a.parts),
+                       dim3(64 * RmsBwdCfg<C>::W), 0, st, a);
+}
+
+template <int DT, int WDT>
+hipError_t launch_rms_dt(bool fwd, const RmsArgs& a, bool vec, hipStream_t st) {
+  const int64_t nq = a.hidden / 4;
+  if (a.hidden > (fwd ? RMS_VEC_FWD_MAX : RMS_VEC_BWD_MAX)) vec = false;
+  if (vec) {
+    // smallest instantiated chunk count covering the row
+    if (nq <= 64) launch_rms_vec<DT, WDT, 1>(fwd, a, st);
+    else if (nq <= 128) launch_rms_vec<DT, WDT, 2>(fwd, a, st);
+    else if (nq <= 192) launch_rms_vec<DT, WDT, 3>(fwd, a, st);
+    else if (nq <= 256) launch_rms_vec<DT, WDT, 4>(fwd, a, st);
+    else if (nq <= 384) launch_rms_vec<DT, WDT, 6>(fwd, a, st);
+    else if (nq <= 512) launch_rms_vec<DT, WDT, 8>(fwd, a, st);
+    else if (nq <= 768) launch_rms_vec<DT, WDT, 12>(fwd, a, st);
+    else launch_rms_vec<DT, WDT, 16>(fwd, a, st);
+  } else if (fwd) {
+    hipLaunchKernelGGL((rmsnorm_fwd_scalar_kernel<DT, WDT>), dim3((unsigned)((a.rows + 3) / 4)),
+                       dim3(256), 0, st, a);
+  } else {
+    // dw partials first: dx may overwrite dy
+    const int64_t rpp = (a.rows + a.parts - 1) / a.parts;
+    hipLaunchKernelGGL((rmsnorm_dw_partial_scalar_kernel<DT, WDT>),
+                       dim3((unsigned)((a.hidden + 255) / 256), (unsigned)a.parts), dim3(256), 0,
+                       st, a, rpp);
+    hipLaunchKernelGGL((rmsnorm_bwd_dx_scalar_kernel<DT, WDT>),
+                       dim3((unsigned)((a.rows + 3) / 4)), dim3(256), 0, st, a);
+  }
+  if (!fwd)
+    hipLaunchKernelGGL((rmsnorm_dw_reduce_kernel<WDT>), dim3((unsigned)((a.hidden + 63) / 64)),
+                       dim3(1024), 0, st, a);
+  return hipGetLastError();
+}
+
+hipError_t launch_rms(bool fwd, int x_dtype, int w_dtype, const RmsArgs& a, bool vec,
+                      hipStream_t st) {
+  if (x_dtype == 2 && w_dtype == 2) return launch_rms_dt<2, 2>(fwd, a, vec, st);
+  if (x_dtype == 2 && w_dtype == 0) return launch_rms_dt<2, 0>(fwd, a, vec, st);
+  if (x_dtype == 1 && w_dtype == 1) return launch_rms_dt<1, 1>(fwd, a, vec, st);
+  if (x_dtype == 1 && w_dtype == 0) return launch_rms_dt<1, 0>(fwd, a, vec, st);
+  return launch_rms_dt<0, 0>(fwd, a, vec, st);
+}
+
+}  // namespace
+
+int64_t rmsnorm_parts(int64_t rows) {
+  const int64_t p = (rows + RMS_PARTS_ROWS - 1) / RMS_PARTS_ROWS;
+  return p < 1 ? 1 : (p > 256 ? 256 : p);
+}
+
+hipError_t launch_rmsnorm_fwd(int x_dtype, int w_dtype, const RmsArgs& a, bool vec,
+                              hipStream_t st) {
+  return launch_rms(true, x_dtype, w_dtype, a, vec, st);
+}
+
+hipError_t launch_rmsnorm_bwd(int x_dtype, int w_dtype, const RmsArgs& a, bool vec,
+                              hipStream_t st) {
+  return launch_rms(false, x_dtype, w_dtype, a, vec, st);
 }
 
 }  // namespace mi

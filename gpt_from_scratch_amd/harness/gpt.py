@@ -16,7 +16,7 @@ kernels run inside a real train step:
   comparison run can substitute other implementations; the defaults are the
   HIP kernels;
 * RMSNorm: fp32 mean square, rsqrt(ms + eps), cast back, times the weight
-  (core/normalization.py:13-25);
+  (core/normalization.py:13-25), by default the fused HIP kernels;
 * loss: softmax cross entropy on the (bf16) logits, mean over [S, B]
   (core/tensor_parallel/loss.py:9-72 at one rank; train.py:179-181), by
   default the fused HIP kernels (`loss_fn` injectable, e.g. the eager
@@ -28,7 +28,8 @@ kernels run inside a real train step:
 * init: xavier-uniform for every projection and the embedding
   (core/tensor_parallel/layers.py:31,66,112), RMSNorm weights 1.
 
-Everything here is ordinary PyTorch except the attention path and the loss.
+Everything here is ordinary PyTorch except the attention path, the loss and
+the RMSNorms.
 """
 from __future__ import annotations
 
@@ -42,6 +43,7 @@ import torch.nn.functional as F
 
 from ..attention_block import attention_block
 from ..cross_entropy import vocab_parallel_cross_entropy
+from ..normalization import rms_norm
 from ..flash_attn import apply_flash_attn
 from ..position_embeddings import RotaryEmbedding
 from ..rope import apply_rope_qk
@@ -67,12 +69,17 @@ def _xavier(out_features, in_features, device):
 
 
 class RMSNorm(nn.Module):
-    def __init__(self, hidden_size, eps, device):
+    """The HIP kernels by default; `eager=True` runs the reference's op sequence."""
+
+    def __init__(self, hidden_size, eps, device, eager=False):
         super().__init__()
         self.eps = eps
+        self.eager = eager
         self.weight = nn.Parameter(torch.ones(hidden_size, device=device, dtype=torch.float32))
 
     def forward(self, x):
+        if not self.eager:
+            return rms_norm(x, self.weight, self.eps)
         dtype = x.dtype
         xf = x.float()
         xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
@@ -121,11 +128,11 @@ class SwiGLU(nn.Module):
 
 
 class Block(nn.Module):
-    def __init__(self, cfg: GPTConfig, device, attention=None, rope=None):
+    def __init__(self, cfg: GPTConfig, device, attention=None, rope=None, eager_ops=False):
         super().__init__()
-        self.norm1 = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device)
+        self.norm1 = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager=eager_ops)
         self.attn = Attention(cfg, device, attention, rope)
-        self.norm2 = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device)
+        self.norm2 = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager=eager_ops)
         self.mlp = SwiGLU(cfg, device)
 
     def forward(self, x):
@@ -136,15 +143,15 @@ class Block(nn.Module):
 class GPT(nn.Module):
     """input ids [B, S] -> logits [S, B, V]."""
 
-    def __init__(self, cfg: GPTConfig, device, attention=None, rope=None):
+    def __init__(self, cfg: GPTConfig, device, attention=None, rope=None, eager_ops=False):
         super().__init__()
         self.cfg = cfg
         emb = torch.empty(cfg.vocab_size, cfg.hidden_size, device=device, dtype=torch.float32)
         nn.init.xavier_uniform_(emb)
         self.embedding = nn.Parameter(emb)
         self.blocks = nn.ModuleList(
-            [Block(cfg, device, attention, rope) for _ in range(cfg.num_layers)])
-        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device)
+            [Block(cfg, device, attention, rope, eager_ops) for _ in range(cfg.num_layers)])
+        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager=eager_ops)
         self.head = _xavier(cfg.vocab_size, cfg.hidden_size, device)
 
     def forward(self, ids):
@@ -225,14 +232,15 @@ def synthetic_batch(batch, seq, vocab, seed, device):
 
 
 def train(cfg: GPTConfig, batch=8, seq=1024, steps=20, seed=5, device="cuda", attention=None,
-          rope=None, warmup=0, loss_fn=None):
+          rope=None, warmup=0, loss_fn=None, eager_ops=False):
     """Build the model and optimizer from `seed`, run `warmup` untimed then
     `steps` timed train steps on one fixed synthetic batch.  Returns
     (losses, tokens_per_second).  `loss_fn(logits, target)` -> per-token loss
-    defaults to the HIP cross entropy."""
+    defaults to the HIP cross entropy; `eager_ops` swaps the model's other HIP
+    operators (RMSNorm) for the reference's eager op sequences."""
     loss_fn = loss_fn or vocab_parallel_cross_entropy
     torch.manual_seed(seed)
-    model = GPT(cfg, device, attention, rope)
+    model = GPT(cfg, device, attention, rope, eager_ops)
     opt = MixedPrecisionAdamW(model)
     inputs, labels = synthetic_batch(batch, seq, cfg.vocab_size, seed, device)
     labels_t = labels.transpose(0, 1).contiguous()

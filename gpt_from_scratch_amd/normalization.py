@@ -1,0 +1,89 @@
+"""RMSNorm in one HIP kernel each way.
+
+Drop-in for ``core/normalization.py`` (``RMSNorm(hidden_size, eps=1e-6)``, used
+by core/transformer_layer.py:77,83 and core/models/gpt.py:22).  The reference's
+forward is five eager passes over the activations (fp32 upcast, square, mean,
+scale, downcast, weight multiply) and its autograd backward saves the fp32
+copies.  Here:
+
+* forward: one read of x, one write of y, plus the fp32 ``rstd`` per row;
+  ``y = round_x(x * rstd) * weight`` with the same intermediate rounding to x's
+  dtype as the reference (normalization.py:23) and the product in the promoted
+  dtype (:24);
+* backward: one read of x and dy, one write of dx, and a deterministic
+  two-level reduction for the weight gradient.
+
+The weight may have x's dtype (the model's bf16 parameters, once the optimizer
+has moved them into its flat buffer) or fp32 (as created); any other pairing
+is promoted the way torch promotes ``x.to(dtype) * weight``.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+
+
+def _rows_view(t: torch.Tensor) -> torch.Tensor:
+    try:
+        _lib._rows(t)
+        return t
+    except ValueError:
+        return t.contiguous()
+
+
+class FusedRMSNorm(torch.autograd.Function):
+    """y = round_x(x * rsqrt(mean(x^2, -1) + eps)) * weight."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, weight: torch.Tensor, eps: float):
+        if weight.dim() != 1 or x.shape[-1] != weight.shape[0]:
+            raise ValueError(f"weight {tuple(weight.shape)} does not match the last dim of x "
+                             f"{tuple(x.shape)}")
+        _lib._require_gpu(x, weight)
+        w = weight
+        if w.dtype != x.dtype and w.dtype != torch.float32:
+            w = w.float()  # x.to(dtype) * weight promotes both to fp32
+        if x.dtype == torch.float32 and w.dtype != torch.float32:
+            w = w.float()
+        xr = _rows_view(x)
+        w = w.contiguous()
+        y = torch.empty(x.shape, dtype=w.dtype if w.dtype == torch.float32 else x.dtype,
+                        device=x.device)
+        rstd = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+        _lib.rmsnorm_fwd(xr, w, eps, y, rstd)
+        ctx.save_for_backward(xr, w, rstd)
+        ctx.weight_dtype = weight.dtype
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        xr, w, rstd = ctx.saved_tensors
+        dy = _rows_view(dy)
+        rows = rstd.numel()
+        dx = torch.empty(xr.shape, dtype=xr.dtype, device=xr.device)
+        dw = torch.empty(w.shape, dtype=w.dtype, device=w.device)
+        ws = torch.empty(_lib.rmsnorm_workspace(rows, xr.shape[-1]), dtype=torch.float32,
+                         device=xr.device)
+        _lib.rmsnorm_bwd(xr, w, rstd, dy, dx, dw, ws)
+        return dx, dw.to(ctx.weight_dtype), None
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    return FusedRMSNorm.apply(x, weight, eps)
+
+
+class RMSNorm(nn.Module):
+    """RMSNorm(hidden_size, eps=1e-6) with an fp32 weight of ones, as
+    core/normalization.py:8-11 (on the current GPU unless `device` is given)."""
+
+    def __init__(self, hidden_size: int, eps: float = 1e-6, device=None):
+        super().__init__()
+        self.eps = eps
+        if device is None:
+            device = torch.cuda.current_device() if torch.cuda.is_available() else "cpu"
+        self.weight = nn.Parameter(torch.ones(hidden_size, device=device, dtype=torch.float32))
+
+    def forward(self, x):
+        return FusedRMSNorm.apply(x, self.weight, self.eps)

@@ -2,7 +2,8 @@
  * mi_attn.h — C ABI of the MI355X (gfx950) attention hot path.
  *
  * Causal / non-causal flash attention (forward with saved log-sum-exp, backward
- * producing dQ, dK, dV) and the interleaved-pair rotary position embedding.
+ * producing dQ, dK, dV) and the interleaved-pair rotary position embedding, plus
+ * the train step's fused vocabulary cross entropy and RMSNorm.
  * Every entry point takes plain device pointers, element strides and sizes, and
  * enqueues its kernels on the given HIP stream (a `hipStream_t`, passed as
  * `void*`; NULL means the null stream).  Nothing here allocates, frees or
@@ -198,6 +199,38 @@ mi_status mi_xent_bwd(mi_dtype dtype, int64_t rows, int64_t vocab, const void* l
                       int64_t row_stride, const int64_t* target, const float* lse,
                       const void* grad_loss, void* grad_logits, int64_t grad_row_stride,
                       void* stream);
+
+/*
+ * RMSNorm forward over `rows` rows of `hidden` elements.  Replaces
+ * RMSNorm.forward, core/normalization.py:13-25:
+ *   r = rsqrt(mean(x^2) + eps)   (fp32),   y = round_x(x * r) * weight
+ * where round_x rounds to x's dtype (:23) and the product is taken in the
+ * promotion of x's and weight's dtypes (:24).  weight ([hidden]) has x's dtype
+ * or is fp32; y has weight's dtype if that is fp32, else x's.  rstd ([rows],
+ * fp32) receives r for mi_rmsnorm_bwd.  Row strides are in elements.
+ */
+mi_status mi_rmsnorm_fwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                         float eps, const void* x, int64_t x_row_stride, const void* weight,
+                         void* y, int64_t y_row_stride, float* rstd, void* stream);
+
+/* fp32 elements of workspace mi_rmsnorm_bwd needs for this shape (0 if invalid). */
+int64_t mi_rmsnorm_bwd_workspace(int64_t rows, int64_t hidden);
+
+/*
+ * RMSNorm backward: dx (x's dtype) and dweight (weight's dtype) from dy (y's
+ * dtype), x, weight and the forward's rstd -- the gradients autograd derives
+ * for core/normalization.py:13-25, computed in fp32:
+ *   dn = dy * weight;  dx = r dn - x r^3 mean(dn * x);
+ *   dweight = sum over rows of dy * round_x(x r).
+ * dweight is reduced through `workspace` in a fixed order (deterministic, and
+ * the same on every device).  dx may alias dy when both have the same dtype
+ * and row stride.
+ */
+mi_status mi_rmsnorm_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                         const void* x, int64_t x_row_stride, const void* weight,
+                         const float* rstd, const void* dy, int64_t dy_row_stride, void* dx,
+                         int64_t dx_row_stride, void* dweight, float* workspace,
+                         int64_t workspace_elems, void* stream);
 
 #ifdef __cplusplus
 }

@@ -18,8 +18,8 @@ HEADER = os.path.join(ROOT, "include", "mi_attn.h")
 
 def _declared():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:mi_status|int|const char\*)\s+(mi_\w+)\s*\(", text,
-                                 re.M)))
+    return sorted(set(re.findall(
+        r"^\s*(?:mi_status|int|int64_t|const char\*)\s+(mi_\w+)\s*\(", text, re.M)))
 
 
 def test_header_declares_expected_api():

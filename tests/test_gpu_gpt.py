@@ -1,7 +1,8 @@
 """Config 5: the full GPT train step (12 layers, hidden 768, 12 heads, SwiGLU,
-RMSNorm, vocab 50257, B=8, S=1024) with attention, RoPE and the loss on the HIP
-kernels, 20 steps, against the same harness with the eager attention math and
-the eager loss swapped in (same seed for init and data).  The two runs share
+RMSNorm, vocab 50257, B=8, S=1024) with attention, RoPE, the loss and the
+RMSNorms on the HIP kernels, 20 steps, against the same harness with the eager
+attention math, the eager loss and the eager RMSNorm swapped in (same seed for
+init and data).  The two runs share
 every other kernel, so the loss difference isolates the numerics of the
 kernels."""
 import pytest
@@ -30,7 +31,7 @@ def test_config5_loss_parity(gpu):
     losses, tps = train(cfg, batch=8, seq=1024, steps=20, seed=5, device=gpu)
     ref, ref_tps = train(cfg, batch=8, seq=1024, steps=20, seed=5, device=gpu,
                          attention=eager_attention, rope=eager_rope,
-                         loss_fn=SoftmaxCrossEntropy.apply)
+                         loss_fn=SoftmaxCrossEntropy.apply, eager_ops=True)
     diffs = [abs(a - b) for a, b in zip(losses, ref)]
     print(f"config5 tokens/s kernels {tps:.0f} eager {ref_tps:.0f}; "
           f"loss[0] {losses[0]:.4f} loss[19] {losses[-1]:.4f}; max |dloss| {max(diffs):.4f}")

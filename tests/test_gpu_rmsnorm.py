@@ -1,0 +1,151 @@
+"""GPU parity of the fused RMSNorm (mi_rmsnorm_fwd / mi_rmsnorm_bwd) against the
+float64 oracle (oracle/normalization.py) on the same rounded inputs.
+
+Tolerances.
+* Forward: the kernel rounds n = x * r to x's dtype as the reference does.
+  Its fp32 r may differ from the float64 one in the last bits, which can move
+  n across a rounding boundary, so a 16-bit n may differ by one unit in the
+  last place (2 u relative), and y is rounded once more (u).  Bound:
+  |y - ref| <= (3 u + 1e-5) |ref| against the unrounded float64 product, with
+  u the unit roundoff of y's dtype (2^-8 bf16, 2^-11 fp16), plus 2^-22 for
+  fp16 values below its smallest normal.  In addition, at least 99% of the
+  elements must equal the oracle exactly after rounding, which a missing
+  intermediate rounding or a wrong eps fails.  An fp32 y (fp32 weight) carries
+  only the flip of n: within (2 u_x + 1e-5) |ref|.
+* Backward: fp32 arithmetic, one final rounding: dx within u |ref| plus
+  1e-5 of the magnitudes that cancel in it (r |dn| + |x| r^3 |mean(dn x)|);
+  dw within u |ref| plus 1e-5 * sum_rows |dy n|, plus |dy| times the change of
+  n for the elements whose rounding to x's dtype the fp32 r (within 5e-7 of
+  the float64 one) can flip.
+"""
+import numpy as np
+import pytest
+import torch
+
+from gpu_ref import seeded
+from oracle import rmsnorm_backward, rmsnorm_forward
+
+pytestmark = pytest.mark.gpu
+
+U = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11, torch.float32: 0.0}
+# below the smallest normal (fp16: 2^-14) the spacing is absolute, 2^-24 for fp16;
+# an n flip there plus the final rounding stays under 2^-22
+TINY = {torch.bfloat16: 1e-30, torch.float16: 2.0 ** -22, torch.float32: 1e-30}
+EPS = 1e-6
+
+
+def _np(t):
+    return t.detach().float().cpu().double().numpy()
+
+
+def _check_forward(y, x, w, eps):
+    yd = y.dtype
+    ref, _ = rmsnorm_forward(_np(x), _np(w), eps, x_dtype=x.dtype)
+    got = _np(y)
+    if yd == torch.float32:
+        # 16-bit x: the n flip (2 u of x's dtype) is the only error left
+        bound = np.abs(ref) * (2 * U[x.dtype] + 1e-5) + TINY[x.dtype]
+        assert (np.abs(got - ref) <= bound).all(), np.abs(got - ref).max()
+        if x.dtype != torch.float32:
+            assert np.mean(got == ref.astype(np.float32)) >= 0.99
+        return
+    bound = np.abs(ref) * (3 * U[yd] + 1e-5) + TINY[yd]
+    assert (np.abs(got - ref) <= bound).all(), np.abs(got - ref).max()
+    exact = torch.from_numpy(ref).to(yd).double().numpy()
+    assert np.mean(got == exact) >= 0.99, np.mean(got == exact)
+
+
+def _check_backward(dx, dw, x, w, dy, eps):
+    xn, wn, dyn = _np(x), _np(w), _np(dy)
+    rdx, rdw = rmsnorm_backward(xn, wn, dyn, eps, x_dtype=x.dtype)
+    H = xn.shape[-1]
+    r = 1.0 / np.sqrt((xn * xn).mean(-1) + eps)
+    dn = dyn * wn
+    s = (dn * xn).sum(-1)
+    scale = r[..., None] * np.abs(dn) + np.abs(xn) * (r ** 3 * np.abs(s) / H)[..., None]
+    got = _np(dx)
+    bound = np.abs(rdx) * (U[dx.dtype] + 1e-5) + 1e-5 * scale + 1e-30
+    assert (np.abs(got - rdx) <= bound).all(), np.abs(got - rdx).max()
+    def rnd(a):
+        return torch.from_numpy(a).to(x.dtype).double().numpy() if x.dtype != torch.float32 else a
+    xr = xn * r[..., None]
+    n = rnd(xr)
+    wscale = np.abs(dyn * n).reshape(-1, H).sum(0)
+    # the kernel's fp32 r is within a few 1e-7 of r: where that moves x r across
+    # a rounding boundary of x's dtype, n (and so dy * n) may take the other value
+    flip = np.abs(dyn * (rnd(xr * (1 + 5e-7)) - rnd(xr * (1 - 5e-7)))).reshape(-1, H).sum(0)
+    gw = _np(dw)
+    bound = np.abs(rdw) * (U[dw.dtype] + 1e-5) + 1e-5 * wscale + flip + 1e-30
+    assert (np.abs(gw - rdw) <= bound).all(), np.abs(gw - rdw).max()
+
+
+def _run(x, w, dy, eps=EPS):
+    from gpt_from_scratch_amd import rms_norm
+    xg = x.detach().clone().requires_grad_(True)
+    wg = w.detach().clone().requires_grad_(True)
+    y = rms_norm(xg, wg, eps)
+    y.backward(dy)
+    return y, xg.grad, wg.grad
+
+
+@pytest.mark.parametrize("xd,wd", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                   (torch.float32, torch.float32), (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("rows,H", [(37, 768), (5, 4), (19, 64), (33, 1000), (9, 2048),
+                                    (6, 3072), (3, 5000), (21, 7)])
+def test_matches_oracle(gpu, xd, wd, rows, H):
+    x = seeded((rows, H), 100 + H, std=1.5, dtype=xd)
+    w = (1.0 + 0.1 * seeded((H,), 200 + H, dtype=torch.float32)).to(wd)
+    yd = torch.float32 if wd == torch.float32 else xd
+    dy = seeded((rows, H), 300 + H, dtype=yd)
+    y, dx, dw = _run(x.to(gpu), w.to(gpu), dy.to(gpu))
+    assert y.dtype == yd and dx.dtype == xd and dw.dtype == wd
+    _check_forward(y, x, w, EPS)
+    _check_backward(dx, dw, x, w, dy, EPS)
+
+
+def test_model_layout_module_and_reference_ops(gpu):
+    """[S, B, H] activations as the blocks hand them over, weight bf16 as after the
+    optimizer moved it into its flat buffer; forward against the reference's own
+    torch op sequence (normalization.py:15-24) on the GPU."""
+    from gpt_from_scratch_amd import RMSNorm
+    S, B, H = 1024, 8, 768
+    g = torch.Generator(device=gpu).manual_seed(3)
+    x = torch.randn(S, B, H, generator=g, device=gpu).to(torch.bfloat16)
+    norm = RMSNorm(H, eps=1e-6, device=gpu)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.1 * torch.randn(H, generator=g, device=gpu))
+    norm.weight.data = norm.weight.data.to(torch.bfloat16)
+    y = norm(x)
+    xf = x.float()
+    ref = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + 1e-6)).to(torch.bfloat16) * norm.weight
+    assert y.dtype == ref.dtype == torch.bfloat16
+    assert float((y == ref).float().mean()) >= 0.99
+    assert float(((y.float() - ref.float()).abs() / ref.float().abs().clamp_min(1e-30)).max()) <= 3 * 2 ** -8 + 1e-5
+
+
+def test_strided_rows_aliasing_and_determinism(gpu):
+    from gpt_from_scratch_amd import _lib, rms_norm
+    H = 768
+    for pad in (4, 1):  # 4-element aligned rows (vector path), then misaligned (scalar)
+        wide = seeded((50, H + pad), 7 + pad).to(gpu)
+        x = wide[:, :H]
+        w = (1 + 0.1 * seeded((H,), 8)).to(gpu)
+        dy = seeded((50, H), 9).to(gpu)
+        y, dx, dw = _run(x, w, dy)
+        _check_forward(y, x, w, EPS)
+        _check_backward(dx, dw, x, w, dy, EPS)
+        _, dx2, dw2 = _run(x, w, dy)
+        assert torch.equal(dx, dx2) and torch.equal(dw, dw2)
+    # dx written over dy
+    x = seeded((40, H), 10).to(gpu)
+    w = (1 + 0.1 * seeded((H,), 11)).to(gpu)
+    dy = seeded((40, H), 12).to(gpu)
+    y = torch.empty_like(x)
+    rstd = torch.empty(40, dtype=torch.float32, device=gpu)
+    _lib.rmsnorm_fwd(x, w, EPS, y, rstd)
+    ws = torch.empty(_lib.rmsnorm_workspace(40, H), dtype=torch.float32, device=gpu)
+    dx, dw = torch.empty_like(x), torch.empty_like(w)
+    _lib.rmsnorm_bwd(x, w, rstd, dy, dx, dw, ws)
+    dy2, dw2 = dy.clone(), torch.empty_like(w)
+    _lib.rmsnorm_bwd(x, w, rstd, dy2, dy2, dw2, ws)
+    assert torch.equal(dx, dy2) and torch.equal(dw, dw2)

@@ -32,7 +32,7 @@ def test_cross_entropy_matches_torch():
 
 
 def test_rmsnorm_formula():
-    n = RMSNorm(16, 1e-5, "cpu")
+    n = RMSNorm(16, 1e-5, "cpu", eager=True)
     n.weight.data.uniform_(0.5, 1.5)
     x = torch.randn(4, 16, dtype=torch.float64)
     y = n(x)
@@ -41,7 +41,7 @@ def test_rmsnorm_formula():
 
 
 def test_parameter_count_matches_reference_config():
-    m = GPT(GPTConfig(), "cpu")
+    m = GPT(GPTConfig(), "cpu", eager_ops=True)
     # embedding + head 2*V*H, per layer qkv 3H^2 + out H^2 + gate_up 2HI + down IH + 2 norms,
     # final norm
     V, H, I, L = 50257, 768, 3072, 12
@@ -81,7 +81,7 @@ def test_tiny_model_trains_on_cpu_with_eager_attention():
     cfg = GPTConfig(vocab_size=97, hidden_size=64, num_layers=2, num_attention_heads=4,
                     max_position_embeddings=32, intermediate_size=128)
     torch.manual_seed(3)
-    model = GPT(cfg, "cpu", attention=eager_attention, rope=eager_rope)
+    model = GPT(cfg, "cpu", attention=eager_attention, rope=eager_rope, eager_ops=True)
     opt = MixedPrecisionAdamW(model)
     ids = torch.randint(0, 97, (2, 17))
     inputs, labels = ids[:, :-1], ids[:, 1:].transpose(0, 1).contiguous()

@@ -272,3 +272,67 @@ def test_xent_gradient_is_finite_difference():
     np.testing.assert_allclose(g, fd, rtol=1e-6, atol=1e-8)
     # rows with an in-range target sum to zero
     np.testing.assert_allclose(g.sum(-1), 0.0, atol=1e-12)
+
+
+# ---- RMSNorm (oracle/normalization.py) ----
+
+def test_rmsnorm_matches_torch_autograd_float64():
+    from oracle import rmsnorm_backward, rmsnorm_forward
+    g = torch.Generator().manual_seed(7)
+    x = torch.randn(5, 3, 24, generator=g, dtype=torch.float64)
+    w = torch.randn(24, generator=g, dtype=torch.float64)
+    dy = torch.randn(5, 3, 24, generator=g, dtype=torch.float64)
+    eps = 1e-6
+    xr, wr = x.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    # torch's own ops, no rounding (x is float64)
+    y = xr * torch.rsqrt(xr.pow(2).mean(-1, keepdim=True) + eps) * wr
+    y.backward(dy)
+    yo, _ = rmsnorm_forward(x.numpy(), w.numpy(), eps)
+    dx, dw = rmsnorm_backward(x.numpy(), w.numpy(), dy.numpy(), eps)
+    np.testing.assert_allclose(yo, y.detach().numpy(), rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(dx, xr.grad.numpy(), rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(dw, wr.grad.numpy(), rtol=1e-11, atol=1e-12)
+
+
+def test_rmsnorm_finite_differences_and_invariants():
+    from oracle import rmsnorm_backward, rmsnorm_forward
+    rng = np.random.default_rng(8)
+    x = rng.normal(size=(2, 9))
+    w = rng.normal(size=9)
+    dy = rng.normal(size=(2, 9))
+    eps = 1e-3
+    dx, dw = rmsnorm_backward(x, w, dy, eps)
+    h = 1e-6
+    fdx = np.zeros_like(x)
+    for i in range(2):
+        for j in range(9):
+            xp, xm = x.copy(), x.copy()
+            xp[i, j] += h
+            xm[i, j] -= h
+            fdx[i, j] = ((rmsnorm_forward(xp, w, eps)[0] - rmsnorm_forward(xm, w, eps)[0]) * dy).sum() / (2 * h)
+    np.testing.assert_allclose(dx, fdx, rtol=1e-6, atol=1e-8)
+    fdw = np.array([((rmsnorm_forward(x, w + h * np.eye(9)[j], eps)[0]
+                      - rmsnorm_forward(x, w - h * np.eye(9)[j], eps)[0]) * dy).sum() / (2 * h)
+                    for j in range(9)])
+    np.testing.assert_allclose(dw, fdw, rtol=1e-6, atol=1e-8)
+    # scale invariance (eps = 0) and x . dx = 0 for w = 1, eps = 0
+    y1, _ = rmsnorm_forward(x, w, 0.0)
+    y2, _ = rmsnorm_forward(37.5 * x, w, 0.0)
+    np.testing.assert_allclose(y1, y2, rtol=1e-13)
+    dx0, _ = rmsnorm_backward(x, np.ones(9), dy, 0.0)
+    np.testing.assert_allclose((dx0 * x).sum(-1), 0.0, atol=1e-12)
+    # a constant row a: n = a / sqrt(a^2 + eps)
+    yc, _ = rmsnorm_forward(np.full((1, 16), -0.25), np.ones(16), eps)
+    np.testing.assert_allclose(yc, -0.25 / math.sqrt(0.0625 + eps), rtol=1e-14)
+
+
+def test_rmsnorm_rounds_n_to_the_input_dtype_before_the_weight():
+    """normalization.py:23-24: y = bf16(n) * w, not n * w."""
+    from oracle import rmsnorm_forward
+    x = np.array([[1.0, 1.0 + 2.0 ** -6, 0.5, 3.0]])
+    w = np.full(4, 1.0 + 2.0 ** -7)  # exactly representable in bf16
+    y_round, r = rmsnorm_forward(x, w, 0.0, x_dtype=torch.bfloat16)
+    n = x * r[:, None]
+    nb = torch.from_numpy(n).to(torch.bfloat16).double().numpy()
+    np.testing.assert_array_equal(y_round, nb * w)
+    assert not np.array_equal(y_round, n * w)
