@@ -144,7 +144,9 @@ def model_ops_bench(dev, lib):
       * RMSNorm over [8192, 768] bf16 (core/normalization.py:13-25): forward
         reads x and w, writes y and the fp32 rstd; backward reads x, dy, w and
         rstd, writes dx and dw (its [parts, 768] fp32 partials stay in cache
-        and are not counted)."""
+        and are not counted);
+      * SwiGLU over [8192, 2 x 3072] bf16 (core/mlp.py:24-28);
+      * the optimizer step over the 190,460,160 parameters (core/optimizer.py:79-104)."""
     import torch
     from gpt_from_scratch_amd import _lib
 
@@ -205,6 +207,57 @@ def model_ops_bench(dev, lib):
                      "traffic": read_traffic(name, "traffic_model_ops_c5.txt")}
     del xs, dys, outs
     torch.cuda.empty_cache()
+
+    # SwiGLU on the gate_up projection [8192, 2 * 3072] bf16 (core/mlp.py:24-28):
+    # forward reads gate_up, writes h; backward reads gate_up and dh, writes
+    # dgate_up.  4 copies (600 MB with dh) keep the inputs out of the cache.
+    inter, NS = 3072, 4
+    gus = [torch.randn(rows, 2 * inter, generator=gen, device=dev).to(torch.bfloat16)
+           for _ in range(NS)]
+    dhs = [torch.randn(rows, inter, generator=gen, device=dev).to(torch.bfloat16)
+           for _ in range(NS)]
+    hs = [torch.empty(rows, inter, dtype=torch.bfloat16, device=dev) for _ in range(NS)]
+    dgus = [torch.empty_like(gus[0]) for _ in range(NS)]
+    sfwd = [(dt, rows, inter, P(gus[i]), 2 * inter, P(hs[i]), inter, sp) for i in range(NS)]
+    sbwd = [(dt, rows, inter, P(gus[i]), 2 * inter, P(dhs[i]), inter, P(dgus[i]), 2 * inter, sp)
+            for i in range(NS)]
+    for name, fn, arglist, nbytes in (
+            ("swiglu_fwd", lib.mi_swiglu_fwd, sfwd, rows * inter * 2 * 3),
+            ("swiglu_bwd", lib.mi_swiglu_bwd, sbwd, rows * inter * 2 * 5)):
+        us = _time_rotating(stream, fn, arglist, 8 * NS, name)
+        gbps = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"bound": "hbm", "avg_us": round(us, 2), "achieved": round(gbps, 1),
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                     "algorithmic_bytes": nbytes, "shape": f"[{rows}, 2 x {inter}] bf16",
+                     "traffic": read_traffic(name, "traffic_model_ops_c5.txt")}
+    del gus, dhs, hs, dgus
+    torch.cuda.empty_cache()
+
+    # The optimizer step over config 5's 190,460,160 parameters
+    # (core/optimizer.py:79-104 with AdamW): the squared-norm pass reads the
+    # bf16 gradients; the step reads gradient, fp32 master, exp_avg, exp_avg_sq
+    # and writes the last three and the bf16 parameters (3 GB, out of cache).
+    n = 190_460_160
+    grad = torch.randn(n, generator=gen, device=dev).to(torch.bfloat16)
+    master = torch.randn(n, generator=gen, device=dev)
+    m1 = torch.zeros(n, device=dev)
+    m2 = torch.zeros(n, device=dev)
+    prm = torch.empty(n, dtype=torch.bfloat16, device=dev)
+    ws = torch.empty(_lib.adamw_workspace(), dtype=torch.float32, device=dev)
+    hp = (1 - 3e-4 * 0.1, 0.1, 0.95, 0.05, 3e-4 / 0.1, 0.05 ** 0.5, 1e-8, 1.0)
+    sq = [(dt, n, P(grad), P(ws), ws.numel(), sp)]
+    st = [(dt, dt, n, P(grad), P(master), P(m1), P(m2), P(prm)) + hp + (P(ws), sp)]
+    for name, fn, arglist, nbytes in (
+            ("grad_sumsq", lib.mi_grad_sumsq, sq, n * 2),
+            ("adamw_step", lib.mi_adamw_step, st, n * (2 + 12 + 12 + 2))):
+        us = _time_rotating(stream, fn, arglist, 10, name)
+        gbps = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"bound": "hbm", "avg_us": round(us, 2), "achieved": round(gbps, 1),
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                     "algorithmic_bytes": nbytes, "shape": f"{n} parameters",
+                     "traffic": read_traffic(name, "traffic_model_ops_c5.txt")}
+    del grad, master, m1, m2, prm
+    torch.cuda.empty_cache()
     return out
 
 
@@ -213,7 +266,8 @@ def gpt_train(dev, steps=20, warmup=3):
     vocab 50257, B=8, S=1024, TP=1, DP=1) with attention and RoPE on the HIP
     kernels; tokens/s = B*S*steps / wall time (train.py:196-198), beside the
     same step with attention done by plain PyTorch matmul/softmax (fp32 math)
-    and the loss and RMSNorm by the reference's eager torch ops."""
+    and the loss, RMSNorm, SwiGLU and optimizer by the reference's eager torch
+    ops."""
     import torch
     from gpt_from_scratch_amd.harness import GPTConfig, SoftmaxCrossEntropy, train
 
@@ -234,8 +288,8 @@ def gpt_train(dev, steps=20, warmup=3):
             "steps": steps, "tokens_per_s": round(tps, 1),
             "ms_per_step": round(8 * 1024 / tps * 1e3, 3),
             "tokens_per_s_eager": round(eager_tps, 1),
-            "eager": "attention as torch matmul/softmax (fp32 math); loss and RMSNorm as the "
-                     "reference's eager torch ops",
+            "eager": "attention as torch matmul/softmax (fp32 math); loss, RMSNorm, SwiGLU and "
+                     "the AdamW step as the reference's eager torch ops",
             "loss_first": round(losses[0], 4), "loss_last": round(losses[-1], 4)}
 
 

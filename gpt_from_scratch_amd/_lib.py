@@ -25,7 +25,8 @@ _DTYPES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
 EXPORTED = ("mi_version", "mi_status_str", "mi_last_error", "mi_attn_fwd", "mi_attn_bwd",
             "mi_attn_bwd_preprocess", "mi_attn_bwd_grads", "mi_attn_bwd_dkdv", "mi_attn_bwd_dq",
             "mi_rope", "mi_rope_qk", "mi_xent_fwd", "mi_xent_bwd", "mi_rmsnorm_fwd",
-            "mi_rmsnorm_bwd_workspace", "mi_rmsnorm_bwd")
+            "mi_rmsnorm_bwd_workspace", "mi_rmsnorm_bwd", "mi_swiglu_fwd", "mi_swiglu_bwd",
+            "mi_adamw_workspace", "mi_grad_sumsq", "mi_adamw_step")
 
 _lib = None
 
@@ -79,6 +80,16 @@ def _declare(lib):
     lib.mi_rmsnorm_bwd_workspace.argtypes = [i64, i64]
     lib.mi_rmsnorm_bwd.restype = i
     lib.mi_rmsnorm_bwd.argtypes = [i, i, i64, i64, p, i64, p, p, p, i64, p, i64, p, p, i64, p]
+    lib.mi_swiglu_fwd.restype = i
+    lib.mi_swiglu_fwd.argtypes = [i, i64, i64, p, i64, p, i64, p]
+    lib.mi_swiglu_bwd.restype = i
+    lib.mi_swiglu_bwd.argtypes = [i, i64, i64, p, i64, p, i64, p, i64, p]
+    lib.mi_adamw_workspace.restype = i64
+    lib.mi_adamw_workspace.argtypes = []
+    lib.mi_grad_sumsq.restype = i
+    lib.mi_grad_sumsq.argtypes = [i, i64, p, p, i64, p]
+    lib.mi_adamw_step.restype = i
+    lib.mi_adamw_step.argtypes = [i, i, i64, p, p, p, p, p, f, f, f, f, f, f, f, f, p, p]
 
 
 def lib():
@@ -244,3 +255,57 @@ def rmsnorm_bwd(x, weight, rstd, dy, dx, dweight, workspace):
                               _ptr(weight), _ptr(rstd), _ptr(dy), dys, _ptr(dx), dxs,
                               _ptr(dweight), _ptr(workspace), workspace.numel(), _stream(x))
     _check(st, "mi_rmsnorm_bwd")
+
+
+def swiglu_fwd(gate_up, out):
+    """Enqueue h = silu(gate) * up over the last dim of gate_up [..., 2I] into out [..., I]."""
+    _require_gpu(gate_up, out)
+    rows, gs = _rows(gate_up)
+    _, os_ = _rows(out)
+    st = lib().mi_swiglu_fwd(dtype_code(gate_up), rows, out.shape[-1], _ptr(gate_up), gs,
+                             _ptr(out), os_, _stream(gate_up))
+    _check(st, "mi_swiglu_fwd")
+
+
+def swiglu_bwd(gate_up, dout, dgate_up):
+    """Enqueue the SwiGLU gradient into dgate_up [..., 2I]."""
+    _require_gpu(gate_up, dout, dgate_up)
+    rows, gs = _rows(gate_up)
+    _, ds = _rows(dout)
+    _, dgs = _rows(dgate_up)
+    st = lib().mi_swiglu_bwd(dtype_code(gate_up), rows, dout.shape[-1], _ptr(gate_up), gs,
+                             _ptr(dout), ds, _ptr(dgate_up), dgs, _stream(gate_up))
+    _check(st, "mi_swiglu_bwd")
+
+
+def adamw_workspace() -> int:
+    return int(lib().mi_adamw_workspace())
+
+
+def grad_sumsq(grad, workspace):
+    """Enqueue workspace[0] = sum(grad^2) (fp32) over the flat grad buffer."""
+    _require_gpu(grad, workspace)
+    st = lib().mi_grad_sumsq(dtype_code(grad), grad.numel(), _ptr(grad), _ptr(workspace),
+                             workspace.numel(), _stream(grad))
+    _check(st, "mi_grad_sumsq")
+
+
+def adamw_step(grad, master, exp_avg, exp_avg_sq, param, hp, grad_sumsq_buf):
+    """Enqueue one AdamW step over flat buffers; hp = (1 - lr*wd, 1 - beta1, beta2,
+    1 - beta2, step_size, bias_correction2_sqrt, eps, clip)."""
+    ts = [grad, master, exp_avg, exp_avg_sq] + ([param] if param is not None else [])
+    _require_gpu(*ts)
+    for t in ts:
+        if not t.is_contiguous():
+            raise ValueError("optimizer buffers must be contiguous")
+    n = grad.numel()
+    for t in ts[1:]:
+        if t.numel() != n:
+            raise ValueError("optimizer buffers must have the same number of elements")
+    st = lib().mi_adamw_step(dtype_code(grad), dtype_code(param if param is not None else master),
+                             n, _ptr(grad), _ptr(master), _ptr(exp_avg), _ptr(exp_avg_sq),
+                             _ptr(param) if param is not None else None,
+                             *[float(x) for x in hp],
+                             _ptr(grad_sumsq_buf) if grad_sumsq_buf is not None else None,
+                             _stream(grad))
+    _check(st, "mi_adamw_step")

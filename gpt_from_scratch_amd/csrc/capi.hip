@@ -548,4 +548,120 @@ mi_status mi_rmsnorm_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64
                   "rmsnorm_bwd");
 }
 
+static mi_status swiglu_common(mi_dtype dtype, int64_t rows, int64_t inter, const void* gu,
+                               int64_t gu_stride, void* out, int64_t out_stride,
+                               int64_t out_min_stride) {
+  if (!dtype_ok(dtype)) return fail(MI_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+  if (rows <= 0 || inter <= 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "sizes must be positive (rows=%lld inter=%lld)",
+                (long long)rows, (long long)inter);
+  if (gu_stride < 2 * inter || out_stride < out_min_stride)
+    return fail(MI_ERR_INVALID_ARGUMENT, "row strides (%lld, %lld) shorter than the rows",
+                (long long)gu_stride, (long long)out_stride);
+  if ((inter + 127) / 128 >= (1ll << 31))
+    return fail(MI_ERR_UNSUPPORTED, "inter = %lld too large", (long long)inter);
+  if (!gu || !out) return fail(MI_ERR_INVALID_ARGUMENT, "gate_up / out: null pointer");
+  if (((uintptr_t)gu) % elem_size(dtype) || ((uintptr_t)out) % elem_size(dtype))
+    return fail(MI_ERR_INVALID_ARGUMENT, "gate_up / out: misaligned");
+  return MI_OK;
+}
+
+// 8-element vectors: every row of every tensor starts on a 16-byte boundary
+// for 16-bit types (32 bytes for fp32, loaded as two 16-byte halves).
+static bool swiglu_vec_ok(int dtype, int64_t inter, std::initializer_list<const void*> ptrs,
+                          std::initializer_list<int64_t> strides) {
+  const int esz = elem_size(dtype);
+  if (inter % 8) return false;
+  for (const void* p : ptrs)
+    if (((uintptr_t)p) % (4 * esz) || (((uintptr_t)p) % 16 && esz == 2)) return false;
+  for (int64_t s : strides)
+    if (s % 8) return false;
+  return true;
+}
+
+mi_status mi_swiglu_fwd(mi_dtype dtype, int64_t rows, int64_t inter, const void* gate_up,
+                        int64_t gate_up_row_stride, void* out, int64_t out_row_stride,
+                        void* stream) {
+  if (mi_status st = swiglu_common(dtype, rows, inter, gate_up, gate_up_row_stride, out,
+                                   out_row_stride, inter))
+    return st;
+  const bool vec = swiglu_vec_ok(dtype, inter, {gate_up, out},
+                                 {gate_up_row_stride, out_row_stride});
+  return launched(mi::launch_swiglu(false, dtype, rows, inter, gate_up, gate_up_row_stride,
+                                    nullptr, 0, out, out_row_stride, vec, (hipStream_t)stream),
+                  "swiglu_fwd");
+}
+
+mi_status mi_swiglu_bwd(mi_dtype dtype, int64_t rows, int64_t inter, const void* gate_up,
+                        int64_t gate_up_row_stride, const void* dout, int64_t dout_row_stride,
+                        void* dgate_up, int64_t dgate_up_row_stride, void* stream) {
+  if (mi_status st = swiglu_common(dtype, rows, inter, gate_up, gate_up_row_stride, dgate_up,
+                                   dgate_up_row_stride, 2 * inter))
+    return st;
+  if (!dout) return fail(MI_ERR_INVALID_ARGUMENT, "dout: null pointer");
+  if (dout_row_stride < inter)
+    return fail(MI_ERR_INVALID_ARGUMENT, "dout row stride %lld < inter %lld",
+                (long long)dout_row_stride, (long long)inter);
+  if (((uintptr_t)dout) % elem_size(dtype))
+    return fail(MI_ERR_INVALID_ARGUMENT, "dout: misaligned");
+  const bool vec = swiglu_vec_ok(dtype, inter, {gate_up, dout, dgate_up},
+                                 {gate_up_row_stride, dout_row_stride, dgate_up_row_stride});
+  return launched(mi::launch_swiglu(true, dtype, rows, inter, gate_up, gate_up_row_stride, dout,
+                                    dout_row_stride, dgate_up, dgate_up_row_stride, vec,
+                                    (hipStream_t)stream),
+                  "swiglu_bwd");
+}
+
+int64_t mi_adamw_workspace(void) { return 1 + mi::adam_parts(); }
+
+mi_status mi_grad_sumsq(mi_dtype grad_dtype, int64_t n, const void* grad, float* workspace,
+                        int64_t workspace_elems, void* stream) {
+  if (!dtype_ok(grad_dtype)) return fail(MI_ERR_INVALID_ARGUMENT, "unknown dtype %d", grad_dtype);
+  if (n <= 0) return fail(MI_ERR_INVALID_ARGUMENT, "n must be positive (got %lld)", (long long)n);
+  if (!grad || !workspace) return fail(MI_ERR_INVALID_ARGUMENT, "grad / workspace: null pointer");
+  if (((uintptr_t)grad) % elem_size(grad_dtype) || ((uintptr_t)workspace) % 4)
+    return fail(MI_ERR_INVALID_ARGUMENT, "grad / workspace: misaligned");
+  if (workspace_elems < mi_adamw_workspace())
+    return fail(MI_ERR_INVALID_ARGUMENT, "workspace holds %lld floats, %lld needed",
+                (long long)workspace_elems, (long long)mi_adamw_workspace());
+  const bool vec = ((uintptr_t)grad) % (4 * elem_size(grad_dtype)) == 0;
+  return launched(mi::launch_grad_sumsq(grad_dtype, n, grad, vec, workspace, workspace + 1,
+                                        (hipStream_t)stream),
+                  "grad_sumsq");
+}
+
+mi_status mi_adamw_step(mi_dtype grad_dtype, mi_dtype param_dtype, int64_t n, const void* grad,
+                        float* master, float* exp_avg, float* exp_avg_sq, void* param,
+                        float weight_decay_factor, float lerp_weight, float beta2,
+                        float one_minus_beta2, float step_size, float bias_correction2_sqrt,
+                        float eps, float clip, const float* grad_sumsq, void* stream) {
+  if (!dtype_ok(grad_dtype) || !dtype_ok(param_dtype))
+    return fail(MI_ERR_INVALID_ARGUMENT, "unknown dtype (grad %d, param %d)", grad_dtype,
+                param_dtype);
+  if (n <= 0) return fail(MI_ERR_INVALID_ARGUMENT, "n must be positive (got %lld)", (long long)n);
+  if (!grad || !master || !exp_avg || !exp_avg_sq)
+    return fail(MI_ERR_INVALID_ARGUMENT, "grad / master / exp_avg / exp_avg_sq: null pointer");
+  if (((uintptr_t)grad) % elem_size(grad_dtype) || ((uintptr_t)master) % 4 ||
+      ((uintptr_t)exp_avg) % 4 || ((uintptr_t)exp_avg_sq) % 4 ||
+      ((uintptr_t)param) % elem_size(param_dtype))
+    return fail(MI_ERR_INVALID_ARGUMENT, "a buffer is misaligned");
+  const float hp[8] = {weight_decay_factor, lerp_weight, beta2, one_minus_beta2, step_size,
+                       bias_correction2_sqrt, eps, clip};
+  for (float x : hp)
+    if (!std::isfinite(x)) return fail(MI_ERR_INVALID_ARGUMENT, "hyperparameters must be finite");
+  if (!(bias_correction2_sqrt > 0.f))
+    return fail(MI_ERR_INVALID_ARGUMENT, "bias_correction2_sqrt must be positive");
+  if (clip > 0.f && !grad_sumsq)
+    return fail(MI_ERR_INVALID_ARGUMENT, "clip > 0 needs grad_sumsq (from mi_grad_sumsq)");
+  const uintptr_t al = 16;
+  const bool vec = ((uintptr_t)grad) % (4 * elem_size(grad_dtype)) == 0 &&
+                   ((uintptr_t)master) % al == 0 && ((uintptr_t)exp_avg) % al == 0 &&
+                   ((uintptr_t)exp_avg_sq) % al == 0 &&
+                   ((uintptr_t)param) % (4 * elem_size(param_dtype)) == 0;
+  return launched(mi::launch_adamw_step(grad_dtype, param_dtype, n, grad, master, exp_avg,
+                                        exp_avg_sq, param, hp, grad_sumsq, vec,
+                                        (hipStream_t)stream),
+                  "adamw_step");
+}
+
 }  // extern "C"

@@ -102,4 +102,22 @@ hipError_t launch_rmsnorm_fwd(int x_dtype, int w_dtype, const RmsArgs& a, bool v
 hipError_t launch_rmsnorm_bwd(int x_dtype, int w_dtype, const RmsArgs& a, bool vec,
                               hipStream_t st);
 
+// SwiGLU on the fused [rows, 2 * inter] gate_up projection (model_ops.hip):
+// forward writes h [rows, inter]; backward (bwd = true) reads dh and writes the
+// [rows, 2 * inter] gradient.
+hipError_t launch_swiglu(bool bwd, int dtype, int64_t rows, int64_t inter, const void* gu,
+                         int64_t gu_stride, const void* dh, int64_t dh_stride, void* out,
+                         int64_t out_stride, bool vec, hipStream_t st);
+
+// The optimizer step (model_ops.hip).  Squared gradient norm into out[0] via
+// adam_parts() partial sums; the AdamW step over the flat buffers with
+// hp = {1 - lr*wd, 1 - beta1, beta2, 1 - beta2, lr / (1 - beta1^t),
+//       sqrt(1 - beta2^t), eps, clip}.
+int64_t adam_parts();
+hipError_t launch_grad_sumsq(int g_dtype, int64_t n, const void* grad, bool vec, float* out,
+                             float* partial, hipStream_t st);
+hipError_t launch_adamw_step(int g_dtype, int p_dtype, int64_t n, const void* grad, float* master,
+                             float* m, float* v, void* param, const float (&hp)[8],
+                             const float* sumsq, bool vec, hipStream_t st);
+
 }  // namespace mi

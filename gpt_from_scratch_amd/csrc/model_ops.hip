@@ -647,4 +647,354 @@ hipError_t launch_rmsnorm_bwd(int x_dtype, int w_dtype, const RmsArgs& a, bool v
   return launch_rms(false, x_dtype, w_dtype, a, vec, st);
 }
 
+// ---------------------------------------------------------------------------
+// SwiGLU activation (ParallelMLP.forward, core/mlp.py:24-28) on the fused
+// gate_up projection [N, 2I]: gate = columns [0, I), up = columns [I, 2I).
+//   s = round(silu(g)),  h = round(s * u)        (F.silu then the product, each
+//                                                  rounded to the tensor dtype)
+// Backward, as autograd evaluates it (mul, then silu_backward, then the chunk's
+// concatenation), written straight into the [N, 2I] gradient:
+//   d_up = round(dh * s),  d_s = round(dh * u),
+//   d_g  = round(d_s * sig * (1 + g (1 - sig))),  sig = 1 / (1 + exp(-g)).
+// 8 elements (16 bytes of 16-bit data) per lane and step when rows are 8-element
+// aligned, scalar otherwise.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct SwigluArgs {
+  int64_t rows, inter;
+  const void* gu;
+  int64_t gu_stride;
+  const void* dh;
+  int64_t dh_stride;
+  void* out;  // h (forward) or dgate_up (backward)
+  int64_t out_stride;
+};
+
+template <int DT>
+__device__ __forceinline__ void swiglu_fwd_elem(float g, float u, float& h) {
+  const float s = round_to<DT>(g / (1.f + __expf(-g)));
+  h = s * u;
+}
+
+template <int DT>
+__device__ __forceinline__ void swiglu_bwd_elem(float g, float u, float dh, float& dg, float& du) {
+  const float e = __expf(-g);
+  const float s = round_to<DT>(g / (1.f + e));
+  du = dh * s;
+  const float ds = round_to<DT>(dh * u);
+  const float sig = 1.f / (1.f + e);
+  dg = ds * (sig * (1.f + g * (1.f - sig)));
+}
+
+// 8 elements of a 16-bit row at i (16-byte aligned) as floats; fp32 rows use
+// two 16-byte loads.
+template <int DT>
+__device__ __forceinline__ void ld8(const void* row, int64_t i, float (&v)[8]) {
+  float a[4], b[4];
+  ld4<DT>(row, i, a);
+  ld4<DT>(row, i + 4, b);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    v[e] = a[e];
+    v[4 + e] = b[e];
+  }
+}
+template <int DT>
+__device__ __forceinline__ void st8(void* row, int64_t i, const float (&v)[8]) {
+  float a[4], b[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    a[e] = v[e];
+    b[e] = v[4 + e];
+  }
+  st4<DT>(row, i, a);
+  st4<DT>(row, i + 4, b);
+}
+
+// Grid: x covers the row's chunks (SW_T lanes per workgroup), y the rows with
+// a stride loop; no per-element division.
+constexpr int SW_T = 128;
+
+template <int DT, bool BWD>
+__global__ __launch_bounds__(SW_T) void swiglu_vec_kernel(SwigluArgs a) {
+  const int64_t c = (int64_t)blockIdx.x * SW_T + threadIdx.x;
+  if (c >= a.inter / 8) return;  // no barrier in this kernel
+  const int64_t i = 8 * c;
+  for (int64_t row = blockIdx.y; row < a.rows; row += gridDim.y) {
+    const void* gr = row_ptr<DT>(a.gu, row, a.gu_stride);
+    float g[8], u[8];
+    ld8<DT>(gr, i, g);
+    ld8<DT>(gr, a.inter + i, u);
+    if constexpr (!BWD) {
+      float h[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) swiglu_fwd_elem<DT>(g[e], u[e], h[e]);
+      st8<DT>(row_ptr<DT>(a.out, row, a.out_stride), i, h);
+    } else {
+      float d[8], dg[8], du[8];
+      ld8<DT>(row_ptr<DT>(a.dh, row, a.dh_stride), i, d);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) swiglu_bwd_elem<DT>(g[e], u[e], d[e], dg[e], du[e]);
+      void* orow = row_ptr<DT>(a.out, row, a.out_stride);
+      st8<DT>(orow, i, dg);
+      st8<DT>(orow, a.inter + i, du);
+    }
+  }
+}
+
+template <int DT, bool BWD>
+__global__ __launch_bounds__(SW_T) void swiglu_scalar_kernel(SwigluArgs a) {
+  typedef typename Store<DT>::type T;
+  const int64_t j = (int64_t)blockIdx.x * SW_T + threadIdx.x;
+  if (j >= a.inter) return;
+  for (int64_t row = blockIdx.y; row < a.rows; row += gridDim.y) {
+    const T* gr = (const T*)a.gu + row * a.gu_stride;
+    const float g = Store<DT>::ld(gr, j), u = Store<DT>::ld(gr, a.inter + j);
+    T* orow = (T*)a.out + row * a.out_stride;
+    if constexpr (!BWD) {
+      float h;
+      swiglu_fwd_elem<DT>(g, u, h);
+      Store<DT>::st(orow, j, h);
+    } else {
+      float dg, du;
+      swiglu_bwd_elem<DT>(g, u, Store<DT>::ld((const T*)a.dh + row * a.dh_stride, j), dg, du);
+      Store<DT>::st(orow, j, dg);
+      Store<DT>::st(orow, a.inter + j, du);
+    }
+  }
+}
+
+template <int DT>
+hipError_t launch_swiglu_dt(bool bwd, const SwigluArgs& a, bool vec, hipStream_t st) {
+  const int64_t per_row = vec ? a.inter / 8 : a.inter;
+  const dim3 grid((unsigned)((per_row + SW_T - 1) / SW_T),
+                  (unsigned)(a.rows < 65535 ? a.rows : 65535));
+  if (vec) {
+    if (bwd) hipLaunchKernelGGL((swiglu_vec_kernel<DT, true>), grid, dim3(SW_T), 0, st, a);
+    else hipLaunchKernelGGL((swiglu_vec_kernel<DT, false>), grid, dim3(SW_T), 0, st, a);
+  } else {
+    if (bwd) hipLaunchKernelGGL((swiglu_scalar_kernel<DT, true>), grid, dim3(SW_T), 0, st, a);
+    else hipLaunchKernelGGL((swiglu_scalar_kernel<DT, false>), grid, dim3(SW_T), 0, st, a);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_swiglu(bool bwd, int dtype, int64_t rows, int64_t inter, const void* gu,
+                         int64_t gu_stride, const void* dh, int64_t dh_stride, void* out,
+                         int64_t out_stride, bool vec, hipStream_t st) {
+  SwigluArgs a{rows, inter, gu, gu_stride, dh, dh_stride, out, out_stride};
+  if (dtype == 2) return launch_swiglu_dt<2>(bwd, a, vec, st);
+  if (dtype == 1) return launch_swiglu_dt<1>(bwd, a, vec, st);
+  return launch_swiglu_dt<0>(bwd, a, vec, st);
+}
+
+// ---------------------------------------------------------------------------
+// The optimizer step of DistributedOptimizer.step at one data-parallel rank
+// (core/optimizer.py:79-104) with torch.optim.AdamW (train.py:130-138), over
+// the flat gradient / fp32 master / moment buffers:
+//   clip (:98-104):   norm = sqrt(sum g^2) (fp32); if norm > clip:
+//                     g <- round_g(g * clip / (norm + 1e-6))   (the bf16 buffer is
+//                     scaled in place in the reference, so the scaled gradient is
+//                     rounded to its dtype)
+//   AdamW (torch's multi-tensor form, fp32):
+//     p <- p * (1 - lr wd);  m <- m + (1 - b1)(g - m);  v <- v b2 + (1 - b2) g g
+//     p <- p - step_size * m / (sqrt(v) / sqrt(1 - b2^t) + eps),
+//     step_size = lr / (1 - b1^t)     (bias corrections computed by the host)
+//   and the model's copy param <- round_p(p) (the all-gather into the bf16
+//   parameter buffer, :95).
+// The squared norm is reduced deterministically: ADAM_PARTS fixed contiguous
+// slices into partial sums, then one workgroup sums them in order.  The step
+// kernel reads the norm from device memory, so nothing waits for the host.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr int ADAM_PARTS = 1024;
+constexpr int ADAM_T = 256;
+
+template <int GT>
+__global__ __launch_bounds__(ADAM_T) void grad_sumsq_partial_kernel(const void* grad, int64_t n,
+                                                                    int64_t chunk, bool vec,
+                                                                    float* partial) {
+  const int64_t start = (int64_t)blockIdx.x * chunk;
+  const int64_t end = min(start + chunk, n);
+  float s = 0.f;
+  if (start < end) {
+    int64_t i = start;
+    if (vec) {
+      const int64_t vend = start + ((end - start) & ~(int64_t)3);
+      const void* base = grad;
+      for (int64_t k = start + 4 * (int64_t)threadIdx.x; k < vend; k += 4 * ADAM_T) {
+        float g[4];
+        ld4<GT>(base, k, g);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) s = __builtin_fmaf(g[e], g[e], s);
+      }
+      i = vend;
+    }
+    typedef typename Store<GT>::type T;
+    for (int64_t k = i + threadIdx.x; k < end; k += ADAM_T) {
+      const float g = Store<GT>::ld((const T*)grad, k);
+      s = __builtin_fmaf(g, g, s);
+    }
+  }
+  s = wave_sum(s);
+  __shared__ float ws[ADAM_T / 64];
+  if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < ADAM_T / 64; ++w) t += ws[w];
+    partial[blockIdx.x] = t;
+  }
+}
+
+// out[0] = sum of partial[0 .. ADAM_PARTS) in a fixed order (one workgroup)
+__global__ __launch_bounds__(ADAM_PARTS) void grad_sumsq_final_kernel(const float* partial,
+                                                                      float* out) {
+  float s = partial[threadIdx.x];
+  s = wave_sum(s);
+  __shared__ float ws[ADAM_PARTS / 64];
+  if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    float t = 0.f;
+#pragma unroll
+    for (int w = 0; w < ADAM_PARTS / 64; ++w) t += ws[w];
+    out[0] = t;
+  }
+}
+
+struct AdamArgs {
+  int64_t n;
+  const void* grad;
+  float *master, *m, *v;
+  void* param;  // may be null
+  float decay, lerp_w, beta2, one_m_beta2, step_size, bc2_sqrt, eps, clip;
+  const float* sumsq;  // device scalar; read when clip > 0
+};
+
+__device__ __forceinline__ float clip_coef(const AdamArgs& a, bool& clipping) {
+  clipping = false;
+  if (!(a.clip > 0.f)) return 1.f;
+  const float norm = sqrtf(*a.sumsq);
+  if (!(norm > a.clip)) return 1.f;
+  clipping = true;
+  return a.clip / (norm + 1e-6f);
+}
+
+__device__ __forceinline__ void adam_elem(const AdamArgs& a, float g, float& p, float& m,
+                                          float& v) {
+  p = p * a.decay;
+  m = m + a.lerp_w * (g - m);
+  v = v * a.beta2;
+  v = v + a.one_m_beta2 * (g * g);
+  const float denom = sqrtf(v) / a.bc2_sqrt + a.eps;
+  p = p + (-a.step_size) * (m / denom);
+}
+
+template <int GT, int PT>
+__global__ __launch_bounds__(ADAM_T) void adamw_step_kernel(AdamArgs a, bool vec) {
+  bool clipping;
+  const float coef = clip_coef(a, clipping);
+  const int64_t nv = vec ? a.n / 4 : 0;
+  const int64_t gstride = (int64_t)gridDim.x * ADAM_T;
+  for (int64_t q = (int64_t)blockIdx.x * ADAM_T + threadIdx.x; q < nv; q += gstride) {
+    const int64_t i = 4 * q;
+    float g[4];
+    ld4<GT>(a.grad, i, g);
+    f32x4 p = *(const f32x4*)(a.master + i);
+    f32x4 m = *(const f32x4*)(a.m + i);
+    f32x4 v = *(const f32x4*)(a.v + i);
+    float po[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const float ge = clipping ? round_to<GT>(g[e] * coef) : g[e];
+      float pe = p[e], me = m[e], ve = v[e];
+      adam_elem(a, ge, pe, me, ve);
+      p[e] = pe;
+      m[e] = me;
+      v[e] = ve;
+      po[e] = pe;
+    }
+    *(f32x4*)(a.master + i) = p;
+    *(f32x4*)(a.m + i) = m;
+    *(f32x4*)(a.v + i) = v;
+    if (a.param) st4<PT>(a.param, i, po);
+  }
+  // elements after the last full vector (all of them when !vec)
+  typedef typename Store<GT>::type TG;
+  typedef typename Store<PT>::type TP;
+  for (int64_t i = 4 * nv + (int64_t)blockIdx.x * ADAM_T + threadIdx.x; i < a.n; i += gstride) {
+    float g = Store<GT>::ld((const TG*)a.grad, i);
+    if (clipping) g = round_to<GT>(g * coef);
+    float p = a.master[i], m = a.m[i], v = a.v[i];
+    adam_elem(a, g, p, m, v);
+    a.master[i] = p;
+    a.m[i] = m;
+    a.v[i] = v;
+    if (a.param) Store<PT>::st((TP*)a.param, i, p);
+  }
+}
+
+template <int GT>
+hipError_t launch_adamw_g(int p_dtype, const AdamArgs& a, bool vec, hipStream_t st) {
+  const int64_t work = vec ? a.n / 4 : a.n;
+  const int64_t want = (work + ADAM_T - 1) / ADAM_T;
+  const dim3 grid((unsigned)(want < 4096 ? (want > 0 ? want : 1) : 4096));
+  if (p_dtype == 2) hipLaunchKernelGGL((adamw_step_kernel<GT, 2>), grid, dim3(ADAM_T), 0, st, a, vec);
+  else if (p_dtype == 1) hipLaunchKernelGGL((adamw_step_kernel<GT, 1>), grid, dim3(ADAM_T), 0, st, a, vec);
+  else hipLaunchKernelGGL((adamw_step_kernel<GT, 0>), grid, dim3(ADAM_T), 0, st, a, vec);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+int64_t adam_parts() { return ADAM_PARTS; }
+
+hipError_t launch_grad_sumsq(int g_dtype, int64_t n, const void* grad, bool vec, float* out,
+                             float* partial, hipStream_t st) {
+  // contiguous slices of a multiple of 4 elements, one per workgroup
+  int64_t chunk = (n + ADAM_PARTS - 1) / ADAM_PARTS;
+  chunk = (chunk + 3) & ~(int64_t)3;
+  if (g_dtype == 2)
+    hipLaunchKernelGGL(grad_sumsq_partial_kernel<2>, dim3(ADAM_PARTS), dim3(ADAM_T), 0, st, grad,
+                       n, chunk, vec, partial);
+  else if (g_dtype == 1)
+    hipLaunchKernelGGL(grad_sumsq_partial_kernel<1>, dim3(ADAM_PARTS), dim3(ADAM_T), 0, st, grad,
+                       n, chunk, vec, partial);
+  else
+    hipLaunchKernelGGL(grad_sumsq_partial_kernel<0>, dim3(ADAM_PARTS), dim3(ADAM_T), 0, st, grad,
+                       n, chunk, vec, partial);
+  hipLaunchKernelGGL(grad_sumsq_final_kernel, dim3(1), dim3(ADAM_PARTS), 0, st, partial, out);
+  return hipGetLastError();
+}
+
+hipError_t launch_adamw_step(int g_dtype, int p_dtype, int64_t n, const void* grad, float* master,
+                             float* m, float* v, void* param, const float (&hp)[8],
+                             const float* sumsq, bool vec, hipStream_t st) {
+  AdamArgs a;
+  a.n = n;
+  a.grad = grad;
+  a.master = master;
+  a.m = m;
+  a.v = v;
+  a.param = param;
+  a.decay = hp[0];
+  a.lerp_w = hp[1];
+  a.beta2 = hp[2];
+  a.one_m_beta2 = hp[3];
+  a.step_size = hp[4];
+  a.bc2_sqrt = hp[5];
+  a.eps = hp[6];
+  a.clip = hp[7];
+  a.sumsq = sumsq;
+  if (g_dtype == 2) return launch_adamw_g<2>(p_dtype, a, vec, st);
+  if (g_dtype == 1) return launch_adamw_g<1>(p_dtype, a, vec, st);
+  return launch_adamw_g<0>(p_dtype, a, vec, st);
+}
+
 }  // namespace mi

@@ -21,15 +21,19 @@ kernels run inside a real train step:
   (core/tensor_parallel/loss.py:9-72 at one rank; train.py:179-181), by
   default the fused HIP kernels (`loss_fn` injectable, e.g. the eager
   `SoftmaxCrossEntropy.apply` below);
+* SwiGLU MLP (core/mlp.py:22-33), the activation by default on the fused HIP
+  kernels;
 * optimizer (core/optimizer.py:6-104 at one rank): parameters and gradients
   live in flat bf16 buffers the model computes in, an fp32 master copy takes
   the AdamW step, gradients are clipped by their global norm first, and the
-  result is copied back to bf16;
+  result is copied back to bf16; by default the fused HIP step
+  (`DistributedOptimizer`), else `MixedPrecisionAdamW` on torch's AdamW;
 * init: xavier-uniform for every projection and the embedding
   (core/tensor_parallel/layers.py:31,66,112), RMSNorm weights 1.
 
-Everything here is ordinary PyTorch except the attention path, the loss and
-the RMSNorms.
+Everything here is ordinary PyTorch (the GEMMs, the embedding) except the
+attention path, the loss, the RMSNorms, the SwiGLU activation and the
+optimizer step.
 """
 from __future__ import annotations
 
@@ -43,7 +47,9 @@ import torch.nn.functional as F
 
 from ..attention_block import attention_block
 from ..cross_entropy import vocab_parallel_cross_entropy
+from ..mlp import swiglu
 from ..normalization import rms_norm
+from ..optimizer import DistributedOptimizer
 from ..flash_attn import apply_flash_attn
 from ..position_embeddings import RotaryEmbedding
 from ..rope import apply_rope_qk
@@ -117,13 +123,19 @@ class Attention(nn.Module):
 
 
 class SwiGLU(nn.Module):
-    def __init__(self, cfg: GPTConfig, device):
+    """The HIP activation kernels by default; `eager=True` runs the reference's ops."""
+
+    def __init__(self, cfg: GPTConfig, device, eager=False):
         super().__init__()
+        self.eager = eager
         self.gate_up = _xavier(2 * cfg.intermediate_size, cfg.hidden_size, device)
         self.down = _xavier(cfg.hidden_size, cfg.intermediate_size, device)
 
     def forward(self, x):
-        gate, up = F.linear(x, self.gate_up).chunk(2, dim=-1)
+        gate_up = F.linear(x, self.gate_up)
+        if not self.eager:
+            return F.linear(swiglu(gate_up), self.down)
+        gate, up = gate_up.chunk(2, dim=-1)
         return F.linear(F.silu(gate) * up, self.down)
 
 
@@ -133,7 +145,7 @@ class Block(nn.Module):
         self.norm1 = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager=eager_ops)
         self.attn = Attention(cfg, device, attention, rope)
         self.norm2 = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager=eager_ops)
-        self.mlp = SwiGLU(cfg, device)
+        self.mlp = SwiGLU(cfg, device, eager=eager_ops)
 
     def forward(self, x):
         x = x + self.attn(self.norm1(x))
@@ -187,7 +199,9 @@ class SoftmaxCrossEntropy(torch.autograd.Function):
 
 class MixedPrecisionAdamW:
     """Flat bf16 parameter/gradient buffers for the model, fp32 master copy
-    for AdamW, global-norm clipping (one data-parallel rank)."""
+    for AdamW, global-norm clipping (one data-parallel rank): the reference's
+    sequence on torch's AdamW (the eager counterpart of the fused
+    DistributedOptimizer)."""
 
     def __init__(self, model, lr=3e-4, betas=(0.9, 0.95), weight_decay=0.1, clip=1.0,
                  dtype=torch.bfloat16):
@@ -237,11 +251,17 @@ def train(cfg: GPTConfig, batch=8, seq=1024, steps=20, seed=5, device="cuda", at
     `steps` timed train steps on one fixed synthetic batch.  Returns
     (losses, tokens_per_second).  `loss_fn(logits, target)` -> per-token loss
     defaults to the HIP cross entropy; `eager_ops` swaps the model's other HIP
-    operators (RMSNorm) for the reference's eager op sequences."""
+    operators (RMSNorm, SwiGLU, the optimizer step) for the reference's eager
+    op sequences."""
     loss_fn = loss_fn or vocab_parallel_cross_entropy
     torch.manual_seed(seed)
     model = GPT(cfg, device, attention, rope, eager_ops)
-    opt = MixedPrecisionAdamW(model)
+    if eager_ops:
+        opt = MixedPrecisionAdamW(model)
+    else:
+        opt = DistributedOptimizer(model, torch.optim.AdamW,
+                                   {"lr": 3e-4, "betas": (0.9, 0.95), "weight_decay": 0.1},
+                                   clip_grad=1.0)
     inputs, labels = synthetic_batch(batch, seq, cfg.vocab_size, seed, device)
     labels_t = labels.transpose(0, 1).contiguous()
 

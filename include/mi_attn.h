@@ -3,7 +3,8 @@
  *
  * Causal / non-causal flash attention (forward with saved log-sum-exp, backward
  * producing dQ, dK, dV) and the interleaved-pair rotary position embedding, plus
- * the train step's fused vocabulary cross entropy and RMSNorm.
+ * the train step's fused vocabulary cross entropy, RMSNorm, SwiGLU and AdamW
+ * step.
  * Every entry point takes plain device pointers, element strides and sizes, and
  * enqueues its kernels on the given HIP stream (a `hipStream_t`, passed as
  * `void*`; NULL means the null stream).  Nothing here allocates, frees or
@@ -231,6 +232,60 @@ mi_status mi_rmsnorm_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64
                          const float* rstd, const void* dy, int64_t dy_row_stride, void* dx,
                          int64_t dx_row_stride, void* dweight, float* workspace,
                          int64_t workspace_elems, void* stream);
+
+/*
+ * SwiGLU on the fused gate_up projection: rows of 2*inter elements, gate in
+ * columns [0, inter), up in [inter, 2*inter).  Replaces
+ * `gate, up = gate_up.chunk(2, dim=-1); x = F.silu(gate) * up`,
+ * core/mlp.py:25-28:  h = round(round(silu(gate)) * up), each product rounded to
+ * the dtype as torch's two ops do; h has rows of inter elements.
+ */
+mi_status mi_swiglu_fwd(mi_dtype dtype, int64_t rows, int64_t inter, const void* gate_up,
+                        int64_t gate_up_row_stride, void* out, int64_t out_row_stride,
+                        void* stream);
+
+/*
+ * Gradient of mi_swiglu_fwd as autograd evaluates the reference's ops (mul,
+ * silu_backward, then the chunk's concatenation): dgate_up rows of 2*inter
+ * elements, d_gate = round(round(dout*up) * silu'(gate)), d_up = round(dout *
+ * round(silu(gate))), written in place of the concatenation.
+ */
+mi_status mi_swiglu_bwd(mi_dtype dtype, int64_t rows, int64_t inter, const void* gate_up,
+                        int64_t gate_up_row_stride, const void* dout, int64_t dout_row_stride,
+                        void* dgate_up, int64_t dgate_up_row_stride, void* stream);
+
+/* fp32 elements of workspace mi_grad_sumsq needs (result in element 0). */
+int64_t mi_adamw_workspace(void);
+
+/*
+ * workspace[0] = sum of grad^2 over n elements in fp32, reduced in a fixed
+ * order (deterministic).  Replaces the local norm of
+ * DistributedOptimizer._clip_grad_norm, core/optimizer.py:100, at one rank.
+ */
+mi_status mi_grad_sumsq(mi_dtype grad_dtype, int64_t n, const void* grad, float* workspace,
+                        int64_t workspace_elems, void* stream);
+
+/*
+ * One AdamW step over flat buffers, with gradient clipping and the copy into
+ * the model's parameter buffer.  Replaces DistributedOptimizer.step at one rank,
+ * core/optimizer.py:79-104, with torch.optim.AdamW (train.py:130-138):
+ *   if clip > 0 and norm = sqrt(*grad_sumsq) > clip:
+ *       g = round_grad(g * clip / (norm + 1e-6))               (:102-104)
+ *   p = p * weight_decay_factor                 (weight_decay_factor = 1 - lr*wd)
+ *   m = m + lerp_weight * (g - m)               (lerp_weight = 1 - beta1)
+ *   v = v * beta2 + one_minus_beta2 * g * g
+ *   p = p - step_size * m / (sqrt(v) / bias_correction2_sqrt + eps)
+ *       (step_size = lr / (1 - beta1^t), bias_correction2_sqrt = sqrt(1 - beta2^t))
+ *   param = round_param(p)                      (the all-gather into the bf16 buffer, :95)
+ * master, exp_avg, exp_avg_sq are fp32 [n], updated in place; param may be
+ * NULL.  grad_sumsq is a device pointer (workspace of mi_grad_sumsq): nothing
+ * is read back to the host.
+ */
+mi_status mi_adamw_step(mi_dtype grad_dtype, mi_dtype param_dtype, int64_t n, const void* grad,
+                        float* master, float* exp_avg, float* exp_avg_sq, void* param,
+                        float weight_decay_factor, float lerp_weight, float beta2,
+                        float one_minus_beta2, float step_size, float bias_correction2_sqrt,
+                        float eps, float clip, const float* grad_sumsq, void* stream);
 
 #ifdef __cplusplus
 }

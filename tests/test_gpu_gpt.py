@@ -1,8 +1,8 @@
 """Config 5: the full GPT train step (12 layers, hidden 768, 12 heads, SwiGLU,
-RMSNorm, vocab 50257, B=8, S=1024) with attention, RoPE, the loss and the
-RMSNorms on the HIP kernels, 20 steps, against the same harness with the eager
-attention math, the eager loss and the eager RMSNorm swapped in (same seed for
-init and data).  The two runs share
+RMSNorm, vocab 50257, B=8, S=1024) with attention, RoPE, the loss, the
+RMSNorms, the SwiGLU activation and the optimizer step on the HIP kernels, 20
+steps, against the same harness with the reference's eager ops swapped in for
+all of them (same seed for init and data).  The two runs share
 every other kernel, so the loss difference isolates the numerics of the
 kernels."""
 import pytest

@@ -336,3 +336,82 @@ def test_rmsnorm_rounds_n_to_the_input_dtype_before_the_weight():
     nb = torch.from_numpy(n).to(torch.bfloat16).double().numpy()
     np.testing.assert_array_equal(y_round, nb * w)
     assert not np.array_equal(y_round, n * w)
+
+
+# ---- SwiGLU (oracle/mlp.py) ----
+
+def test_swiglu_matches_torch_float64_and_autograd():
+    from oracle import swiglu_backward, swiglu_forward
+    g = torch.Generator().manual_seed(21)
+    gu = (torch.randn(6, 2 * 10, generator=g, dtype=torch.float64) * 3).requires_grad_(True)
+    gate, up = gu.chunk(2, dim=-1)
+    h = torch.nn.functional.silu(gate) * up
+    dh = torch.randn(6, 10, generator=g, dtype=torch.float64)
+    h.backward(dh)
+    np.testing.assert_allclose(swiglu_forward(gu.detach().numpy()), h.detach().numpy(),
+                               rtol=1e-14, atol=1e-15)
+    np.testing.assert_allclose(swiglu_backward(gu.detach().numpy(), dh.numpy()),
+                               gu.grad.numpy(), rtol=1e-12, atol=1e-14)
+
+
+def test_swiglu_closed_forms_and_finite_differences():
+    from oracle import swiglu_backward, swiglu_forward
+    gu = np.array([[0.0, 40.0, -40.0, 2.0, 3.0, -1.5]])
+    h = swiglu_forward(gu)
+    np.testing.assert_allclose(h[0], [0.0, 40.0 * 3.0, -40.0 * np.exp(-40.0) * -1.5], rtol=1e-12,
+                               atol=1e-300)
+    rng = np.random.default_rng(22)
+    x = rng.normal(size=(3, 8)) * 2
+    dh = rng.normal(size=(3, 4))
+    grad = swiglu_backward(x, dh)
+    eps = 1e-6
+    fd = np.zeros_like(x)
+    for i in range(3):
+        for j in range(8):
+            xp, xm = x.copy(), x.copy()
+            xp[i, j] += eps
+            xm[i, j] -= eps
+            fd[i, j] = ((swiglu_forward(xp) - swiglu_forward(xm)) * dh).sum() / (2 * eps)
+    np.testing.assert_allclose(grad, fd, rtol=1e-6, atol=1e-9)
+
+
+def test_swiglu_rounds_silu_before_the_product():
+    from oracle import swiglu_forward
+    g = torch.tensor([1.3, 0.7, 2.9, -0.4], dtype=torch.bfloat16).double()
+    u = torch.tensor([1.01, 3.3, 0.51, 7.7], dtype=torch.bfloat16).double()
+    gu = torch.cat([g, u]).numpy()[None]
+    ref = (torch.nn.functional.silu(g.to(torch.bfloat16)) * u.to(torch.bfloat16)).double().numpy()
+    got = torch.from_numpy(swiglu_forward(gu, torch.bfloat16)).to(torch.bfloat16).double().numpy()
+    np.testing.assert_array_equal(got[0], ref)
+
+
+# ---- optimizer step (oracle/optimizer.py) ----
+
+def test_adamw_matches_torch_adamw_float64():
+    from oracle import adamw_step
+    g = torch.Generator().manual_seed(31)
+    p0 = torch.randn(50, generator=g, dtype=torch.float64)
+    ref = p0.clone().requires_grad_(True)
+    opt = torch.optim.AdamW([ref], lr=3e-3, betas=(0.9, 0.95), weight_decay=0.1, eps=1e-8)
+    p, m, v = p0.numpy(), np.zeros(50), np.zeros(50)
+    for t in range(1, 6):
+        grad = torch.randn(50, generator=g, dtype=torch.float64)
+        ref.grad = grad.clone()
+        opt.step()
+        p, m, v = adamw_step(p, m, v, grad.numpy(), t, 3e-3, (0.9, 0.95), 1e-8, 0.1)
+        np.testing.assert_allclose(p, ref.detach().numpy(), rtol=1e-13, atol=1e-15)
+        np.testing.assert_allclose(m, opt.state[ref]["exp_avg"].numpy(), rtol=1e-13)
+        np.testing.assert_allclose(v, opt.state[ref]["exp_avg_sq"].numpy(), rtol=1e-13)
+
+
+def test_adamw_first_step_is_signed_lr_and_clip_scales_to_threshold():
+    from oracle import adamw_step, clip_gradient
+    grad = np.array([3.0, -0.02, 1e-3, -7.0])
+    p, _, _ = adamw_step(np.zeros(4), np.zeros(4), np.zeros(4), grad, 1, 1e-2, (0.9, 0.95),
+                         1e-12, 0.0)
+    np.testing.assert_allclose(p, -1e-2 * np.sign(grad), rtol=1e-8)
+    gc, norm = clip_gradient(grad, 1.0)
+    assert abs(norm - np.sqrt((grad ** 2).sum())) < 1e-12
+    np.testing.assert_allclose(np.sqrt((gc ** 2).sum()), 1.0 * norm / (norm + 1e-6), rtol=1e-12)
+    g2, _ = clip_gradient(grad * 1e-3, 1.0)
+    np.testing.assert_array_equal(g2, grad * 1e-3)  # below the threshold: unchanged
