@@ -624,7 +624,7 @@ mi_status mi_grad_sumsq(mi_dtype grad_dtype, int64_t n, const void* grad, float*
   if (workspace_elems < mi_adamw_workspace())
     return fail(MI_ERR_INVALID_ARGUMENT, "workspace holds %lld floats, %lld needed",
                 (long long)workspace_elems, (long long)mi_adamw_workspace());
-  const bool vec = ((uintptr_t)grad) % (4 * elem_size(grad_dtype)) == 0;
+  const bool vec = ((uintptr_t)grad) % 16 == 0;
   return launched(mi::launch_grad_sumsq(grad_dtype, n, grad, vec, workspace, workspace + 1,
                                         (hipStream_t)stream),
                   "grad_sumsq");

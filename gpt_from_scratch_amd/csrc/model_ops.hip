@@ -805,65 +805,82 @@ hipError_t launch_swiglu(bool bwd, int dtype, int64_t rows, int64_t inter, const
 //     step_size = lr / (1 - b1^t)     (bias corrections computed by the host)
 //   and the model's copy param <- round_p(p) (the all-gather into the bf16
 //   parameter buffer, :95).
-// The squared norm is reduced deterministically: ADAM_PARTS fixed contiguous
-// slices into partial sums, then one workgroup sums them in order.  The step
+// The squared norm is reduced deterministically: ADAM_PARTS workgroups with a
+// fixed grid-stride partition write partial sums, then one workgroup sums them
+// in order.  The step
 // kernel reads the norm from device memory, so nothing waits for the host.
 // ---------------------------------------------------------------------------
 namespace {
 
-constexpr int ADAM_PARTS = 1024;
+constexpr int ADAM_PARTS = 4096;  // workgroups of the norm pass = partial sums
 constexpr int ADAM_T = 256;
+constexpr int ADAM_STEP_GRID = 1024;  // measured best for read + write streams
 
+// 16 bytes of the gradient as floats (8 16-bit or 4 fp32 elements)
 template <int GT>
-__global__ __launch_bounds__(ADAM_T) void grad_sumsq_partial_kernel(const void* grad, int64_t n,
-                                                                    int64_t chunk, bool vec,
-                                                                    float* partial) {
-  const int64_t start = (int64_t)blockIdx.x * chunk;
-  const int64_t end = min(start + chunk, n);
+__device__ __forceinline__ float sumsq16(const u32x4& v) {
   float s = 0.f;
-  if (start < end) {
-    int64_t i = start;
-    if (vec) {
-      const int64_t vend = start + ((end - start) & ~(int64_t)3);
-      const void* base = grad;
-      for (int64_t k = start + 4 * (int64_t)threadIdx.x; k < vend; k += 4 * ADAM_T) {
-        float g[4];
-        ld4<GT>(base, k, g);
+  if constexpr (GT == 0) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) s = __builtin_fmaf(g[e], g[e], s);
-      }
-      i = vend;
-    }
-    typedef typename Store<GT>::type T;
-    for (int64_t k = i + threadIdx.x; k < end; k += ADAM_T) {
-      const float g = Store<GT>::ld((const T*)grad, k);
+    for (int e = 0; e < 4; ++e) {
+      const float g = __uint_as_float(v[e]);
       s = __builtin_fmaf(g, g, s);
     }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float g = elem<GT>(v, e);
+      s = __builtin_fmaf(g, g, s);
+    }
+  }
+  return s;
+}
+
+// Grid-stride over 16-byte vectors (one per lane per iteration, consecutive
+// across the grid: the streaming pattern that reads fastest), then the
+// elements after the last whole vector.  Block b's partial sum goes to
+// partial[b]; the grid size is fixed, so the summation order is too.
+template <int GT>
+__global__ __launch_bounds__(ADAM_T) void grad_sumsq_partial_kernel(const void* grad, int64_t n,
+                                                                    bool vec, float* partial) {
+  constexpr int EPV = GT == 0 ? 4 : 8;  // elements per 16-byte vector
+  const int64_t nv = vec ? n / EPV : 0;
+  const int64_t stride = (int64_t)gridDim.x * ADAM_T;
+  const int64_t t = (int64_t)blockIdx.x * ADAM_T + threadIdx.x;
+  float s = 0.f;
+  const u32x4* gv = (const u32x4*)grad;
+  for (int64_t q = t; q < nv; q += stride) s += sumsq16<GT>(__builtin_nontemporal_load(gv + q));
+  typedef typename Store<GT>::type T;
+  for (int64_t k = nv * EPV + t; k < n; k += stride) {
+    const float g = Store<GT>::ld((const T*)grad, k);
+    s = __builtin_fmaf(g, g, s);
   }
   s = wave_sum(s);
   __shared__ float ws[ADAM_T / 64];
   if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
   __syncthreads();
   if (threadIdx.x == 0) {
-    float t = 0.f;
+    float u = 0.f;
 #pragma unroll
-    for (int w = 0; w < ADAM_T / 64; ++w) t += ws[w];
-    partial[blockIdx.x] = t;
+    for (int w = 0; w < ADAM_T / 64; ++w) u += ws[w];
+    partial[blockIdx.x] = u;
   }
 }
 
 // out[0] = sum of partial[0 .. ADAM_PARTS) in a fixed order (one workgroup)
-__global__ __launch_bounds__(ADAM_PARTS) void grad_sumsq_final_kernel(const float* partial,
-                                                                      float* out) {
-  float s = partial[threadIdx.x];
+__global__ __launch_bounds__(1024) void grad_sumsq_final_kernel(const float* partial,
+                                                                float* out) {
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < ADAM_PARTS / 1024; ++k) s += partial[k * 1024 + threadIdx.x];
   s = wave_sum(s);
-  __shared__ float ws[ADAM_PARTS / 64];
+  __shared__ float ws[16];
   if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
   __syncthreads();
   if (threadIdx.x == 0) {
     float t = 0.f;
 #pragma unroll
-    for (int w = 0; w < ADAM_PARTS / 64; ++w) t += ws[w];
+    for (int w = 0; w < 16; ++w) t += ws[w];
     out[0] = t;
   }
 }
@@ -906,9 +923,9 @@ __global__ __launch_bounds__(ADAM_T) void adamw_step_kernel(AdamArgs a, bool vec
     const int64_t i = 4 * q;
     float g[4];
     ld4<GT>(a.grad, i, g);
-    f32x4 p = *(const f32x4*)(a.master + i);
-    f32x4 m = *(const f32x4*)(a.m + i);
-    f32x4 v = *(const f32x4*)(a.v + i);
+    f32x4 p = __builtin_nontemporal_load((const f32x4*)(a.master + i));
+    f32x4 m = __builtin_nontemporal_load((const f32x4*)(a.m + i));
+    f32x4 v = __builtin_nontemporal_load((const f32x4*)(a.v + i));
     float po[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -920,9 +937,9 @@ __global__ __launch_bounds__(ADAM_T) void adamw_step_kernel(AdamArgs a, bool vec
       v[e] = ve;
       po[e] = pe;
     }
-    *(f32x4*)(a.master + i) = p;
-    *(f32x4*)(a.m + i) = m;
-    *(f32x4*)(a.v + i) = v;
+    __builtin_nontemporal_store(p, (f32x4*)(a.master + i));
+    __builtin_nontemporal_store(m, (f32x4*)(a.m + i));
+    __builtin_nontemporal_store(v, (f32x4*)(a.v + i));
     if (a.param) st4<PT>(a.param, i, po);
   }
   // elements after the last full vector (all of them when !vec)
@@ -944,7 +961,7 @@ template <int GT>
 hipError_t launch_adamw_g(int p_dtype, const AdamArgs& a, bool vec, hipStream_t st) {
   const int64_t work = vec ? a.n / 4 : a.n;
   const int64_t want = (work + ADAM_T - 1) / ADAM_T;
-  const dim3 grid((unsigned)(want < 4096 ? (want > 0 ? want : 1) : 4096));
+  const dim3 grid((unsigned)(want < ADAM_STEP_GRID ? (want > 0 ? want : 1) : ADAM_STEP_GRID));
   if (p_dtype == 2) hipLaunchKernelGGL((adamw_step_kernel<GT, 2>), grid, dim3(ADAM_T), 0, st, a, vec);
   else if (p_dtype == 1) hipLaunchKernelGGL((adamw_step_kernel<GT, 1>), grid, dim3(ADAM_T), 0, st, a, vec);
   else hipLaunchKernelGGL((adamw_step_kernel<GT, 0>), grid, dim3(ADAM_T), 0, st, a, vec);
@@ -957,19 +974,16 @@ int64_t adam_parts() { return ADAM_PARTS; }
 
 hipError_t launch_grad_sumsq(int g_dtype, int64_t n, const void* grad, bool vec, float* out,
                              float* partial, hipStream_t st) {
-  // contiguous slices of a multiple of 4 elements, one per workgroup
-  int64_t chunk = (n + ADAM_PARTS - 1) / ADAM_PARTS;
-  chunk = (chunk + 3) & ~(int64_t)3;
   if (g_dtype == 2)
     hipLaunchKernelGGL(grad_sumsq_partial_kernel<2>, dim3(ADAM_PARTS), dim3(ADAM_T), 0, st, grad,
-                       n, chunk, vec, partial);
+                       n, vec, partial);
   else if (g_dtype == 1)
     hipLaunchKernelGGL(grad_sumsq_partial_kernel<1>, dim3(ADAM_PARTS), dim3(ADAM_T), 0, st, grad,
-                       n, chunk, vec, partial);
+                       n, vec, partial);
   else
     hipLaunchKernelGGL(grad_sumsq_partial_kernel<0>, dim3(ADAM_PARTS), dim3(ADAM_T), 0, st, grad,
-                       n, chunk, vec, partial);
-  hipLaunchKernelGGL(grad_sumsq_final_kernel, dim3(1), dim3(ADAM_PARTS), 0, st, partial, out);
+                       n, vec, partial);
+  hipLaunchKernelGGL(grad_sumsq_final_kernel, dim3(1), dim3(1024), 0, st, partial, out);
   return hipGetLastError();
 }
 
