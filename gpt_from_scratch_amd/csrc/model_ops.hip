@@ -166,7 +166,7 @@ __global__ __launch_bounds__(XT) void xent_bwd_kernel(const void* logits, int64_
   const u32x4* zv = (const u32x4*)(z + head);
   u32x4* gv = (u32x4*)(gz + head);
   constexpr int N = Vec16<DT>::N;
-  constexpr int U = 4;
+  constexpr int U = 8;  // 16-byte vectors in flight per thread (4: 1.5% slower)
   for (int64_t i0 = tid; i0 < nvec; i0 += U * XT) {
     u32x4 v[U];
 #pragma unroll
