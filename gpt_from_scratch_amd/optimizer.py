@@ -24,7 +24,8 @@ With ``torch.optim.AdamW`` the step is:
 The reference instead converts the gradient buffer to an fp32 copy, runs
 torch's multi-tensor AdamW (several passes over the master and the moments)
 and converts the master back.  Any other ``optimizer_cls`` runs the
-reference's own sequence on torch's optimizer.
+reference's own sequence on torch's optimizer (on the GPU: parameters
+elsewhere are refused, as by every operator of this package).
 
 The moments live in ``self.optimizer.state`` under torch's names, so
 ``state_dict()`` / ``load_state_dict()`` read and write torch's AdamW format,
@@ -32,8 +33,6 @@ and the hyperparameters are read from ``self.optimizer.param_groups`` at every
 step (a learning-rate schedule that edits them works as with torch).
 """
 from __future__ import annotations
-
-import math
 
 import torch
 
@@ -59,6 +58,7 @@ class DistributedOptimizer:
         self.clip_grad = clip_grad
         self.dtype = dtype
         self.params = [p for p in model.parameters() if p.requires_grad]
+        _lib._require_gpu(*self.params)
         total = sum(p.numel() for p in self.params)
         self.padding_size = 0
         self.padded_numel = total
@@ -78,11 +78,13 @@ class DistributedOptimizer:
         self.optimizer = optimizer_cls([self.fp32_master_shard], **optimizer_kwargs)
         self.fused = optimizer_cls is torch.optim.AdamW and self._fusable()
         self._ws = None
+        self._norm_valid = False
 
     def _fusable(self) -> bool:
         g = self.optimizer.param_groups[0]
+        # the fused step keeps torch's default (non-capturable) state layout
         return (not g.get("amsgrad", False) and not g.get("maximize", False)
-                and self.fp32_master_shard.is_cuda)
+                and not g.get("capturable", False) and not g.get("differentiable", False))
 
     def zero_grad(self):
         """Clear the gradient buffer (never set grads to None: they point into it)."""
@@ -115,11 +117,15 @@ class DistributedOptimizer:
         clip = self.clip_grad is not None and self.clip_grad > 0.0
         if clip:
             _lib.grad_sumsq(self.grad_buffer, self._ws)
+        self._norm_valid = clip
         _lib.adamw_step(self.grad_buffer, master.data, state["exp_avg"], state["exp_avg_sq"],
                         self.param_buffer, hp, self._ws if clip else None)
 
     def _step_reference(self):
-        """core/optimizer.py:79-104 at one rank, for optimizers other than AdamW."""
+        """core/optimizer.py:79-104 at one rank, on torch's optimizer: other optimizer
+        classes, and AdamW variants the fused step does not cover (amsgrad, maximize,
+        capturable, differentiable)."""
+        self._norm_valid = False
         reduced = self.grad_buffer.clone()
         if self.clip_grad is not None and self.clip_grad > 0.0:
             norm = torch.sqrt(torch.sum(reduced.to(torch.float32) ** 2))
@@ -131,9 +137,10 @@ class DistributedOptimizer:
         self.param_buffer.copy_(self.fp32_master_shard.detach().to(self.dtype))
 
     def grad_norm(self) -> torch.Tensor:
-        """The global gradient norm of the last step (a device tensor), as clipped against."""
-        if self._ws is None:
-            raise RuntimeError("no step has run")
+        """The global gradient norm of the last fused step (a device tensor), as
+        clipped against.  Only computed when clipping is on."""
+        if not self._norm_valid:
+            raise RuntimeError("no fused step with clipping has run")
         return torch.sqrt(self._ws[0])
 
     def state_dict(self):

@@ -161,3 +161,48 @@ def test_cross_entropy_python_checks():
         vocab_parallel_cross_entropy(z, torch.zeros(4, 3))
     with pytest.raises(RuntimeError, match="ROCm GPUs only"):
         vocab_parallel_cross_entropy(z, torch.zeros(4, 3, dtype=torch.int64))
+
+
+def test_model_op_entry_points_reject_bad_arguments():
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(16)
+    # RMSNorm: weight dtype must be x's or fp32; row stride >= hidden; workspace size
+    assert lib.mi_rmsnorm_fwd(2, 1, 4, 768, 1e-6, fake, 768, fake, fake, 768, fake, None) == 1
+    assert b"weight" in lib.mi_last_error()
+    assert lib.mi_rmsnorm_fwd(2, 2, 4, 768, 1e-6, fake, 700, fake, fake, 768, fake, None) == 1
+    assert lib.mi_rmsnorm_fwd(2, 2, 4, 768, -1.0, fake, 768, fake, fake, 768, fake, None) == 1
+    assert b"eps" in lib.mi_last_error()
+    need = lib.mi_rmsnorm_bwd_workspace(4, 768)
+    assert need == 768 and lib.mi_rmsnorm_bwd_workspace(0, 768) == 0
+    assert lib.mi_rmsnorm_bwd(2, 2, 4, 768, fake, 768, fake, fake, fake, 768, fake, 768, fake,
+                              fake, need - 1, None) == 1
+    assert b"workspace" in lib.mi_last_error()
+    # SwiGLU: gate_up rows must hold 2 * inter elements
+    assert lib.mi_swiglu_fwd(2, 4, 3072, fake, 3072, fake, 3072, None) == 1
+    assert lib.mi_swiglu_bwd(2, 4, 3072, fake, 6144, None, 3072, fake, 6144, None) == 1
+    assert b"dout" in lib.mi_last_error()
+    # optimizer: workspace size, clip without a norm, non-finite hyperparameters
+    ws = lib.mi_adamw_workspace()
+    assert ws > 1
+    assert lib.mi_grad_sumsq(2, 100, fake, fake, ws - 1, None) == 1
+    hp = [0.99997, 0.1, 0.95, 0.05, 3e-3, 0.2236, 1e-8]
+    assert lib.mi_adamw_step(2, 2, 100, fake, fake, fake, fake, fake, *hp, 1.0, None, None) == 1
+    assert b"grad_sumsq" in lib.mi_last_error()
+    assert lib.mi_adamw_step(2, 2, 100, fake, fake, fake, fake, fake, *hp[:-1], float("nan"),
+                             0.0, None, None) == 1
+    assert lib.mi_adamw_step(2, 2, 0, fake, fake, fake, fake, fake, *hp, 0.0, None, None) == 1
+
+
+def test_model_op_python_checks():
+    import torch
+    from gpt_from_scratch_amd import DistributedOptimizer, rms_norm, swiglu
+    with pytest.raises(ValueError, match="even"):
+        swiglu(torch.randn(4, 7))
+    with pytest.raises(RuntimeError, match="ROCm GPUs only"):
+        swiglu(torch.randn(4, 8))
+    with pytest.raises(ValueError, match="last dim"):
+        rms_norm(torch.randn(4, 8), torch.ones(7))
+    with pytest.raises(RuntimeError, match="ROCm GPUs only"):
+        rms_norm(torch.randn(4, 8), torch.ones(8))
+    with pytest.raises(RuntimeError, match="ROCm GPUs only"):
+        DistributedOptimizer(torch.nn.Linear(4, 3), torch.optim.AdamW, {"lr": 1e-2})

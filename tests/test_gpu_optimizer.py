@@ -117,3 +117,29 @@ def test_grad_sumsq_matches_torch(gpu):
         _lib.grad_sumsq(g, ws)
         ref = float(g.double().pow(2).sum())
         assert abs(float(ws[0]) - ref) <= 1e-5 * ref + 1e-30
+
+
+def test_other_optimizers_and_variants_take_the_reference_sequence(gpu):
+    """optimizer_cls other than AdamW, and AdamW with amsgrad, run torch's own step
+    on the same flat buffers, as core/optimizer.py does for any optimizer_cls."""
+    from gpt_from_scratch_amd.optimizer import DistributedOptimizer
+    for cls, kw in ((torch.optim.SGD, {"lr": 1e-2, "momentum": 0.9}),
+                    (torch.optim.AdamW, dict(KW, amsgrad=True))):
+        opt = DistributedOptimizer(_model(gpu, 11), cls, kw, clip_grad=1.0)
+        assert not opt.fused
+        ref = opt.fp32_master_shard.detach().clone().requires_grad_(True)
+        ref_opt = cls([ref], **kw)
+        for step in range(1, 4):
+            g = _grads(opt.grad_buffer.numel(), step, gpu, 1.0)
+            opt.grad_buffer.copy_(g)
+            opt.step()
+            gc = g.clone()
+            norm = torch.sqrt(torch.sum(gc.float() ** 2))
+            if norm > 1.0:
+                gc.mul_(1.0 / (norm + 1e-6))
+            ref.grad = gc.float()
+            ref_opt.step()
+            assert torch.equal(opt.fp32_master_shard.detach(), ref.detach())
+            assert torch.equal(opt.param_buffer, ref.detach().to(torch.bfloat16))
+        with pytest.raises(RuntimeError, match="no fused step"):
+            opt.grad_norm()
