@@ -149,3 +149,15 @@ def test_strided_rows_aliasing_and_determinism(gpu):
     dy2, dw2 = dy.clone(), torch.empty_like(w)
     _lib.rmsnorm_bwd(x, w, rstd, dy2, dy2, dw2, ws)
     assert torch.equal(dx, dy2) and torch.equal(dw, dw2)
+
+
+def test_backward_with_several_rows_per_wave(gpu):
+    """5000 rows > 256 partial rows x 16 waves: every wave of the backward loops
+    over more than one row, and the dw partials cover all of them."""
+    rows, H = 5000, 768
+    x = seeded((rows, H), 61, std=1.5)
+    w = (1.0 + 0.1 * seeded((H,), 62, dtype=torch.float32)).to(torch.bfloat16)
+    dy = seeded((rows, H), 63)
+    y, dx, dw = _run(x.to(gpu), w.to(gpu), dy.to(gpu))
+    _check_forward(y, x, w, EPS)
+    _check_backward(dx, dw, x, w, dy, EPS)

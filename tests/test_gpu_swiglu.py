@@ -104,3 +104,15 @@ def test_reference_ops_at_config5_shape(gpu):
         assert eq >= 0.99, eq
         rel = ((got.float() - want.float()).abs() / want.float().abs().clamp_min(1e-30))
         assert float(rel.max()) <= 3 * 2 ** -8 + 1e-5
+
+
+def test_more_rows_than_one_grid_column(gpu):
+    """70000 rows: the row dimension of the grid is capped at 65535 and loops."""
+    gu = seeded((70000, 32), 71, std=2.0)
+    dh = seeded((70000, 16), 72)
+    h, dgu = _run(gu.to(gpu), dh.to(gpu))
+    _close("h", h, swiglu_forward(_np(gu), torch.bfloat16), torch.bfloat16, 3)
+    ref_d = swiglu_backward(_np(gu), _np(dh), torch.bfloat16)
+    _close("d_gate", dgu[:, :16], ref_d[:, :16], torch.bfloat16, 1,
+           _dgate_floor(_np(gu), _np(dh), torch.bfloat16))
+    _close("d_up", dgu[:, 16:], ref_d[:, 16:], torch.bfloat16, 3)
