@@ -10,10 +10,12 @@ host keeps the GPU queue full.
 
 Printed: ONE JSON line with the metric of BASELINE.json (algorithmic TFLOP/s of
 fwd+bwd, causal counted as half of dense: 7*B*H*S^2*D flops per step) from a
-timed pass of K steps with events only at its ends, the per-kernel durations
-from a second timed pass of K steps with an event before every launch, the
-roofline of the dominant kernel, the RoPE bandwidth, and the CPU baseline (the
-oracle's fp32 eager attention on the host cores).
+timed pass of K steps with events only at its ends (after W untimed steps: the
+GPU needs tens of milliseconds of load to reach steady clocks), the per-kernel
+durations from K back-to-back launches of each kernel alone, the roofline of
+the dominant kernel, the RoPE bandwidth, the train step's fused operators and
+config-5 tokens/s, and the CPU baseline (the oracle's fp32 eager attention on
+the host cores).
 
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
 """
@@ -38,14 +40,16 @@ def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=20)
+    # ~45 ms of untimed steps: the GPU needs tens of milliseconds of sustained
+    # load to reach its steady clocks (20 steps measured 18% slower)
+    ap.add_argument("--warmup", type=int, default=500)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget of the baseline sample")
     ap.add_argument("--no-gpt", action="store_true",
                     help="skip the config-5 GPT train-step measurement")
     ap.add_argument("--no-model-ops", action="store_true",
-                    help="skip the config-5 cross-entropy kernel measurement")
+                    help="skip the config-5 model-operator kernel measurements")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the timed steps, run a plain elementwise kernel that reads and "
                          "writes 256 MiB each (reference point for HBM byte counters)")
@@ -340,15 +344,11 @@ def main():
              ("attn_bwd_preprocess", lib.mi_attn_bwd_preprocess, pre_args),
              ("attn_bwd", lib.mi_attn_bwd_grads, grads_args)]
 
-    def step(evs=None):
-        for i, (name, fn, a) in enumerate(calls):
-            if evs is not None:
-                evs[i].record(stream)
+    def step():
+        for name, fn, a in calls:
             st = fn(*a)
             if st != 0:
                 raise RuntimeError(f"{name}: {lib.mi_last_error().decode()}")
-        if evs is not None:
-            evs[len(calls)].record(stream)
 
     for _ in range(args.warmup):
         step()
@@ -366,18 +366,20 @@ def main():
     torch.cuda.synchronize()
     ms_per_step = t_start.elapsed_time(t_end) / args.steps
 
-    # Second timed pass of K steps with an event before every launch, for the
-    # per-kernel durations (each interval also holds the launch gap before the
-    # next kernel; the events themselves are kept out of the first pass).
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(len(calls) + 1)]
-           for _ in range(args.steps)]
-    torch.cuda.synchronize()
-    for s in range(args.steps):
-        step(evs[s])
-    torch.cuda.synchronize()
+    # Per-kernel durations: each kernel of the step launched K times back to
+    # back on its own (its inputs are unchanged, so every launch redoes the same
+    # work), with events only at the ends of each run; the intervals hold the
+    # K - 1 dispatch gaps between launches, not the events' own overhead.
     per_kernel_us = {}
-    for i, (name, _, _) in enumerate(calls):
-        per_kernel_us[name] = statistics.mean(e[i].elapsed_time(e[i + 1]) for e in evs) * 1e3
+    for name, fn, a in calls:
+        k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        k0.record(stream)
+        for _ in range(args.steps):
+            fn(*a)
+        k1.record(stream)
+        torch.cuda.synchronize()
+        per_kernel_us[name] = k0.elapsed_time(k1) / args.steps * 1e3
 
     kflops = {"attn_fwd": flops["fwd"], "attn_bwd": flops["bwd"]}
     kernels = {}
