@@ -729,8 +729,9 @@ hipError_t launch_dq_e(const AttnArgs& a, hipStream_t st) {
   return launch_dq_d<E, 128>(a, st);
 }
 
-// D = 128: the two kinds need different register budgets (the dK/dV kind
-// alone runs at 1 wave/SIMD), so they stay separate launches.
+// D = 128: two launches.  Both kinds sit at the 256-register limit of two waves
+// per SIMD there (the dK/dV kind spills), and one combined launch measured
+// 10-15% slower than the two.
 template <typename E>
 hipError_t launch_both_e(const AttnArgs& a, hipStream_t st) {
   if (a.D == 64) return launch_both_d<E, 64>(a, st);
