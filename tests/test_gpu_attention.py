@@ -243,3 +243,41 @@ def test_errors_surface_as_exceptions(gpu):
     q = torch.randn(1, 1, 64, 64, device=gpu, dtype=torch.bfloat16)
     with pytest.raises(TypeError):
         apply_flash_attn(q, q.float(), q)
+
+
+@pytest.mark.parametrize("B,H,S,D", [(2, 3, 512, 64), (1, 4, 1024, 128)])
+def test_backward_deterministic_writes_every_output_keeps_inputs(gpu, B, H, S, D):
+    """mi_attn_bwd_grads on NaN-filled outputs, three times: every element of dQ,
+    dK and dV is written, the runs agree bit for bit (no atomics), and Q, K, V,
+    dO, lse and delta are unchanged."""
+    import ctypes
+    import math
+    from gpt_from_scratch_amd import _lib
+    lib = _lib.lib()
+    g = torch.Generator(device=gpu).manual_seed(7)
+    Q, K, V, dO = (torch.randn(B, H, S, D, generator=g, device=gpu).to(torch.bfloat16)
+                   for _ in range(4))
+    O = torch.empty_like(Q)
+    M = torch.empty(B, H, S, device=gpu)
+    Dl = torch.empty_like(M)
+    dQ, dK, dV = (torch.full_like(Q, float("nan")) for _ in range(3))
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    ST = lambda t: (ctypes.c_int64 * 4)(*t.stride())
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    sc = 1 / math.sqrt(D)
+    assert lib.mi_attn_fwd(2, B, H, S, D, 1, sc, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(O),
+                           ST(O), P(M), sp) == 0
+    assert lib.mi_attn_bwd_preprocess(2, B, H, S, D, P(O), ST(O), P(dO), ST(dO), P(Dl), sp) == 0
+    before = [t.clone() for t in (Q, K, V, dO, M, Dl)]
+    runs = []
+    for _ in range(3):
+        assert lib.mi_attn_bwd_grads(2, B, H, S, D, 1, sc, P(Q), ST(Q), P(K), ST(K), P(V), ST(V),
+                                     P(dO), ST(dO), P(M), P(Dl), P(dQ), ST(dQ), P(dK), ST(dK),
+                                     P(dV), ST(dV), sp) == 0
+        torch.cuda.synchronize()
+        runs.append([t.clone() for t in (dQ, dK, dV)])
+    for t in runs[0]:
+        assert not bool(torch.isnan(t).any())
+    for r in runs[1:]:
+        assert all(torch.equal(a, b) for a, b in zip(runs[0], r))
+    assert all(torch.equal(a, b) for a, b in zip(before, (Q, K, V, dO, M, Dl)))
