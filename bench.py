@@ -10,8 +10,8 @@ host keeps the GPU queue full.
 
 Printed: ONE JSON line with the metric of BASELINE.json (algorithmic TFLOP/s of
 fwd+bwd, causal counted as half of dense: 7*B*H*S^2*D flops per step) from a
-timed pass of K steps with events only at its ends (after W untimed steps: the
-GPU needs tens of milliseconds of load to reach steady clocks), the per-kernel
+timed pass of K steps with events only at its ends (after at least 50 ms of
+untimed steps for the GPU to reach steady clocks, then W untimed steps), the per-kernel
 durations from K back-to-back launches of each kernel alone, the roofline of
 the dominant kernel, the RoPE bandwidth, the train step's fused operators and
 config-5 tokens/s, and the CPU baseline (the oracle's fp32 eager attention on
@@ -40,9 +40,9 @@ def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=100)
-    # ~45 ms of untimed steps: the GPU needs tens of milliseconds of sustained
-    # load to reach its steady clocks (20 steps measured 18% slower)
-    ap.add_argument("--warmup", type=int, default=500)
+    # untimed steps after the clock warm-up (which alone takes care of the
+    # steady clocks: without it, 20 warm-up steps measured 18% slower than 500)
+    ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=12.0,
                     help="approximate CPU time budget of the baseline sample")
@@ -350,6 +350,20 @@ def main():
             if st != 0:
                 raise RuntimeError(f"{name}: {lib.mi_last_error().decode()}")
 
+    # Clock warm-up, untimed, before the W warm-up steps: the GPU reaches its
+    # steady clocks only after tens of milliseconds of sustained load, so the
+    # step runs until 50 ms of GPU time have passed whatever W is.
+    clock_warmup_steps = 0
+    c0, c1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    c0.record(stream)
+    while True:
+        for _ in range(50):
+            step()
+        clock_warmup_steps += 50
+        c1.record(stream)
+        c1.synchronize()
+        if c0.elapsed_time(c1) >= 50.0 or clock_warmup_steps >= 20000:
+            break
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -446,7 +460,8 @@ def main():
     tflops = flops["total"] / (ms_per_step * 1e-3) / 1e12
     out = {
         "metric": METRIC, "value": round(tflops, 2), "unit": "TFLOP/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_per_step, 5),
+        "steps": args.steps, "warmup": args.warmup, "clock_warmup_steps": clock_warmup_steps,
+        "ms_per_step": round(ms_per_step, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded N(0,1) q/k/v/dO, RoPE theta=10000 on q/k)",
         "config": {"workload": "causal flash attention fwd+bwd (O, LSE, dQ, dK, dV), config 2",
