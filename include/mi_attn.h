@@ -34,14 +34,23 @@
 extern "C" {
 #endif
 
-typedef enum {
+/* The enums are int-sized in C; in C++ they get int as a fixed underlying type
+ * (same size and values), so that any int a C caller passes is a valid value
+ * for the implementation to reject. */
+#ifdef __cplusplus
+#define MI_ENUM_INT : int
+#else
+#define MI_ENUM_INT
+#endif
+
+typedef enum MI_ENUM_INT {
   MI_OK = 0,
   MI_ERR_INVALID_ARGUMENT = 1, /* bad shape, stride, pointer or dtype */
   MI_ERR_UNSUPPORTED = 2,      /* valid request that no kernel here covers */
   MI_ERR_LAUNCH = 3            /* the HIP runtime refused a launch */
 } mi_status;
 
-typedef enum { MI_F32 = 0, MI_F16 = 1, MI_BF16 = 2 } mi_dtype;
+typedef enum MI_ENUM_INT { MI_F32 = 0, MI_F16 = 1, MI_BF16 = 2 } mi_dtype;
 
 /* Library version, (major << 16) | minor. */
 int mi_version(void);
