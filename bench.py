@@ -308,7 +308,7 @@ def main():
     import torch
     from gpt_from_scratch_amd import _lib
     from gpt_from_scratch_amd.rope import apply_rope_qk
-    from oracle import rope_tables
+    from gpt_from_scratch_amd.position_embeddings import RotaryEmbedding
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -319,7 +319,8 @@ def main():
     g = torch.Generator().manual_seed(2)
     qkv = torch.randn(S, B, 3, H, D, generator=g).to(torch.bfloat16).to(dev)
     do = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16).to(dev)
-    cos, sin = (t.to(torch.bfloat16).to(dev) for t in rope_tables(D, S))
+    rot = RotaryEmbedding(D, max_position_embeddings=S, device="cpu")
+    cos, sin = (t.to(torch.bfloat16).to(dev) for t in (rot.cos_cached, rot.sin_cached))
     q, k, v = qkv.unbind(2)
     qr, kr = apply_rope_qk(q, k, cos, sin)
     Q, K, V = qr.permute(1, 2, 0, 3), kr.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3)
