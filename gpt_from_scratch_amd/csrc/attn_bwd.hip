@@ -42,9 +42,9 @@ template <int DT, int VEC>
 __global__ __launch_bounds__(256) void attn_delta_kernel(AttnArgs a, FastDiv divS, FastDiv divH,
                                                          uint32_t nrows) {
   typedef typename Store<DT>::type T;
-  const uint32_t t = blockIdx.x * 256 + threadIdx.x;
-  const uint32_t row = t >> 3;
-  const int sub = t & 7;
+  // 32 rows per workgroup; nrows < 2^31, so the row index fits 32 bits
+  const uint32_t row = blockIdx.x * 32u + (threadIdx.x >> 3);
+  const int sub = threadIdx.x & 7;
   float acc = 0.f;
   if (row < nrows) {
     const uint32_t bh = fdiv(row, divS);
@@ -744,7 +744,7 @@ template <int DT>
 hipError_t launch_delta_t(const AttnArgs& a, hipStream_t st) {
   const uint32_t nrows = (uint32_t)a.B * a.H * a.S;
   const FastDiv dS = make_fastdiv(a.S), dH = make_fastdiv(a.H);
-  const dim3 grid((nrows * 8 + 255) / 256);
+  const dim3 grid((uint32_t)(((uint64_t)nrows + 31) / 32));
   constexpr int V16 = (DT == 0) ? 4 : 8;
   if constexpr (DT != 0) {
     auto a16 = [](const TensorArg& t) {
