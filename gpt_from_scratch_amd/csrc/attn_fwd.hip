@@ -61,15 +61,25 @@ struct FwdCfg {
 };
 
 // LDS layout of a staged tile: BKV rows of D elements, no padding; the
-// 16-byte chunk c of row r sits at chunk position c ^ swz(r).
-//   K: swz = r & 7        the A-operand reads of K Q^T (each lane a 16-byte
-//                         chunk, eight consecutive rows per LDS cycle) land
-//                         on eight different chunk positions;
-//   V: swz = 2 * (r & 3)  the transposing reads of V^T (16-lane groups over
-//                         four consecutive rows and two adjacent chunks)
-//                         likewise.
-__device__ __forceinline__ int swz_k(int r) { return r & 7; }
-__device__ __forceinline__ int swz_v(int r) { return (r & 3) << 1; }
+// 16-byte chunk c of row r sits at chunk position c ^ swz(r).  The gfx950 LDS
+// has 64 four-byte banks: one 256-byte bank line holds two rows at D = 64 and
+// one row at D = 128, and a 16-byte read serves 16 lanes per cycle.
+//   K: the A-operand reads of K Q^T (each lane one 16-byte chunk, 16
+//      consecutive rows per cycle) must land on 16 different 16-byte bank
+//      groups: at D = 64 the two rows of a bank line differ in bit 0, so the
+//      8 chunk positions are spread over rows r and r + 8 by (r & 7) ^ bit 3;
+//      at D = 128 by r & 15.  (r & 7 alone at D = 64 measured half the read
+//      rate of a conflict-free pattern in a probe of this access.)
+//   V: the transposing reads of V^T cover four consecutive rows and four
+//      adjacent chunks per 32 lanes: 2 * (r & 3) at D = 64 (rows of one bank
+//      line differ in bit 0 already), 4 * (r & 3) at D = 128.
+// Both swizzles repeat within 16 rows, and the V swizzle within 8, which the
+// operand reads assume (K block offsets are multiples of 32 rows; the second
+// transposing read of an operand is 8 rows on).
+template <int D>
+__device__ __forceinline__ int swz_k(int r) { return D == 64 ? ((r & 7) ^ ((r >> 3) & 1)) : (r & 15); }
+template <int D>
+__device__ __forceinline__ int swz_v(int r) { return D == 64 ? ((r & 3) << 1) : ((r & 3) << 2); }
 
 constexpr float kRescaleSlack = 8.f;  // log2 units: probabilities stay <= 2^8
 
@@ -135,8 +145,8 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
   for (int m = 0; m < C::SPW; ++m) {
     const int r = (wave + 4 * m) * C::RPS + lane / C::CPR;
     const int pos = lane % C::CPR;
-    kdo[m] = (uint32_t)((r * a.k.ss + ((pos ^ swz_k(r)) << 3)) * 2);
-    vdo[m] = (uint32_t)((r * a.v.ss + ((pos ^ swz_v(r)) << 3)) * 2);
+    kdo[m] = (uint32_t)((r * a.k.ss + ((pos ^ swz_k<D>(r)) << 3)) * 2);
+    vdo[m] = (uint32_t)((r * a.v.ss + ((pos ^ swz_v<D>(r)) << 3)) * 2);
   }
   auto dma = [&](const uint16_t* base, int64_t ss, const uint32_t(&off)[C::SPW], int t,
                  uint16_t* tile) __attribute__((always_inline)) {
@@ -153,12 +163,12 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
   //   16((lane/16)%2) + 4(lane%4).
   int kro[C::KS], vro[C::DB];
 #pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) kro[ks] = l32 * D + (((2 * ks + g) ^ swz_k(l32)) << 3);
+  for (int ks = 0; ks < C::KS; ++ks) kro[ks] = l32 * D + (((2 * ks + g) ^ swz_k<D>(l32)) << 3);
 #pragma unroll
   for (int db = 0; db < C::DB; ++db) {
     const int r = 4 * g + ((lane & 15) >> 2);
     const int ch = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-    vro[db] = r * D + ((ch ^ swz_v(r)) << 3) + 4 * (lane & 1);
+    vro[db] = r * D + ((ch ^ swz_v<D>(r)) << 3) + 4 * (lane & 1);
   }
 
   // ---- per-wave compute pieces ----
