@@ -20,9 +20,9 @@
 //     transposing LDS read (ds_read_b64_tr_b16);
 //   * one tile per step (S, softmax, P V) with double buffers: the loads of
 //     tile j+1 run under step j, one barrier per step.  Only one S tile is live,
-//     so D = 64 fits 128 VGPRs and four waves per SIMD (three workgroups per CU
-//     at once), which hides the step's latency better than pipelining S_{j+1}
-//     under softmax_j inside a wave at half the occupancy;
+//     so D = 64 fits a three-waves-per-SIMD register budget (three workgroups
+//     per CU at once), which hides the step's latency better than pipelining
+//     S_{j+1} under softmax_j inside a wave at half the occupancy;
 //   * key tiles below the diagonal run a branch-free body; the diagonal tiles
 //     run a masked body that also skips tiles a wave cannot see;
 //   * the running max is only moved (and O, l rescaled) when a new score
@@ -56,8 +56,12 @@ struct FwdCfg {
   static constexpr int CPR = D / 8;                  // 16-byte chunks per row
   static constexpr int RPS = 64 / CPR;               // rows per 1 KB slice (one wave instruction)
   static constexpr int SPW = TILE * 2 / 1024 / 4;    // slices per wave per tile
-  // Waves per SIMD the register budget is held to: D = 64 fits 128 VGPRs.
-  static constexpr int WAVES_PER_EU = D == 64 ? 4 : 2;
+  // Waves per SIMD the register budget is held to.  D = 64 fits 128 VGPRs
+  // (four waves) with an 8-byte spill and the operand reads issued just in
+  // time; at three waves (up to 168 VGPRs, ~149 used) it runs 2-3% faster (also
+  // at S = 2048, where the grid would fill four), and config 2's 768 workgroups
+  // put only three on each CU anyway.
+  static constexpr int WAVES_PER_EU = D == 64 ? 3 : 2;
 };
 
 // LDS layout of a staged tile: BKV rows of D elements, no padding; the
