@@ -58,9 +58,8 @@ struct FwdCfg {
   static constexpr int SPW = TILE * 2 / 1024 / 4;    // slices per wave per tile
   // Waves per SIMD the register budget is held to.  D = 64 fits 128 VGPRs
   // (four waves) with an 8-byte spill and the operand reads issued just in
-  // time; at three waves (up to 168 VGPRs, ~149 used) it runs 2-3% faster (also
-  // at S = 2048, where the grid would fill four), and config 2's 768 workgroups
-  // put only three on each CU anyway.
+  // time; at three waves (up to 168 VGPRs, ~149 used) it runs 2-3% faster at
+  // configs B8 S1024 and B4 S2048 (both 768 workgroups, three per CU anyway).
   static constexpr int WAVES_PER_EU = D == 64 ? 3 : 2;
 };
 
