@@ -76,3 +76,58 @@ def rope_inputs(B, H, S, D, seed, std=1.0, dtype=torch.bfloat16, device="cuda"):
 
 def scale_of(D):
     return 1.0 / math.sqrt(D)
+
+
+def rescale_stress_inputs(S, D, device="cpu"):
+    """q, k, v, dO (bf16, [1, 4, S, D]) whose scores grow along the key axis: q's
+    axis-0 component is 8 and k's rises linearly to 100 * sqrt(D / 64), so the
+    top score of a query rises by more than 8 log2 units per 64-key tile."""
+    g = torch.Generator().manual_seed(71 + D)
+    q = torch.randn(1, 4, S, D, generator=g) * 0.5
+    k = torch.randn(1, 4, S, D, generator=g) * 0.5
+    v = torch.randn(1, 4, S, D, generator=g)
+    do = torch.randn(1, 4, S, D, generator=g)
+    q[..., 0] = 8.0
+    k[..., 0] = torch.linspace(0.0, 100.0 * math.sqrt(D / 64), S)
+    return tuple(t.to(torch.bfloat16).to(device) for t in (q, k, v, do))
+
+
+def grad_rounding_budget(q, k, v, do, o, causal):
+    """fp32 gradients of attention and an element-wise bound on how far a
+    computation that rounds like the reference may sit from them.
+
+    The reference rounds P to bf16 before dV = P^T dO and scale * dS to bf16
+    before dQ = dS K and dK = dS^T Q (core/myFlashAttn.py:1049, :1055, :1308), and
+    computes delta = rowsum(dO * O) from the bf16 O.  The bound allows one bf16
+    ulp (2^-8, twice round-to-nearest's half ulp) of each rounded term propagated
+    through its product, the resulting error of delta, and the rounding of the
+    gradient itself.  Returns (want, budget): dicts over "dq", "dk", "dv".
+    """
+    qf, kf, vf, dof = (t.float() for t in (q, k, v, do))
+    S, D = q.shape[-2], q.shape[-1]
+    sc = 1.0 / math.sqrt(D)
+    sco = (qf @ kf.transpose(-1, -2)) * sc
+    if causal:
+        sco = sco.masked_fill(torch.ones(S, S, dtype=torch.bool, device=q.device).triu(1),
+                              float("-inf"))
+    pr = torch.softmax(sco, dim=-1)
+    dp = dof @ vf.transpose(-1, -2)
+    ds = pr * (dp - (pr * dp).sum(-1, keepdim=True))
+    u = 2.0 ** -8
+    ddelta = u * (dof.abs() * o.float().abs()).sum(-1, keepdim=True)
+    want = {"dq": sc * (ds @ kf), "dk": sc * (ds.transpose(-1, -2) @ qf),
+            "dv": pr.transpose(-1, -2) @ dof}
+    budget = {
+        "dq": sc * (u * (ds.abs() @ kf.abs()) + ddelta * (pr @ kf.abs())),
+        "dk": sc * (u * (ds.abs().transpose(-1, -2) @ qf.abs())
+                    + (pr * ddelta).transpose(-1, -2) @ qf.abs()),
+        "dv": u * (pr.transpose(-1, -2) @ dof.abs()),
+    }
+    for n in budget:
+        budget[n] = budget[n] + u * want[n].abs() + 1e-4
+    return want, budget
+
+
+def budget_ratio(got, want, budget):
+    """Largest |got - want| / budget over the elements (<= 1 passes)."""
+    return float(((got.float() - want).abs() / budget).max())

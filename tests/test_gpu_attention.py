@@ -11,7 +11,8 @@ import math
 import pytest
 import torch
 
-from gpu_ref import (TOL_FP32, assert_close_bf16, metrics, reference, rope_inputs, seeded)
+from gpu_ref import (TOL_FP32, assert_close_bf16, budget_ratio, grad_rounding_budget, metrics,
+                     reference, rescale_stress_inputs, rope_inputs, seeded)
 from oracle import attention_backward, attention_forward, rope_apply, rope_tables
 
 pytestmark = pytest.mark.gpu
@@ -281,3 +282,33 @@ def test_backward_deterministic_writes_every_output_keeps_inputs(gpu, B, H, S, D
     for r in runs[1:]:
         assert all(torch.equal(a, b) for a, b in zip(runs[0], r))
     assert all(torch.equal(a, b) for a, b in zip(before, (Q, K, V, dO, M, Dl)))
+
+
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("S,D", [(1024, 64), (512, 128)])
+def test_running_max_moves_every_tile(gpu, S, D, causal):
+    """Scores that grow along the key axis (gpu_ref.rescale_stress_inputs): every
+    query's maximum sits at its last visible key and rises by more than the
+    forward's slack of 2^8 (8 in log2 units) from one 64-key tile to the next, so
+    the rescale of O and l runs at nearly every step.  O and LSE are checked
+    against the fp32 oracle.  The gradients cancel large terms (dS sums to zero
+    over keys whose axis-0 component reaches ~100-141), so they are held, element
+    by element, to the rounding budget of the reference's own bf16 rounding points
+    (gpu_ref.grad_rounding_budget; tests/test_oracle.py shows that the reference's
+    rounding stays inside it and that plausible mistakes do not)."""
+    from gpt_from_scratch_amd import flash_attn_forward
+    q, k, v, do = rescale_stress_inputs(S, D, gpu)
+    # the per-tile rise of the top score, in log2 units, exceeds the slack of 8
+    rise = 8.0 * float(k[0, 0, 64, 0] - k[0, 0, 0, 0]) / math.sqrt(D) / math.log(2)
+    assert rise > 8.0, rise
+    o, dq, dk, dv = _run(q, k, v, do, causal)
+    _, lse = flash_attn_forward(q, k, v, causal)
+    torch.cuda.synchronize()
+    ref = reference(q, k, v, do, causal, with_backward=False)
+    for name, got in (("o", o), ("lse", lse)):
+        assert_close_bf16(name, got, ref[name])
+    want, budget = grad_rounding_budget(q, k, v, do, o, causal)
+    for name, got in (("dq", dq), ("dk", dk), ("dv", dv)):
+        worst = budget_ratio(got, want[name], budget[name])
+        print(f"S{S} D{D} causal={causal} {name}: worst error {worst:.3f} of the budget")
+        assert worst <= 1.0, f"{name}: error reaches {worst:.3f} of the rounding budget"

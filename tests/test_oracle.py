@@ -415,3 +415,40 @@ def test_adamw_first_step_is_signed_lr_and_clip_scales_to_threshold():
     np.testing.assert_allclose(np.sqrt((gc ** 2).sum()), 1.0 * norm / (norm + 1e-6), rtol=1e-12)
     g2, _ = clip_gradient(grad * 1e-3, 1.0)
     np.testing.assert_array_equal(g2, grad * 1e-3)  # below the threshold: unchanged
+
+
+@pytest.mark.parametrize("causal", [True, False])
+def test_grad_rounding_budget_admits_reference_rounding_rejects_mistakes(causal):
+    """The gradient budget of the GPU rescale-stress test (gpu_ref.grad_rounding_budget)
+    is neither vacuous nor too tight: a CPU restatement that rounds where the
+    reference does (bf16 P before dV, bf16 scale*dS before dQ/dK, delta from the
+    bf16 O; core/myFlashAttn.py:1049, :1055, :1308) stays inside it, and four
+    plausible mistakes fall outside it."""
+    from gpu_ref import budget_ratio, grad_rounding_budget, rescale_stress_inputs
+    S, D = 256, 64
+    q, k, v, do = rescale_stress_inputs(S, D)
+    qf, kf, vf, dof = (t.float() for t in (q, k, v, do))
+    sc = 1.0 / math.sqrt(D)
+    mask = torch.ones(S, S, dtype=torch.bool).triu(1) if causal else torch.zeros(S, S, dtype=torch.bool)
+    p = torch.softmax(((qf @ kf.transpose(-1, -2)) * sc).masked_fill(mask, float("-inf")), -1)
+    o = (p @ vf).to(torch.bfloat16)
+    want, budget = grad_rounding_budget(q, k, v, do, o, causal)
+    bf = lambda t: t.to(torch.bfloat16).float()
+    dp = dof @ vf.transpose(-1, -2)
+    delta = (dof * o.float()).sum(-1, keepdim=True)
+    ds = bf(p * (dp - delta) * sc)
+    emul = {"dq": bf(ds @ kf), "dk": bf(ds.transpose(-1, -2) @ qf),
+            "dv": bf(bf(p).transpose(-1, -2) @ dof)}
+    for n in ("dq", "dk", "dv"):
+        assert budget_ratio(emul[n], want[n], budget[n]) <= 1.0, n
+    p_nomask = torch.softmax((qf @ kf.transpose(-1, -2)) * sc, -1)
+    mistakes = {
+        "dq without the delta term": ("dq", bf(bf(p * dp * sc) @ kf)),
+        "dq against keys shifted by one row": ("dq", bf(ds @ torch.roll(kf, 1, dims=-2))),
+        "dk without the softmax scale": ("dk", bf(bf(p * (dp - delta)).transpose(-1, -2) @ qf)),
+        "dv with the probabilities transposed": ("dv", bf(bf(p) @ dof)),
+    }
+    if causal:
+        mistakes["dv without the causal mask"] = ("dv", bf(bf(p_nomask).transpose(-1, -2) @ dof))
+    for what, (n, got) in mistakes.items():
+        assert budget_ratio(got, want[n], budget[n]) > 1.0, what
