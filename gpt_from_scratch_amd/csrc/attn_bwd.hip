@@ -151,10 +151,15 @@ struct BwdCfg {
 // LDS layout of a streamed tile: TILE rows of D elements, no padding; the
 // 16-byte chunk c of row r sits at chunk position c ^ swz(r), with
 //   swz(r) = 2*(r & 3) + ((r >> 2) & 1).
-// The tiles are read two ways and the swizzle suits both: 16-byte row reads
-// (eight consecutive rows, one chunk each: swz takes eight distinct values)
-// and transposing reads (16-lane groups over four consecutive rows and two
-// adjacent chunks: swz >> 1 takes four distinct values there).
+// The tiles are read two ways: 16-byte row reads (consecutive rows, one chunk
+// each: swz takes eight distinct values on eight rows) and transposing reads
+// (four consecutive rows and two adjacent chunks per 16 lanes: swz >> 1 takes
+// four distinct values there, and the operand's second read 8 rows on relies
+// on swz repeating every 8 rows).  The gfx950 LDS serves a 16-byte read for 16
+// lanes per cycle over 64 banks, so the row reads see a 2-way conflict between
+// rows r and r + 8; removing it needs a swizzle that differs between them, i.e.
+// a second offset for the transposing reads, in kernels at their register
+// limit.
 __device__ __forceinline__ int bwd_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
 struct BwdItem {
