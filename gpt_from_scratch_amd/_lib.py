@@ -144,8 +144,26 @@ def _stream(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
+def _check_attn_tensors(q, same, stats):
+    """Shapes and dtypes the attention kernels index by: every tensor of `same`
+    is [B, H, S, D] in q's dtype; every one of `stats` (lse, delta) is a dense
+    fp32 [B, H, S] (the kernels address it as (b*H + h)*S + s)."""
+    if q.dim() != 4:
+        raise ValueError(f"q must be [B, H, S, D]; got shape {tuple(q.shape)}")
+    B, H, S, _ = q.shape
+    for name, t in same:
+        if t.shape != q.shape or t.dtype != q.dtype:
+            raise ValueError(f"{name} must match q ({tuple(q.shape)}, {q.dtype}); got "
+                             f"{tuple(t.shape)}, {t.dtype}")
+    for name, t in stats:
+        if t.dtype != torch.float32 or t.shape != (B, H, S) or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous float32 [B, H, S] = [{B}, {H}, {S}] "
+                             f"tensor; got {t.dtype} {tuple(t.shape)} strides {t.stride()}")
+
+
 def attn_fwd(q, k, v, o, lse, causal: bool, scale: float):
     """Enqueue the forward on the current stream: writes o [B,H,S,D] and lse [B,H,S] fp32."""
+    _check_attn_tensors(q, (("k", k), ("v", v), ("o", o)), (("lse", lse),))
     _require_gpu(q, k, v, o, lse)
     B, H, S, D = q.shape
     st = lib().mi_attn_fwd(dtype_code(q), B, H, S, D, int(bool(causal)), float(scale),
@@ -157,6 +175,8 @@ def attn_fwd(q, k, v, o, lse, causal: bool, scale: float):
 
 def attn_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float):
     """Enqueue the backward on the current stream: writes delta, dq, dk, dv."""
+    _check_attn_tensors(q, (("k", k), ("v", v), ("o", o), ("do", do), ("dq", dq), ("dk", dk),
+                            ("dv", dv)), (("lse", lse), ("delta", delta)))
     _require_gpu(q, k, v, o, do, lse, delta, dq, dk, dv)
     B, H, S, D = q.shape
     st = lib().mi_attn_bwd(dtype_code(q), B, H, S, D, int(bool(causal)), float(scale),
@@ -207,6 +227,10 @@ def _rows(t: torch.Tensor):
         if t.shape[d] != 1 and t.stride(d) != expect:
             raise ValueError(f"leading dims of {tuple(t.shape)} / {t.stride()} are not one row axis")
         expect *= t.shape[d]
+    # rows that overlap (a broadcast row axis has stride 0) cannot be written
+    # row by row and are refused by the C ABI: callers copy such tensors first
+    if rows > 1 and rs < t.shape[-1]:
+        raise ValueError(f"rows of {tuple(t.shape)} / {t.stride()} overlap (row stride {rs})")
     return rows, rs
 
 

@@ -29,6 +29,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .rope import _check as _rope_check
 
 
 def _viewable(t: torch.Tensor, shape) -> torch.Tensor:
@@ -54,6 +55,8 @@ class AttentionBlock(torch.autograd.Function):
             raise AssertionError("HEAD_DIM must be even")
         qkv5 = _viewable(qkv, (S, B, 3, heads, D))
         q, k, v = qkv5.unbind(2)
+        # the C ABI takes no table length: short or mis-shaped tables are refused here
+        _rope_check(q, cos, sin)
         rot = torch.empty((S, B, 2, heads, D), dtype=qkv.dtype, device=qkv.device)
         _lib.rope_qk(q, k, cos, sin, rot[:, :, 0], rot[:, :, 1], inverse=False)
         o = torch.empty((S, B, heads, D), dtype=qkv.dtype, device=qkv.device)

@@ -225,8 +225,8 @@ __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& 
   const int w0 = it.tile * BwdCfg<D>::OWN + 32 * wave;  // first row of this wave (SGPR)
   if (w0 < a.S) {
     // wave base in the descriptor, lane offset (row l%32, 8 columns) in one VGPR
-    const auto r0 = tile_rsrc(head_ptr(t0, b, h) + (int64_t)w0 * t0.ss);
-    const auto r1 = tile_rsrc(head_ptr(t1, b, h) + (int64_t)w0 * t1.ss);
+    const auto r0 = tile_rsrc(head_ptr(t0, b, h) + (int64_t)w0 * t0.ss, rows_extent(32, t0.ss, D));
+    const auto r1 = tile_rsrc(head_ptr(t1, b, h) + (int64_t)w0 * t1.ss, rows_extent(32, t1.ss, D));
     const uint32_t o0 = (uint32_t)(((lane & 31) * t0.ss + 8 * (lane >> 5)) * 2);
     const uint32_t o1 = (uint32_t)(((lane & 31) * t1.ss + 8 * (lane >> 5)) * 2);
     // kind 0 keeps V negated (sign bits of both 16-bit halves flipped)
@@ -239,9 +239,9 @@ __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& 
     if (it.kind) {
       const int64_t o = (int64_t)it.bh * a.S + w0;
       res.lse2 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                     tile_rsrc(a.lse + o), (lane & 31) * 4, 0, 0)) * kLog2e;
+                     tile_rsrc(a.lse + o, 32 * 4), (lane & 31) * 4, 0, 0)) * kLog2e;
       res.dl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                   tile_rsrc(a.delta + o), (lane & 31) * 4, 0, 0));
+                   tile_rsrc(a.delta + o, 32 * 4), (lane & 31) * 4, 0, 0));
     }
   } else {
 #pragma unroll
@@ -291,8 +291,8 @@ __device__ __forceinline__ void dma_stage(const StageSrc<D>& s, int kind, int ro
   using C = BwdCfg<D>;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const auto r0 = tile_rsrc(s.p0 + (int64_t)row0 * s.ss0);
-  const auto r1 = tile_rsrc(s.p1 + (int64_t)row0 * s.ss1);
+  const auto r0 = tile_rsrc(s.p0 + (int64_t)row0 * s.ss0, rows_extent(C::TILE, s.ss0, D));
+  const auto r1 = tile_rsrc(s.p1 + (int64_t)row0 * s.ss1, rows_extent(C::TILE, s.ss1, D));
 #pragma unroll
   for (int m = 0; m < C::SPW; ++m) {
     buffer_load_lds16(r0, s.off0[m], dst.t0 + (wave + 4 * m) * 512);
@@ -301,7 +301,7 @@ __device__ __forceinline__ void dma_stage(const StageSrc<D>& s, int kind, int ro
   if (kind == 0 && wave >= 2 && lane < C::TILE) {
     // waves 2 and 3: lse and delta of the tile's query rows (4 bytes per lane)
     const float* src = (wave == 2 ? s.lse : s.delta) + row0;
-    buffer_load_lds4(tile_rsrc(src), lane * 4, dst.sl + (wave - 2) * C::TILE);
+    buffer_load_lds4(tile_rsrc(src, C::TILE * 4), lane * 4, dst.sl + (wave - 2) * C::TILE);
   }
 }
 

@@ -36,6 +36,7 @@
 //     head is B*H).  Workgroups w and w + #CU share a CU, so every odd round
 //     of #CU workgroups is taken in reverse (XCD kept): a CU's co-resident
 //     tiles pair heavy with light.
+#include <atomic>
 #include <type_traits>
 
 #include "mi_device.h"
@@ -153,7 +154,7 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
   }
   auto dma = [&](const uint16_t* base, int64_t ss, const uint32_t(&off)[C::SPW], int t,
                  uint16_t* tile) __attribute__((always_inline)) {
-    const auto rs = tile_rsrc(base + (int64_t)t * C::BKV * ss);
+    const auto rs = tile_rsrc(base + (int64_t)t * C::BKV * ss, rows_extent(C::BKV, ss, D));
 #pragma unroll
     for (int m = 0; m < C::SPW; ++m)
       buffer_load_lds16(rs, off[m], tile + (wave + 4 * m) * 512);
@@ -297,24 +298,30 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
   if (g == 0) a.lse[(int64_t)bh * S + qrow] = (m_run + fast_log2(l_tot)) * kLn2;
 }
 
-// Compute units of the current device (cached), the size of one dispatch
-// round of the grid ordering; 0 when unknown or not a multiple of the 8 XCDs.
-int cu_count() {
-  static int cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
-  if (cache[dev] == 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
-    cache[dev] = (n > 0 && n % 8 == 0) ? n : -1;
+// Compute units of the device `st` launches on (cached per device), the size
+// of one dispatch round of the grid ordering; 0 when unknown or not a multiple
+// of the 8 XCDs.  Calls may come from several host threads at once (the
+// forward from the caller's, the backward from autograd's): the cache entries
+// are atomics, and a race only makes two threads store the same value.
+int cu_count(hipStream_t st) {
+  static std::atomic<int> cache[64];
+  int dev = -1;
+  if (hipStreamGetDevice(st, &dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = cache[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      cus = 0;
+    n = (cus > 0 && cus % 8 == 0) ? cus : -1;
+    cache[dev].store(n, std::memory_order_relaxed);
   }
-  return cache[dev] > 0 ? cache[dev] : 0;
+  return n > 0 ? n : 0;
 }
 
 template <typename E, int D>
 hipError_t launch_fwd_d(const AttnArgs& a, hipStream_t st) {
   const int n_qtiles = (a.S + FwdCfg<D>::BQ - 1) / FwdCfg<D>::BQ;
-  int n_cu = cu_count();
+  int n_cu = cu_count(st);
   if (n_cu == 0) n_cu = 1 << 30;  // one round: no reversal
   dim3 grid(n_qtiles * a.B * a.H), block(FwdCfg<D>::NT);
   if (a.causal)

@@ -3,8 +3,9 @@
 // Validates every argument before anything is enqueued, picks the kernel
 // family (bf16/f16 MFMA when the shape and alignment allow it, exact-fp32
 // VALU otherwise) and reports failures as status codes plus a per-thread
-// message.  No allocation, no synchronisation, no global mutable state apart
-// from the thread-local error text.
+// message.  No allocation and no synchronisation.  Global mutable state: the
+// thread-local error text, and the forward's per-device cache of the compute
+// unit count (atomic entries, written once per device with the same value).
 #include <cmath>
 #include <initializer_list>
 #include <utility>

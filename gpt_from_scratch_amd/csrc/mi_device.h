@@ -145,13 +145,20 @@ __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_lo
 
 // ---------------------------------------------------------------------------
 // Buffer resource for raw buffer loads based at `p` (wave-uniform pointer, so
-// the descriptor lives in SGPRs and per-tile rebasing is scalar arithmetic).
-// Word 3 = 0x00020000: 32-bit data format, no swizzle, no stride (gfx9 family).
-// The range is left open: callers only address rows that exist.
+// the descriptor lives in SGPRs and per-tile rebasing is scalar arithmetic),
+// covering `bytes` bytes from p: a load at or past that extent returns zeros
+// (and a direct-to-LDS load writes zeros) instead of reading whatever memory
+// follows.  Word 3 = 0x00020000: 32-bit data format, no swizzle, no stride
+// (gfx9 family).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* p) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 0x7fffffff,
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* p, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes,
                                            0x00020000);
+}
+
+// Bytes spanned by `rows` rows of `cols` 16-bit elements, `ss` elements apart.
+__device__ __forceinline__ uint32_t rows_extent(int rows, int64_t ss, int cols) {
+  return (uint32_t)(((int64_t)(rows - 1) * ss + cols) * 2);
 }
 
 // ---------------------------------------------------------------------------

@@ -47,6 +47,9 @@ struct MaxSum {
   __device__ __forceinline__ void add_group(const float* x, int n) {
     float mx = x[0];
     for (int e = 1; e < n; ++e) mx = fmaxf(mx, x[e]);
+    // an all -inf group adds exp(-inf) = 0; skipping it also keeps the first
+    // group's x - m away from -inf - (-inf) = NaN
+    if (mx == -INFINITY) return;
     if (mx > m) {
       s *= fast_exp2((m - mx) * kLog2e);  // exp(-inf) = 0 on the first group
       m = mx;

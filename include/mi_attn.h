@@ -156,6 +156,11 @@ mi_status mi_attn_bwd_dq(mi_dtype dtype, int B, int H, int S, int D, int causal,
  *   forward (inverse = 0): (e, o) -> (e*c - o*s, e*s + o*c)
  *   inverse (inverse = 1): (e, o) -> (e*c + o*s, o*c - e*s)   (rotation by -theta)
  * with c = cos[s, i], s = sin[s, i].  x_dtype and tab_dtype are independent.
+ * The tables must hold at least S rows of D/2 angles (their extent is not
+ * passed, so it is the caller's to check).
+ * In place: `out` may be `x` itself with the same strides (every element is
+ * read and then written by the same lane); any other overlap of out with x is
+ * undefined.
  * Replaces `_rope_kernel` launches in TritonRoPE.forward / .backward,
  * core/rope_triton.py:10-72 (launch :33-40 and :63-70, kernel :74-141).
  */
@@ -169,7 +174,9 @@ mi_status mi_rope(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, int
 
 /*
  * The same rotation applied to q and k (same shape, dtype and tables) in one
- * launch.  Replaces the two TritonRoPE.apply calls of apply_rope_qk,
+ * launch.  In place as for mi_rope: q_out may be q and k_out may be k (same
+ * pointers and strides); the outputs must not otherwise overlap either input.
+ * Replaces the two TritonRoPE.apply calls of apply_rope_qk,
  * core/rope_triton.py:147-148, and their two backward launches.
  */
 mi_status mi_rope_qk(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, int D,

@@ -105,6 +105,24 @@ def test_python_api_shape_errors():
         apply_rope(torch.randn(4, 1, 1, 7), torch.ones(4, 3), torch.ones(4, 3))
 
 
+def test_attention_stats_and_gradient_checks():
+    """lse/delta must be dense fp32 [B, H, S] and dO must match q: checked before
+    any launch (the kernels index them as (b*H + h)*S + s)."""
+    import torch
+    from gpt_from_scratch_amd import flash_attn_backward
+    q = torch.randn(1, 2, 8, 16)
+    m = torch.zeros(1, 2, 8)
+    for bad_m in (m.double(), torch.zeros(1, 2, 16)[:, :, ::2], torch.zeros(2, 1, 8)):
+        with pytest.raises(ValueError, match="lse"):
+            flash_attn_backward(q, q, q, q, bad_m, q)
+    with pytest.raises(ValueError, match="do"):
+        flash_attn_backward(q, q, q, q, m, torch.randn(1, 2, 8, 8))
+    with pytest.raises(ValueError, match="do"):
+        flash_attn_backward(q, q, q, q, m, q.double())
+    with pytest.raises(RuntimeError, match="ROCm GPUs only"):
+        flash_attn_backward(q, q, q, q, m, q)
+
+
 def test_attention_block_shape_errors():
     """The fused block checks its [S, B, 3*H*D] input before any launch."""
     import torch
@@ -116,6 +134,13 @@ def test_attention_block_shape_errors():
         attention_block(torch.randn(8, 30), cos, sin, 2)
     with pytest.raises(AssertionError, match="even"):
         attention_block(torch.randn(8, 2, 18), cos, sin, 2)
+    # tables shorter than the sequence, narrower than D/2, or not 2-D
+    qkv = torch.randn(8, 2, 24)
+    for c in (torch.ones(7, 2), torch.ones(8, 1), torch.ones(8), torch.ones(1, 8, 2)):
+        with pytest.raises(ValueError, match="cos"):
+            attention_block(qkv, c, torch.ones(8, 2), 2)
+    with pytest.raises(ValueError, match="sin"):
+        attention_block(qkv, torch.ones(8, 2), torch.ones(4, 2), 2)
 
 
 def test_rotary_embedding_tables_cpu():
@@ -206,3 +231,27 @@ def test_model_op_python_checks():
         rms_norm(torch.randn(4, 8), torch.ones(8))
     with pytest.raises(RuntimeError, match="ROCm GPUs only"):
         DistributedOptimizer(torch.nn.Linear(4, 3), torch.optim.AdamW, {"lr": 1e-2})
+
+
+def test_rows_view_of_model_op_tensors():
+    """The row view the model-operator bindings hand to the C ABI: leading dims
+    collapse into one row axis; overlapping rows (a broadcast row axis, stride
+    0) and non-collapsible strides raise ValueError, which the modules answer
+    with a contiguous copy."""
+    import torch
+    from gpt_from_scratch_amd import _lib
+    x = torch.zeros(6, 4, 10)
+    assert _lib._rows(x) == (24, 10)
+    assert _lib._rows(torch.zeros(7, 10)[:, :5]) == (7, 10)
+    assert _lib._rows(torch.zeros(10)) == (1, 10)
+    assert _lib._rows(torch.zeros(10).expand(1, 10))[0] == 1  # one row: its stride is unused
+    for bad in (torch.zeros(10).expand(5, 10), torch.zeros(3, 1, 10).expand(3, 4, 10),
+                torch.zeros(4, 6, 10).transpose(0, 1)):
+        with pytest.raises(ValueError):
+            _lib._rows(bad)
+    from gpt_from_scratch_amd.mlp import _rows_view as mlp_rows
+    from gpt_from_scratch_amd.normalization import _rows_view as norm_rows
+    b = torch.arange(10.).expand(5, 10)
+    for f in (mlp_rows, norm_rows):
+        c = f(b)
+        assert c.is_contiguous() and torch.equal(c, b)

@@ -1,7 +1,11 @@
-"""The fused attention block (qkv projection layout in, [S, B, H*D] out) against
-the unfused composition in the reference's block order (core/transformer_layer.py:
-42-61): RoPE on q/k, permute, flash attention, permute back and reshape.  Same
-kernels, same arithmetic: forward output and qkv gradient must match bit for bit."""
+"""The fused attention block (qkv projection layout in, [S, B, H*D] out):
+
+* against the unfused composition in the reference's block order
+  (core/transformer_layer.py:42-61): RoPE on q/k, permute, flash attention,
+  permute back and reshape.  Same kernels, same arithmetic: forward output and
+  qkv gradient must match bit for bit;
+* against the oracle's float32 autograd of that chain on the CPU, at config 2's
+  shape and at D = 128, within the bf16 bounds."""
 import pytest
 import torch
 
@@ -34,3 +38,72 @@ def test_block_matches_composition(gpu, S, B, H, D, causal):
     assert o1.shape == (S, B, H * D)
     assert torch.equal(o1, o2)
     assert torch.equal(x1.grad, x2.grad)
+
+
+def _oracle_block(qkv, cos, sin, H, g, causal):
+    """The reference block's maths on the CPU in float32 with autograd
+    (core/transformer_layer.py:42-61): view [S, B, 3, H, D], RoPE on q and k
+    with the model's tables (core/rope_triton.py:112-133), permute to
+    [B, H, S, D], softmax(Q K^T / sqrt(D) + mask) V (core/myFlashAttn.py:9-23),
+    permute and reshape to [S, B, H*D]; backward through all of it.  The
+    tensors that cross between the reference's two kernels are in the
+    activation dtype there, and are rounded to it here: the rotated q, k
+    (``empty_like(x)``, rope_triton.py:22) and the attention gradients dQ, dK
+    that the inverse rotation receives (myFlashAttn.py:349-351)."""
+    from oracle import attention_forward, rope_apply
+    S, B, _ = qkv.shape
+    D = qkv.shape[-1] // (3 * H)
+    x = qkv.detach().cpu().float().requires_grad_()
+    q, k, v = x.view(S, B, 3, H, D).unbind(2)
+    c, s = cos.cpu().float(), sin.cpu().float()
+    dt = qkv.dtype
+
+    class Round(torch.autograd.Function):
+        """Rounds to the activation dtype in forward and in backward."""
+        @staticmethod
+        def forward(ctx, t):
+            return t.to(dt).float()
+
+        @staticmethod
+        def backward(ctx, gt):
+            return gt.to(dt).float()
+
+    rnd = Round.apply
+    qr = rnd(rope_apply(q, c, s, dtype=torch.float32)).permute(1, 2, 0, 3)
+    kr = rnd(rope_apply(k, c, s, dtype=torch.float32)).permute(1, 2, 0, 3)
+    o, _ = attention_forward(qr, kr, v.permute(1, 2, 0, 3), causal, dtype=torch.float32)
+    o = o.permute(2, 0, 1, 3).reshape(S, B, H * D)
+    o.backward(g.detach().cpu().float())
+    return o.detach(), x.grad
+
+
+@pytest.mark.parametrize("S,B,H,D,std", [(1024, 8, 12, 64, 1.0), (2048, 1, 4, 128, 0.5)])
+def test_block_against_oracle(gpu, S, B, H, D, std):
+    """The fused block (RoPE into a [S, B, 2, H, D] buffer, attention on strided
+    views, O stored as [S, B, H*D], dQ/dK/dV into one [S, B, 3, H, D] gradient
+    with the inverse rotation in place) against the oracle's autograd of the
+    unfused reference chain: config 2's shape and a D = 128 shape.  Output and
+    each slot of the qkv gradient (the q and k slots carry the in-place inverse
+    rotation) within the bf16 bounds (max-abs 2e-2, mean-rel 1e-2); the q and k
+    slots are rounded once more than an attention gradient (the inverse
+    rotation's output), so their elements may also move by that rounding,
+    2^-8 |ref|."""
+    from gpt_from_scratch_amd import RotaryEmbedding, attention_block
+    from gpu_ref import assert_close_bf16
+    qkv = seeded((S, B, 3 * H * D), 190 + D, std).to(gpu)
+    cos, sin = RotaryEmbedding(D, S, device=gpu)(qkv, seq_len=S)
+    g = seeded((S, B, H * D), 191 + D).to(gpu)
+    x = qkv.clone().requires_grad_()
+    o = attention_block(x, cos, sin, H, True)
+    o.backward(g)
+    torch.cuda.synchronize()
+    ro, rgrad = _oracle_block(qkv, cos, sin, H, g, True)
+    assert_close_bf16("o", o.detach().cpu(), ro)
+    got = x.grad.cpu().view(S, B, 3, H, D)
+    want = rgrad.view(S, B, 3, H, D)
+    assert_close_bf16("dv", got[:, :, 2], want[:, :, 2])
+    for i, name in ((0, "dq"), (1, "dk")):
+        err = (got[:, :, i].float() - want[:, :, i]).abs()
+        bound = 2e-2 + 2.0 ** -8 * want[:, :, i].abs()
+        assert bool((err <= bound).all()), (name, float(err.max()), float((err - bound).max()))
+        assert float(err.mean() / want[:, :, i].abs().mean()) <= 1e-2, name

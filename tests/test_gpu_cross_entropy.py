@@ -123,3 +123,32 @@ def test_large_logits_are_stable(gpu):
     ref_grad = cross_entropy_backward(z.double().numpy(), t.numpy(), dl.double().numpy())
     _check("loss", loss, ref_loss, torch.bfloat16, 4e-6)
     np.testing.assert_allclose(grad.float().cpu().numpy(), ref_grad, atol=2.0 ** -8)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_minus_inf_logits(gpu, dtype):
+    """-inf logits (masked vocabulary slots) in a row's scalar head, vector body
+    and scalar tail: they contribute exp(-inf) = 0, the loss and the gradient
+    stay finite and match the oracle.  Rows start at odd 2-byte offsets (a
+    [S, B, V] slice), so every row has a head and a tail; one row has -inf as the
+    first element a thread sees."""
+    rows, V = 6, 1003
+    base = seeded((rows, V + 5), 701, std=2.0, dtype=dtype)
+    z = base[:, 3:3 + V].clone()
+    ninf = float("-inf")
+    z[0, 0] = ninf          # first element of the row (scalar head)
+    z[1, V - 1] = ninf      # last element (scalar tail)
+    z[2, 500:520] = ninf    # inside the vector body
+    z[3, :8] = ninf         # several head elements
+    z[4, ::7] = ninf        # spread over every part
+    buf = torch.zeros(rows, V + 5, dtype=dtype)
+    buf[:, 3:3 + V] = z
+    t = torch.tensor([5, 6, 7, 9, 10, 11])
+    dl = seeded((rows,), 702, dtype=dtype)
+    zg = buf.to(gpu)[:, 3:3 + V]
+    loss, grad = _run(zg, t.to(gpu), dl.to(gpu))
+    assert torch.isfinite(loss).all() and torch.isfinite(grad).all()
+    ref_loss, _ = cross_entropy_forward(z.double().numpy(), t.numpy())
+    ref_grad = cross_entropy_backward(z.double().numpy(), t.numpy(), dl.double().numpy())
+    _check("loss", loss, ref_loss, dtype, 4e-6)
+    _check("grad", grad, ref_grad, dtype, 4e-6 * np.abs(dl.double().numpy())[:, None])

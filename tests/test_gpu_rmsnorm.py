@@ -161,3 +161,22 @@ def test_backward_with_several_rows_per_wave(gpu):
     y, dx, dw = _run(x.to(gpu), w.to(gpu), dy.to(gpu))
     _check_forward(y, x, w, EPS)
     _check_backward(dx, dw, x, w, dy, EPS)
+
+
+def test_row_broadcast_gradient(gpu):
+    """A valid autograd gradient whose row axis has stride 0 (the gradient of
+    (y.sum(0) * c).sum() is one row broadcast over all rows): the module copies
+    it before the kernels instead of handing overlapping rows to the C ABI."""
+    rows, H = 17, 768
+    x = seeded((rows, H), 501, std=1.5, dtype=torch.bfloat16).to(gpu)
+    w = (1.0 + 0.1 * seeded((H,), 502, dtype=torch.float32)).to(torch.bfloat16).to(gpu)
+    c = seeded((H,), 503, dtype=torch.bfloat16).to(gpu)
+    from gpt_from_scratch_amd import rms_norm
+    xg = x.clone().requires_grad_(True)
+    wg = w.clone().requires_grad_(True)
+    (rms_norm(xg, wg, EPS).sum(0) * c).sum().backward()
+    dy = c.expand(rows, H)
+    _check_backward(xg.grad, wg.grad, x, w, dy, EPS)
+    # the same broadcast tensor as a forward input
+    y = rms_norm(x[:1].expand(rows, H), w, EPS)
+    _check_forward(y, x[:1].expand(rows, H).contiguous(), w, EPS)

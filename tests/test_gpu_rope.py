@@ -142,3 +142,28 @@ def test_long_sequence_invariants(gpu):
     back = torch.empty_like(y)
     _lib.rope(y, cos, sin, back, inverse=True)
     assert float((back - x).abs().max()) < 1e-5
+
+
+@pytest.mark.parametrize("dtype,D", [(torch.bfloat16, 64), (torch.float32, 64),
+                                     (torch.bfloat16, 6)])
+def test_in_place(gpu, dtype, D):
+    """out == x (same pointer and strides) is allowed: the result equals the
+    out-of-place rotation bit for bit, for mi_rope and for mi_rope_qk, on the
+    vector path (D = 64) and the scalar pair path (D = 6)."""
+    from gpt_from_scratch_amd import _lib
+    S, B, H = 200, 2, 3
+    qkv = seeded((S, B, 3, H, D), 33 + D, dtype=dtype).to(gpu)
+    cos, sin = (t.to(dtype).to(gpu) for t in rope_tables(D, S))
+    q, k, _ = qkv.unbind(2)
+    for inverse in (False, True):
+        want_q, want_k = torch.empty_like(q), torch.empty_like(k)
+        _lib.rope_qk(q, k, cos, sin, want_q, want_k, inverse)
+        x = qkv.clone()
+        xq, xk, _ = x.unbind(2)
+        _lib.rope_qk(xq, xk, cos, sin, xq, xk, inverse)
+        assert torch.equal(xq, want_q) and torch.equal(xk, want_k)
+        y = qkv.clone()
+        yq = y[:, :, 0]
+        _lib.rope(yq, cos, sin, yq, inverse)
+        assert torch.equal(yq, want_q)
+        assert torch.equal(y[:, :, 1:], qkv[:, :, 1:])  # nothing else touched

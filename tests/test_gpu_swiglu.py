@@ -116,3 +116,19 @@ def test_more_rows_than_one_grid_column(gpu):
     _close("d_gate", dgu[:, :16], ref_d[:, :16], torch.bfloat16, 1,
            _dgate_floor(_np(gu), _np(dh), torch.bfloat16))
     _close("d_up", dgu[:, 16:], ref_d[:, 16:], torch.bfloat16, 3)
+
+
+def test_row_broadcast_gradient(gpu):
+    """dh with a stride-0 row axis (the gradient of (h.sum(0) * c).sum()): copied
+    before the kernel, not refused by the C ABI."""
+    rows, inter = 9, 3072
+    gu = seeded((rows, 2 * inter), 601, std=2.0, dtype=torch.bfloat16)
+    c = seeded((inter,), 602, dtype=torch.bfloat16)
+    from gpt_from_scratch_amd import swiglu
+    x = gu.to(gpu).requires_grad_(True)
+    (swiglu(x).sum(0) * c.to(gpu)).sum().backward()
+    dh = c.expand(rows, inter)
+    ref_d = swiglu_backward(_np(gu), _np(dh), torch.bfloat16)
+    _close("d_gate", x.grad[:, :inter], ref_d[:, :inter], torch.bfloat16, 1,
+           _dgate_floor(_np(gu), _np(dh), torch.bfloat16))
+    _close("d_up", x.grad[:, inter:], ref_d[:, inter:], torch.bfloat16, 3)
