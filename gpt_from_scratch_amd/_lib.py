@@ -26,7 +26,10 @@ EXPORTED = ("mi_version", "mi_status_str", "mi_last_error", "mi_attn_fwd", "mi_a
             "mi_attn_bwd_preprocess", "mi_attn_bwd_grads", "mi_attn_bwd_dkdv", "mi_attn_bwd_dq",
             "mi_rope", "mi_rope_qk", "mi_xent_fwd", "mi_xent_bwd", "mi_rmsnorm_fwd",
             "mi_rmsnorm_bwd_workspace", "mi_rmsnorm_bwd", "mi_swiglu_fwd", "mi_swiglu_bwd",
-            "mi_adamw_workspace", "mi_grad_sumsq", "mi_adamw_step")
+            "mi_adamw_workspace", "mi_grad_sumsq", "mi_adamw_step", "mi_attn_bwd_noalloc")
+
+# B*H*S limit of mi_attn_bwd_noalloc (its static delta array), include/mi_attn.h
+NOALLOC_MAX_ROWS = 1 << 20
 
 _lib = None
 
@@ -53,6 +56,10 @@ def _declare(lib):
     lib.mi_attn_bwd.argtypes = [i, i, i, i, i, i, f,
                                 p, i64p, p, i64p, p, i64p, p, i64p, p, i64p,
                                 p, p, p, i64p, p, i64p, p, i64p, p]
+    lib.mi_attn_bwd_noalloc.restype = i
+    lib.mi_attn_bwd_noalloc.argtypes = [i, i, i, i, i, i, f,
+                                        p, i64p, p, i64p, p, i64p, p, i64p, p, i64p,
+                                        p, p, i64p, p, i64p, p, i64p, p]
     lib.mi_attn_bwd_preprocess.restype = i
     lib.mi_attn_bwd_preprocess.argtypes = [i, i, i, i, i, p, i64p, p, i64p, p, p]
     lib.mi_attn_bwd_grads.restype = i
@@ -186,6 +193,21 @@ def attn_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float)
                            _ptr(dq), _strides(dq, 4), _ptr(dk), _strides(dk, 4),
                            _ptr(dv), _strides(dv, 4), _stream(q))
     _check(st, "mi_attn_bwd")
+
+
+def attn_bwd_noalloc(q, k, v, o, do, lse, dq, dk, dv, causal: bool, scale: float):
+    """mi_attn_bwd without a delta workspace (the library's static array): writes dq, dk, dv."""
+    _check_attn_tensors(q, (("k", k), ("v", v), ("o", o), ("do", do), ("dq", dq), ("dk", dk),
+                            ("dv", dv)), (("lse", lse),))
+    _require_gpu(q, k, v, o, do, lse, dq, dk, dv)
+    B, H, S, D = q.shape
+    st = lib().mi_attn_bwd_noalloc(dtype_code(q), B, H, S, D, int(bool(causal)), float(scale),
+                                   _ptr(q), _strides(q, 4), _ptr(k), _strides(k, 4),
+                                   _ptr(v), _strides(v, 4), _ptr(o), _strides(o, 4),
+                                   _ptr(do), _strides(do, 4), _ptr(lse),
+                                   _ptr(dq), _strides(dq, 4), _ptr(dk), _strides(dk, 4),
+                                   _ptr(dv), _strides(dv, 4), _stream(q))
+    _check(st, "mi_attn_bwd_noalloc")
 
 
 def rope(x, cos, sin, out, inverse: bool):

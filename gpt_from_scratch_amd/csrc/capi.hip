@@ -6,6 +6,7 @@
 // message.  No allocation and no synchronisation.  Global mutable state: the
 // thread-local error text, and the forward's per-device cache of the compute
 // unit count (atomic entries, written once per device with the same value).
+#include <atomic>
 #include <cmath>
 #include <initializer_list>
 #include <utility>
@@ -666,3 +667,70 @@ mi_status mi_adamw_step(mi_dtype grad_dtype, mi_dtype param_dtype, int64_t n, co
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------------------
+// mi_attn_bwd_noalloc: the delta workspace of mi_attn_bwd taken from a static
+// device array instead of the caller.  `scratch` names a host-side stand-in
+// for the array in host code, so host code only ever uses the per-device
+// address that hipGetSymbolAddress returns (kept in g_scratch).
+// ---------------------------------------------------------------------------
+namespace {
+
+__device__ __attribute__((aligned(256))) float scratch[MI_ATTN_NOALLOC_MAX_ROWS];
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+
+// Device address of `scratch` on the device `stream` belongs to, looked up
+// once per device with that device current (threads that race here store the
+// same address).
+mi_status scratch_on(void* stream, float** out) {
+  int dev = -1;
+  hipError_t e = hipStreamGetDevice((hipStream_t)stream, &dev);
+  if (e != hipSuccess) return fail(MI_ERR_LAUNCH, "hipStreamGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(MI_ERR_UNSUPPORTED, "device %d: at most %d devices", dev, kMaxDevices);
+  float* p = g_scratch[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    int cur = -1;
+    if ((e = hipGetDevice(&cur)) != hipSuccess)
+      return fail(MI_ERR_LAUNCH, "hipGetDevice: %s", hipGetErrorString(e));
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess)
+      return fail(MI_ERR_LAUNCH, "hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+    void* addr = nullptr;
+    const hipError_t es = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (cur != dev && (e = hipSetDevice(cur)) != hipSuccess)
+      return fail(MI_ERR_LAUNCH, "hipSetDevice(%d): %s", cur, hipGetErrorString(e));
+    if (es != hipSuccess || addr == nullptr)
+      return fail(MI_ERR_LAUNCH, "hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                  hipGetErrorString(es));
+    p = (float*)addr;
+    g_scratch[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return MI_OK;
+}
+
+}  // namespace
+
+extern "C" mi_status mi_attn_bwd_noalloc(
+    mi_dtype dtype, int B, int H, int S, int D, int causal, float scale, const void* q,
+    const int64_t q_strides[4], const void* k, const int64_t k_strides[4], const void* v,
+    const int64_t v_strides[4], const void* o, const int64_t o_strides[4], const void* dout,
+    const int64_t dout_strides[4], const float* lse, void* dq, const int64_t dq_strides[4],
+    void* dk, const int64_t dk_strides[4], void* dv, const int64_t dv_strides[4], void* stream) {
+  mi_status st;
+  if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
+  const int64_t rows = (int64_t)B * H * S;
+  if (rows > MI_ATTN_NOALLOC_MAX_ROWS)
+    return fail(MI_ERR_INVALID_ARGUMENT,
+                "B*H*S = %lld exceeds MI_ATTN_NOALLOC_MAX_ROWS = %d (the static delta array)",
+                (long long)rows, MI_ATTN_NOALLOC_MAX_ROWS);
+  float* delta = nullptr;
+  if ((st = scratch_on(stream, &delta)) != MI_OK) return st;
+  // mi_attn_bwd validates every other argument before it enqueues anything;
+  // the preprocess overwrites delta[0, rows) before the gradient launch reads it.
+  return mi_attn_bwd(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v, v_strides,
+                     o, o_strides, dout, dout_strides, lse, delta, dq, dq_strides, dk, dk_strides,
+                     dv, dv_strides, stream);
+}

@@ -303,6 +303,34 @@ mi_status mi_adamw_step(mi_dtype grad_dtype, mi_dtype param_dtype, int64_t n, co
                         float one_minus_beta2, float step_size, float bias_correction2_sqrt,
                         float eps, float clip, const float* grad_sumsq, void* stream);
 
+/*
+ * mi_attn_bwd without the delta workspace argument, for callers that cannot
+ * allocate device memory: code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc.  It has no counterpart in the reference
+ * (whose backward allocates D itself, core/myFlashAttn.py:323).
+ * delta lives in a library-owned static device array of
+ * MI_ATTN_NOALLOC_MAX_ROWS floats (4 MiB) on each GPU the library runs on,
+ * held until the process ends; its address is looked up once per device on
+ * the first call there.  B*H*S must not exceed MI_ATTN_NOALLOC_MAX_ROWS
+ * (MI_ERR_INVALID_ARGUMENT otherwise, before anything is enqueued).  The call
+ * allocates nothing.  Every call on one GPU shares that array: calls that
+ * overlap on one GPU (other streams, other threads) race and must be
+ * serialised by the caller.  Results are those of mi_attn_bwd (same kernels).
+ */
+#define MI_ATTN_NOALLOC_MAX_ROWS (1 << 20)
+mi_status mi_attn_bwd_noalloc(mi_dtype dtype, int B, int H, int S, int D, int causal,
+                              float scale,
+                              const void* q, const int64_t q_strides[4],
+                              const void* k, const int64_t k_strides[4],
+                              const void* v, const int64_t v_strides[4],
+                              const void* o, const int64_t o_strides[4],
+                              const void* dout, const int64_t dout_strides[4],
+                              const float* lse,
+                              void* dq, const int64_t dq_strides[4],
+                              void* dk, const int64_t dk_strides[4],
+                              void* dv, const int64_t dv_strides[4],
+                              void* stream);
+
 #ifdef __cplusplus
 }
 #endif
