@@ -288,7 +288,7 @@ def attn_config_bench(dev, lib, B, H, S, D, seed, std, steps):
     Q, K, V = qr.permute(1, 2, 0, 3), kr.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3)
     O = torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev)
     LSE = torch.empty(B, H, S, dtype=torch.float32, device=dev)
-    DELTA = torch.empty_like(LSE)
+    DELTA = torch.empty((2,) + tuple(LSE.shape), dtype=torch.float32, device=dev)  # workspace
     dQ, dK, dV = (torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev) for _ in range(3))
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
@@ -297,7 +297,7 @@ def attn_config_bench(dev, lib, B, H, S, D, seed, std, steps):
     hdr = (_lib.dtype_code(Q), B, H, S, D)
     scale = 1.0 / math.sqrt(D)
     fwd = hdr + (1, scale, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(O), ST(O), P(LSE), sp)
-    pre = hdr + (P(O), ST(O), P(do), ST(do), P(DELTA), sp)
+    pre = hdr + (P(O), ST(O), P(do), ST(do), P(LSE), P(DELTA), sp)
     grads = hdr + (1, scale, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(do), ST(do), P(LSE),
                    P(DELTA), P(dQ), ST(dQ), P(dK), ST(dK), P(dV), ST(dV), sp)
     calls = [("attn_fwd", lib.mi_attn_fwd, fwd), ("attn_bwd_preprocess", lib.mi_attn_bwd_preprocess, pre),
@@ -428,7 +428,7 @@ def main():
     Q, K, V = qr.permute(1, 2, 0, 3), kr.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3)
     O = torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev)
     LSE = torch.empty(B, H, S, dtype=torch.float32, device=dev)
-    DELTA = torch.empty_like(LSE)
+    DELTA = torch.empty((2,) + tuple(LSE.shape), dtype=torch.float32, device=dev)  # workspace
     dQ, dK, dV = (torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev) for _ in range(3))
 
     lib = _lib.lib()
@@ -439,7 +439,7 @@ def main():
     dt = _lib.dtype_code(Q)
     hdr = (dt, B, H, S, D)
     fwd_args = hdr + (1, scale, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(O), ST(O), P(LSE), sp)
-    pre_args = hdr + (P(O), ST(O), P(do), ST(do), P(DELTA), sp)
+    pre_args = hdr + (P(O), ST(O), P(do), ST(do), P(LSE), P(DELTA), sp)
     grads_args = hdr + (1, scale, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(do), ST(do), P(LSE),
                         P(DELTA), P(dQ), ST(dQ), P(dK), ST(dK), P(dV), ST(dV), sp)
     # The product path: mi_attn_fwd, then mi_attn_bwd = preprocess + grads.

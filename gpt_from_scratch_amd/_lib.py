@@ -28,7 +28,7 @@ EXPORTED = ("mi_version", "mi_status_str", "mi_last_error", "mi_attn_fwd", "mi_a
             "mi_rmsnorm_bwd_workspace", "mi_rmsnorm_bwd", "mi_swiglu_fwd", "mi_swiglu_bwd",
             "mi_adamw_workspace", "mi_grad_sumsq", "mi_adamw_step", "mi_attn_bwd_noalloc")
 
-# B*H*S limit of mi_attn_bwd_noalloc (its static delta array), include/mi_attn.h
+# B*H*S limit of mi_attn_bwd_noalloc (its static workspace array), include/mi_attn.h
 NOALLOC_MAX_ROWS = 1 << 20
 
 _lib = None
@@ -61,7 +61,7 @@ def _declare(lib):
                                         p, i64p, p, i64p, p, i64p, p, i64p, p, i64p,
                                         p, p, i64p, p, i64p, p, i64p, p]
     lib.mi_attn_bwd_preprocess.restype = i
-    lib.mi_attn_bwd_preprocess.argtypes = [i, i, i, i, i, p, i64p, p, i64p, p, p]
+    lib.mi_attn_bwd_preprocess.argtypes = [i, i, i, i, i, p, i64p, p, i64p, p, p, p]
     lib.mi_attn_bwd_grads.restype = i
     lib.mi_attn_bwd_grads.argtypes = [i, i, i, i, i, i, f, p, i64p, p, i64p, p, i64p, p, i64p,
                                       p, p, p, i64p, p, i64p, p, i64p, p]
@@ -151,10 +151,11 @@ def _stream(t: torch.Tensor):
     return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
-def _check_attn_tensors(q, same, stats):
+def _check_attn_tensors(q, same, stats, ws=None):
     """Shapes and dtypes the attention kernels index by: every tensor of `same`
-    is [B, H, S, D] in q's dtype; every one of `stats` (lse, delta) is a dense
-    fp32 [B, H, S] (the kernels address it as (b*H + h)*S + s)."""
+    is [B, H, S, D] in q's dtype; every one of `stats` (lse) is a dense fp32
+    [B, H, S] (the kernels address it as (b*H + h)*S + s); the backward
+    workspace `ws` is a dense fp32 [2, B, H, S] (delta, then lse * log2(e))."""
     if q.dim() != 4:
         raise ValueError(f"q must be [B, H, S, D]; got shape {tuple(q.shape)}")
     B, H, S, _ = q.shape
@@ -166,6 +167,11 @@ def _check_attn_tensors(q, same, stats):
         if t.dtype != torch.float32 or t.shape != (B, H, S) or not t.is_contiguous():
             raise ValueError(f"{name} must be a contiguous float32 [B, H, S] = [{B}, {H}, {S}] "
                              f"tensor; got {t.dtype} {tuple(t.shape)} strides {t.stride()}")
+    if ws is not None and (ws.dtype != torch.float32 or ws.shape != (2, B, H, S)
+                           or not ws.is_contiguous()):
+        raise ValueError(f"the backward workspace must be a contiguous float32 [2, B, H, S] = "
+                         f"[2, {B}, {H}, {S}] tensor; got {ws.dtype} {tuple(ws.shape)} strides "
+                         f"{ws.stride()}")
 
 
 def attn_fwd(q, k, v, o, lse, causal: bool, scale: float):
@@ -180,23 +186,30 @@ def attn_fwd(q, k, v, o, lse, causal: bool, scale: float):
     _check(st, "mi_attn_fwd")
 
 
-def attn_bwd(q, k, v, o, do, lse, delta, dq, dk, dv, causal: bool, scale: float):
-    """Enqueue the backward on the current stream: writes delta, dq, dk, dv."""
+def bwd_workspace(lse):
+    """The backward workspace for a forward's lse [B, H, S]: fp32 [2, B, H, S]
+    (delta = rowsum(dO * O), then lse * log2(e))."""
+    return torch.empty((2,) + tuple(lse.shape), dtype=torch.float32, device=lse.device)
+
+
+def attn_bwd(q, k, v, o, do, lse, ws, dq, dk, dv, causal: bool, scale: float):
+    """Enqueue the backward on the current stream: writes the workspace ws
+    ([2, B, H, S]: delta, lse * log2(e)) and dq, dk, dv."""
     _check_attn_tensors(q, (("k", k), ("v", v), ("o", o), ("do", do), ("dq", dq), ("dk", dk),
-                            ("dv", dv)), (("lse", lse), ("delta", delta)))
-    _require_gpu(q, k, v, o, do, lse, delta, dq, dk, dv)
+                            ("dv", dv)), (("lse", lse),), ws)
+    _require_gpu(q, k, v, o, do, lse, ws, dq, dk, dv)
     B, H, S, D = q.shape
     st = lib().mi_attn_bwd(dtype_code(q), B, H, S, D, int(bool(causal)), float(scale),
                            _ptr(q), _strides(q, 4), _ptr(k), _strides(k, 4),
                            _ptr(v), _strides(v, 4), _ptr(o), _strides(o, 4),
-                           _ptr(do), _strides(do, 4), _ptr(lse), _ptr(delta),
+                           _ptr(do), _strides(do, 4), _ptr(lse), _ptr(ws),
                            _ptr(dq), _strides(dq, 4), _ptr(dk), _strides(dk, 4),
                            _ptr(dv), _strides(dv, 4), _stream(q))
     _check(st, "mi_attn_bwd")
 
 
 def attn_bwd_noalloc(q, k, v, o, do, lse, dq, dk, dv, causal: bool, scale: float):
-    """mi_attn_bwd without a delta workspace (the library's static array): writes dq, dk, dv."""
+    """mi_attn_bwd without a workspace argument (the library's static array): writes dq, dk, dv."""
     _check_attn_tensors(q, (("k", k), ("v", v), ("o", o), ("do", do), ("dq", dq), ("dk", dk),
                             ("dv", dv)), (("lse", lse),))
     _require_gpu(q, k, v, o, do, lse, dq, dk, dv)

@@ -79,10 +79,10 @@ class AttentionBlock(torch.autograd.Function):
                 (s * d_o.element_size()) % 16 for s in d_o.stride()[:-1]):
             d_o = d_o.contiguous()
         d_qkv = torch.empty((S, B, 3, heads, D), dtype=qkv5.dtype, device=qkv5.device)
-        delta = torch.empty((B, heads, S), dtype=torch.float32, device=qkv5.device)
+        ws = _lib.bwd_workspace(lse)
         dq, dk, dv = d_qkv[:, :, 0], d_qkv[:, :, 1], d_qkv[:, :, 2]
         _lib.attn_bwd(rot[:, :, 0].permute(bhsd), rot[:, :, 1].permute(bhsd),
-                      qkv5[:, :, 2].permute(bhsd), o.permute(bhsd), d_o.permute(bhsd), lse, delta,
+                      qkv5[:, :, 2].permute(bhsd), o.permute(bhsd), d_o.permute(bhsd), lse, ws,
                       dq.permute(bhsd), dk.permute(bhsd), dv.permute(bhsd), causal, scale)
         # gradients of the rotated q, k -> gradients of q, k: inverse rotation in place
         _lib.rope_qk(dq, dk, cos, sin, dq, dk, inverse=True)

@@ -35,8 +35,10 @@ namespace mi {
 namespace {
 
 // ---------------------------------------------------------------------------
-// delta[b,h,s] = sum_d dO[b,h,s,d] * O[b,h,s,d]   (fp32 accumulation)
-// Eight lanes per row; each lane takes every 8th chunk of VEC elements.
+// delta[b,h,s] = sum_d dO[b,h,s,d] * O[b,h,s,d]   (fp32 accumulation), and
+// the second half of the workspace: lse * log2(e), the form the dK/dV loop
+// subtracts inside exp2 (one multiply per row here instead of one per score
+// there).  Eight lanes per row; each lane takes every 8th chunk of VEC elements.
 // ---------------------------------------------------------------------------
 template <int DT, int VEC>
 __global__ __launch_bounds__(256) void attn_delta_kernel(AttnArgs a, FastDiv divS, FastDiv divH,
@@ -62,7 +64,10 @@ __global__ __launch_bounds__(256) void attn_delta_kernel(AttnArgs a, FastDiv div
   acc += __shfl_xor(acc, 1, 64);
   acc += __shfl_xor(acc, 2, 64);
   acc += __shfl_xor(acc, 4, 64);
-  if (row < nrows && sub == 0) a.delta[row] = acc;
+  if (row < nrows && sub == 0) {
+    a.delta[row] = acc;
+    a.delta[nrows + row] = a.lse[row] * kLog2e;
+  }
 }
 
 // One 16-bit value (bf16 or fp16, per DT) held in the low bits of x, as fp32.
@@ -117,7 +122,10 @@ __global__ __launch_bounds__(256) void attn_delta_v16_kernel(AttnArgs a, FastDiv
     acc += __shfl_xor(acc, 2, 64);
     acc += __shfl_xor(acc, 4, 64);
     const uint32_t row = rbase + 32 * r;
-    if (row < nrows && sub == 0) a.delta[row] = acc;
+    if (row < nrows && sub == 0) {
+      a.delta[row] = acc;
+      a.delta[nrows + row] = a.lse[row] * kLog2e;
+    }
   }
 }
 
@@ -175,7 +183,7 @@ struct Resident {
 };
 
 // One LDS staging buffer: the two streamed tiles and, for the dK/dV kind,
-// lse and delta of the tile's query rows (as stored in memory).
+// lse * log2(e) and delta of the tile's query rows (as in the workspace).
 struct BwdBuf {
   uint16_t* t0;
   uint16_t* t1;
@@ -200,7 +208,7 @@ struct StageSrc {
   const uint16_t* p1;
   int64_t ss0, ss1;
   uint32_t off0[BwdCfg<D>::SPW], off1[BwdCfg<D>::SPW];
-  const float* lse;
+  const float* lse;    // lse * log2(e) rows of this head
   const float* delta;
 };
 
@@ -239,7 +247,7 @@ __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& 
     if (it.kind) {
       const int64_t o = (int64_t)it.bh * a.S + w0;
       res.lse2 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                     tile_rsrc(a.lse + o, 32 * 4), (lane & 31) * 4, 0, 0)) * kLog2e;
+                     tile_rsrc(a.lse2 + o, 32 * 4), (lane & 31) * 4, 0, 0));
       res.dl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                    tile_rsrc(a.delta + o, 32 * 4), (lane & 31) * 4, 0, 0));
     }
@@ -278,7 +286,7 @@ __device__ __forceinline__ StageSrc<D> stage_src(const AttnArgs& a, const BwdIte
     s.off0[m] = (uint32_t)((r * t0.ss + col) * 2);
     s.off1[m] = (uint32_t)((r * t1.ss + col) * 2);
   }
-  s.lse = a.lse + (int64_t)it.bh * a.S;
+  s.lse = a.lse2 + (int64_t)it.bh * a.S;
   s.delta = a.delta + (int64_t)it.bh * a.S;
   return s;
 }
@@ -407,7 +415,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * jj + i;
-            float p = fast_exp2(__builtin_fmaf(s[r], c, l4[i] * -kLog2e));
+            float p = fast_exp2(__builtin_fmaf(s[r], c, -l4[i]));
             if (MASKED && diag && l32 > 8 * jj + 4 * g + i) p = 0.f;
             s[r] = p;
             dp[r] = -(p * dp[r]);

@@ -95,14 +95,14 @@ mi_status launched(hipError_t e, const char* what) {
 mi_status check_grad_inputs(int dtype, int D, int S, const void* q, const int64_t* qs,
                             const void* k, const int64_t* ks, const void* v, const int64_t* vs,
                             const void* dout, const int64_t* dos, const float* lse,
-                            const float* delta) {
+                            const float* ws) {
   mi_status st;
   if ((st = check_attn_tensor("q", q, qs)) != MI_OK) return st;
   if ((st = check_attn_tensor("k", k, ks)) != MI_OK) return st;
   if ((st = check_attn_tensor("v", v, vs)) != MI_OK) return st;
   if ((st = check_attn_tensor("dout", dout, dos)) != MI_OK) return st;
-  if (lse == nullptr || delta == nullptr)
-    return fail(MI_ERR_INVALID_ARGUMENT, "lse / delta: null pointer");
+  if (lse == nullptr || ws == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "lse / workspace: null pointer");
   if (!mi::valu_supports(D) && !mi::mfma_supports(dtype, D, S))
     return fail(MI_ERR_UNSUPPORTED, "head dim %d not supported (16, 32, 64, 128)", D);
   return MI_OK;
@@ -111,14 +111,15 @@ mi_status check_grad_inputs(int dtype, int D, int S, const void* q, const int64_
 mi::AttnArgs grad_args(int B, int H, int S, int D, int causal, float scale, const void* q,
                        const int64_t* qs, const void* k, const int64_t* ks, const void* v,
                        const int64_t* vs, const void* dout, const int64_t* dos,
-                       const float* lse, const float* delta) {
+                       const float* lse, const float* ws) {
   mi::AttnArgs a = {};
   a.q = targ(q, qs);
   a.k = targ(k, ks);
   a.v = targ(v, vs);
   a.dout = targ(dout, dos);
   a.lse = const_cast<float*>(lse);
-  a.delta = const_cast<float*>(delta);
+  a.delta = const_cast<float*>(ws);                 // ws[0 .. B*H*S): delta
+  a.lse2 = ws + (int64_t)B * H * S;                 // ws[B*H*S ..): lse * log2(e)
   a.B = B; a.H = H; a.S = S; a.D = D;
   a.scale = scale;
   a.scale_log2 = scale * 1.4426950408889634f;
@@ -130,7 +131,7 @@ mi::AttnArgs grad_args(int B, int H, int S, int D, int causal, float scale, cons
 
 extern "C" {
 
-int mi_version(void) { return (1 << 16) | 0; }
+int mi_version(void) { return (2 << 16) | 0; }
 
 const char* mi_status_str(mi_status s) {
   switch (s) {
@@ -182,7 +183,7 @@ mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal, fl
                       const void* q, const int64_t q_strides[4], const void* k,
                       const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
                       const void* o, const int64_t o_strides[4], const void* dout,
-                      const int64_t dout_strides[4], const float* lse, float* delta, void* dq,
+                      const int64_t dout_strides[4], const float* lse, float* ws, void* dq,
                       const int64_t dq_strides[4], void* dk, const int64_t dk_strides[4],
                       void* dv, const int64_t dv_strides[4], void* stream) {
   // Validate everything up front so that nothing is enqueued on a bad call.
@@ -191,15 +192,15 @@ mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal, fl
   if ((st = check_attn_tensor("o", o, o_strides)) != MI_OK) return st;
   if ((st = check_attn_tensor("dq", dq, dq_strides)) != MI_OK) return st;
   if ((st = check_grad_inputs(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
-                              dout_strides, lse, delta)) != MI_OK)
+                              dout_strides, lse, ws)) != MI_OK)
     return st;
   if ((st = check_attn_tensor("dk", dk, dk_strides)) != MI_OK) return st;
   if ((st = check_attn_tensor("dv", dv, dv_strides)) != MI_OK) return st;
-  if ((st = mi_attn_bwd_preprocess(dtype, B, H, S, D, o, o_strides, dout, dout_strides, delta,
+  if ((st = mi_attn_bwd_preprocess(dtype, B, H, S, D, o, o_strides, dout, dout_strides, lse, ws,
                                    stream)) != MI_OK)
     return st;
   return mi_attn_bwd_grads(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
-                           v_strides, dout, dout_strides, lse, delta, dq, dq_strides, dk,
+                           v_strides, dout, dout_strides, lse, ws, dq, dq_strides, dk,
                            dk_strides, dv, dv_strides, stream);
 }
 
@@ -207,14 +208,14 @@ mi_status mi_attn_bwd_grads(mi_dtype dtype, int B, int H, int S, int D, int caus
                             const void* q, const int64_t q_strides[4], const void* k,
                             const int64_t k_strides[4], const void* v,
                             const int64_t v_strides[4], const void* dout,
-                            const int64_t dout_strides[4], const float* lse, const float* delta,
+                            const int64_t dout_strides[4], const float* lse, const float* ws,
                             void* dq, const int64_t dq_strides[4], void* dk,
                             const int64_t dk_strides[4], void* dv, const int64_t dv_strides[4],
                             void* stream) {
   mi_status st;
   if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
   if ((st = check_grad_inputs(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
-                              dout_strides, lse, delta)) != MI_OK)
+                              dout_strides, lse, ws)) != MI_OK)
     return st;
   if ((st = check_attn_tensor("dq", dq, dq_strides)) != MI_OK) return st;
   if ((st = check_attn_tensor("dk", dk, dk_strides)) != MI_OK) return st;
@@ -225,32 +226,35 @@ mi_status mi_attn_bwd_grads(mi_dtype dtype, int B, int H, int S, int D, int caus
       aligned16(dout, dout_strides, esz) && aligned16(dq, dq_strides, esz) &&
       aligned16(dk, dk_strides, esz) && aligned16(dv, dv_strides, esz)) {
     mi::AttnArgs a = grad_args(B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
-                               v_strides, dout, dout_strides, lse, delta);
+                               v_strides, dout, dout_strides, lse, ws);
     a.dq = targ(dq, dq_strides);
     a.dk = targ(dk, dk_strides);
     a.dv = targ(dv, dv_strides);
     return launched(mi::launch_attn_bwd_mfma(dtype, a, (hipStream_t)stream), "attn_bwd_mfma");
   }
   if ((st = mi_attn_bwd_dkdv(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
-                             v_strides, dout, dout_strides, lse, delta, dk, dk_strides, dv,
+                             v_strides, dout, dout_strides, lse, ws, dk, dk_strides, dv,
                              dv_strides, stream)) != MI_OK)
     return st;
   return mi_attn_bwd_dq(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
-                        v_strides, dout, dout_strides, lse, delta, dq, dq_strides, stream);
+                        v_strides, dout, dout_strides, lse, ws, dq, dq_strides, stream);
 }
 
 mi_status mi_attn_bwd_preprocess(mi_dtype dtype, int B, int H, int S, int D, const void* o,
                                  const int64_t o_strides[4], const void* dout,
-                                 const int64_t dout_strides[4], float* delta, void* stream) {
+                                 const int64_t dout_strides[4], const float* lse, float* ws,
+                                 void* stream) {
   mi_status st;
   if ((st = check_shape(dtype, B, H, S, D, 1.f)) != MI_OK) return st;
   if ((st = check_attn_tensor("o", o, o_strides)) != MI_OK) return st;
   if ((st = check_attn_tensor("dout", dout, dout_strides)) != MI_OK) return st;
-  if (delta == nullptr) return fail(MI_ERR_INVALID_ARGUMENT, "delta: null pointer");
+  if (lse == nullptr || ws == nullptr)
+    return fail(MI_ERR_INVALID_ARGUMENT, "lse / workspace: null pointer");
   mi::AttnArgs a = {};
   a.o = targ(o, o_strides);
   a.dout = targ(dout, dout_strides);
-  a.delta = delta;
+  a.lse = const_cast<float*>(lse);
+  a.delta = ws;
   a.B = B; a.H = H; a.S = S; a.D = D;
   return launched(mi::launch_attn_delta(dtype, a, (hipStream_t)stream), "attn_delta");
 }
@@ -259,17 +263,17 @@ mi_status mi_attn_bwd_dkdv(mi_dtype dtype, int B, int H, int S, int D, int causa
                            const void* q, const int64_t q_strides[4], const void* k,
                            const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
                            const void* dout, const int64_t dout_strides[4], const float* lse,
-                           const float* delta, void* dk, const int64_t dk_strides[4], void* dv,
+                           const float* ws, void* dk, const int64_t dk_strides[4], void* dv,
                            const int64_t dv_strides[4], void* stream) {
   mi_status st;
   if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
   if ((st = check_grad_inputs(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
-                              dout_strides, lse, delta)) != MI_OK)
+                              dout_strides, lse, ws)) != MI_OK)
     return st;
   if ((st = check_attn_tensor("dk", dk, dk_strides)) != MI_OK) return st;
   if ((st = check_attn_tensor("dv", dv, dv_strides)) != MI_OK) return st;
   mi::AttnArgs a = grad_args(B, H, S, D, causal, scale, q, q_strides, k, k_strides, v, v_strides,
-                             dout, dout_strides, lse, delta);
+                             dout, dout_strides, lse, ws);
   a.dk = targ(dk, dk_strides);
   a.dv = targ(dv, dv_strides);
   const int esz = elem_size(dtype);
@@ -286,16 +290,16 @@ mi_status mi_attn_bwd_dq(mi_dtype dtype, int B, int H, int S, int D, int causal,
                          const void* q, const int64_t q_strides[4], const void* k,
                          const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
                          const void* dout, const int64_t dout_strides[4], const float* lse,
-                         const float* delta, void* dq, const int64_t dq_strides[4],
+                         const float* ws, void* dq, const int64_t dq_strides[4],
                          void* stream) {
   mi_status st;
   if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
   if ((st = check_grad_inputs(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
-                              dout_strides, lse, delta)) != MI_OK)
+                              dout_strides, lse, ws)) != MI_OK)
     return st;
   if ((st = check_attn_tensor("dq", dq, dq_strides)) != MI_OK) return st;
   mi::AttnArgs a = grad_args(B, H, S, D, causal, scale, q, q_strides, k, k_strides, v, v_strides,
-                             dout, dout_strides, lse, delta);
+                             dout, dout_strides, lse, ws);
   a.dq = targ(dq, dq_strides);
   const int esz = elem_size(dtype);
   const bool al = aligned16(q, q_strides, esz) && aligned16(k, k_strides, esz) &&
@@ -669,14 +673,14 @@ mi_status mi_adamw_step(mi_dtype grad_dtype, mi_dtype param_dtype, int64_t n, co
 }  // extern "C"
 
 // ---------------------------------------------------------------------------
-// mi_attn_bwd_noalloc: the delta workspace of mi_attn_bwd taken from a static
+// mi_attn_bwd_noalloc: the workspace of mi_attn_bwd taken from a static
 // device array instead of the caller.  `scratch` names a host-side stand-in
 // for the array in host code, so host code only ever uses the per-device
 // address that hipGetSymbolAddress returns (kept in g_scratch).
 // ---------------------------------------------------------------------------
 namespace {
 
-__device__ __attribute__((aligned(256))) float scratch[MI_ATTN_NOALLOC_MAX_ROWS];
+__device__ __attribute__((aligned(256))) float scratch[2 * MI_ATTN_NOALLOC_MAX_ROWS];
 
 constexpr int kMaxDevices = 64;
 std::atomic<float*> g_scratch[kMaxDevices];
@@ -724,13 +728,13 @@ extern "C" mi_status mi_attn_bwd_noalloc(
   const int64_t rows = (int64_t)B * H * S;
   if (rows > MI_ATTN_NOALLOC_MAX_ROWS)
     return fail(MI_ERR_INVALID_ARGUMENT,
-                "B*H*S = %lld exceeds MI_ATTN_NOALLOC_MAX_ROWS = %d (the static delta array)",
+                "B*H*S = %lld exceeds MI_ATTN_NOALLOC_MAX_ROWS = %d (the static workspace)",
                 (long long)rows, MI_ATTN_NOALLOC_MAX_ROWS);
-  float* delta = nullptr;
-  if ((st = scratch_on(stream, &delta)) != MI_OK) return st;
+  float* ws = nullptr;
+  if ((st = scratch_on(stream, &ws)) != MI_OK) return st;
   // mi_attn_bwd validates every other argument before it enqueues anything;
-  // the preprocess overwrites delta[0, rows) before the gradient launch reads it.
+  // the preprocess overwrites ws[0, 2 * rows) before the gradient launch reads it.
   return mi_attn_bwd(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v, v_strides,
-                     o, o_strides, dout, dout_strides, lse, delta, dq, dq_strides, dk, dk_strides,
+                     o, o_strides, dout, dout_strides, lse, ws, dq, dq_strides, dk, dk_strides,
                      dv, dv_strides, stream);
 }

@@ -17,7 +17,8 @@ struct TensorArg {
 struct AttnArgs {
   TensorArg q, k, v, o, dout, dq, dk, dv;
   float* lse;
-  float* delta;
+  float* delta;        // backward workspace [2, B, H, S]: delta, then lse2
+  const float* lse2;   // lse * log2(e) (= delta + B*H*S), written by the preprocess
   int B, H, S, D;
   float scale;       // softmax scale (1/sqrt(D) in the model)
   float scale_log2;  // scale * log2(e)

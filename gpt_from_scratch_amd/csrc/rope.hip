@@ -12,9 +12,10 @@
 // q and of k, so a wave reads whole 1 KiB segments of both, the angles of
 // those pairs come in with one vector load per table and serve both tensors,
 // and the index decomposition (multiply-high division by the run-time
-// sizes) is done once.  Results are written with non-temporal stores (the
-// output is not read again by this kernel; measured ~15% faster than plain
-// stores at the model's shapes).  A scalar path (one pair per lane, any
+// sizes) is done once.  Every lane takes four items and issues all their
+// loads before the first store.  Results are written with non-temporal
+// stores (the output is not read again by this kernel; measured ~15% faster
+// than plain stores at the model's shapes).  A scalar path (one pair per lane, any
 // strides) covers layouts the vector path cannot.
 #include "mi_device.h"
 #include "mi_kernels.h"
@@ -81,61 +82,75 @@ __device__ __forceinline__ void load_angles(const void* tab, int64_t i, float (&
 
 // 16-byte vector path: requires unit dim strides, D % VEC == 0, 16-byte
 // aligned rows, unit pair stride in the tables and table rows (and bases)
-// aligned to the angle vector.  NTEN tensors (q, or q and k) per lane.
-template <int XDT, int TDT, int NTEN>
+// aligned to the angle vector.  NTEN tensors (q, or q and k) per lane.  A
+// workgroup covers U * 256 consecutive items, lane i items i, i + 256, ...
+// (each pass of 256 lanes reads whole 1 KiB segments); every lane issues all
+// its loads (tables and the U chunks of both tensors) before its first store,
+// so U * NTEN 16-byte loads per lane are in flight at once.
+template <int XDT, int TDT, int NTEN, int U>
 __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a, RopeDivs dv, uint32_t total) {
   constexpr int VEC = (XDT == 0) ? 4 : 8;  // elements per lane and tensor
   constexpr int NP = VEC / 2;               // pairs per lane
-  for (uint32_t item = blockIdx.x * 256u + threadIdx.x; item < total; item += gridDim.x * 256u) {
-  uint32_t r = fdiv(item, dv.C);
-  const uint32_t cidx = item - r * dv.C.d;
-  const uint32_t r2 = fdiv(r, dv.H);
-  const uint32_t h = r - r2 * dv.H.d;
-  const uint32_t s = fdiv(r2, dv.B);
-  const uint32_t b = r2 - s * dv.B.d;
-  const int pair0 = cidx * NP;
-
-  float cs[NP], sn[NP];
-  load_angles<TDT, NP>(a.cos_tab, s * a.cs_s + pair0, cs);
-  load_angles<TDT, NP>(a.sin_tab, s * a.ss_s + pair0, sn);
-
+  const uint32_t first = blockIdx.x * (256u * U) + threadIdx.x;
+  u32x4 x[U][NTEN];
+  float cs[U][NP], sn[U][NP];
+  int64_t out_off[U][NTEN];
 #pragma unroll
-  for (int t = 0; t < NTEN; ++t) {
-  const RopeTensor& T = a.t[t];
-  const int64_t in_off = s * T.is_s + b * T.is_b + h * T.is_h + (int64_t)cidx * VEC;
-  const int64_t out_off = s * T.os_s + b * T.os_b + h * T.os_h + (int64_t)cidx * VEC;
-  if constexpr (XDT == 0) {
-    const f32x4 x = *(const f32x4*)((const float*)T.in + in_off);
-    f32x4 y;
+  for (int u = 0; u < U; ++u) {
+    const uint32_t item = first + 256u * u;
+    if (item >= total) continue;
+    uint32_t r = fdiv(item, dv.C);
+    const uint32_t cidx = item - r * dv.C.d;
+    const uint32_t r2 = fdiv(r, dv.H);
+    const uint32_t h = r - r2 * dv.H.d;
+    const uint32_t s = fdiv(r2, dv.B);
+    const uint32_t b = r2 - s * dv.B.d;
+    const int pair0 = cidx * NP;
+    load_angles<TDT, NP>(a.cos_tab, s * a.cs_s + pair0, cs[u]);
+    load_angles<TDT, NP>(a.sin_tab, s * a.ss_s + pair0, sn[u]);
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      float re, ro;
-      rotate(x[2 * p], x[2 * p + 1], cs[p], sn[p], a.inverse, re, ro);
-      y[2 * p] = re;
-      y[2 * p + 1] = ro;
+    for (int t = 0; t < NTEN; ++t) {
+      const RopeTensor& T = a.t[t];
+      const int64_t in_off = s * T.is_s + b * T.is_b + h * T.is_h + (int64_t)cidx * VEC;
+      out_off[u][t] = s * T.os_s + b * T.os_b + h * T.os_h + (int64_t)cidx * VEC;
+      x[u][t] = (XDT == 0) ? *(const u32x4*)((const float*)T.in + in_off)
+                           : *(const u32x4*)((const uint16_t*)T.in + in_off);
     }
-    __builtin_nontemporal_store(y, (f32x4*)((float*)T.out + out_off));
-  } else {
-    const u32x4 x = *(const u32x4*)((const uint16_t*)T.in + in_off);
-    u32x4 y;
+  }
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const uint32_t w = x[p];
-      float e, o;
-      if constexpr (XDT == 2) {
-        e = __uint_as_float(w << 16);
-        o = __uint_as_float(w & 0xffff0000u);
-      } else {
-        e = F16::to_f32((uint16_t)(w & 0xffffu));
-        o = F16::to_f32((uint16_t)(w >> 16));
+  for (int u = 0; u < U; ++u) {
+    if (first + 256u * u >= total) continue;
+#pragma unroll
+    for (int t = 0; t < NTEN; ++t) {
+      u32x4 y;
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        float e, o;
+        if constexpr (XDT == 0) {
+          e = __uint_as_float(x[u][t][2 * p]);
+          o = __uint_as_float(x[u][t][2 * p + 1]);
+        } else if constexpr (XDT == 2) {
+          e = __uint_as_float(x[u][t][p] << 16);
+          o = __uint_as_float(x[u][t][p] & 0xffff0000u);
+        } else {
+          e = F16::to_f32((uint16_t)(x[u][t][p] & 0xffffu));
+          o = F16::to_f32((uint16_t)(x[u][t][p] >> 16));
+        }
+        float re, ro;
+        rotate(e, o, cs[u][p], sn[u][p], a.inverse, re, ro);
+        if constexpr (XDT == 0) {
+          y[2 * p] = __float_as_uint(re);
+          y[2 * p + 1] = __float_as_uint(ro);
+        } else {
+          y[p] = (XDT == 2) ? BF16::pack2(re, ro) : F16::pack2(re, ro);
+        }
       }
-      float re, ro;
-      rotate(e, o, cs[p], sn[p], a.inverse, re, ro);
-      y[p] = (XDT == 2) ? BF16::pack2(re, ro) : F16::pack2(re, ro);
+      const RopeTensor& T = a.t[t];
+      if constexpr (XDT == 0)
+        __builtin_nontemporal_store(y, (u32x4*)((float*)T.out + out_off[u][t]));
+      else
+        __builtin_nontemporal_store(y, (u32x4*)((uint16_t*)T.out + out_off[u][t]));
     }
-    __builtin_nontemporal_store(y, (u32x4*)((uint16_t*)T.out + out_off));
-  }
-  }
   }
 }
 
@@ -180,15 +195,15 @@ hipError_t rope_launch(const RopeArgs& a, bool vec, hipStream_t st) {
   if (vec) {
     // one lane per (s, b, h, 16-byte chunk), all tensors
     const uint64_t total = (uint64_t)a.S * a.B * a.H * C;
-    // a grid-stride loop over at most 2048 workgroups: 4% faster than one item
-    // per lane when the inputs are cache-resident, the same from HBM (512: slower)
-    uint64_t nwg = (total + 255) / 256;
-    if (nwg > 2048) nwg = 2048;
-    const dim3 grid((uint32_t)nwg), block(256);
+    // four items per lane (C2: 768 workgroups, every load of the launch in
+    // flight at once): 9.3 us from HBM against 10.7 us for the grid-stride loop
+    // over 2048 workgroups; two items 10.6, six 10.2, eight 12.2 us
+    constexpr int U = 4;
+    const dim3 grid((uint32_t)((total + 256 * U - 1) / (256 * U))), block(256);
     if (a.ntensors == 2)
-      hipLaunchKernelGGL((rope_vec_kernel<XDT, TDT, 2>), grid, block, 0, st, a, dv, (uint32_t)total);
+      hipLaunchKernelGGL((rope_vec_kernel<XDT, TDT, 2, U>), grid, block, 0, st, a, dv, (uint32_t)total);
     else
-      hipLaunchKernelGGL((rope_vec_kernel<XDT, TDT, 1>), grid, block, 0, st, a, dv, (uint32_t)total);
+      hipLaunchKernelGGL((rope_vec_kernel<XDT, TDT, 1, U>), grid, block, 0, st, a, dv, (uint32_t)total);
   } else {
     const uint64_t total = (uint64_t)a.ntensors * a.S * a.B * a.H * C;
     const dim3 grid((uint32_t)((total + 255) / 256)), block(256);

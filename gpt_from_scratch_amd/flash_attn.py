@@ -68,11 +68,11 @@ class FlashAttn(torch.autograd.Function):
         dO = _kernel_ready(dO)
         if dO.dtype != Q.dtype:
             dO = dO.to(Q.dtype)
-        D = torch.empty_like(M)
+        ws = _lib.bwd_workspace(M)  # D (the reference's delta, :323) and lse * log2(e)
         dQ = torch.empty(Q.shape, dtype=Q.dtype, device=Q.device)
         dK = torch.empty(K.shape, dtype=K.dtype, device=K.device)
         dV = torch.empty(V.shape, dtype=V.dtype, device=V.device)
-        _lib.attn_bwd(Q, K, V, O, dO, M, D, dQ, dK, dV, ctx.causal_mask, ctx.softmax_scale)
+        _lib.attn_bwd(Q, K, V, O, dO, M, ws, dQ, dK, dV, ctx.causal_mask, ctx.softmax_scale)
         return dQ, dK, dV, None
 
 
@@ -97,9 +97,9 @@ def flash_attn_backward(q, k, v, o, m, do, causal_mask=True):
     """Backward only, without autograd: returns ``(dQ, dK, dV, delta)``."""
     B, H, S, D = q.shape
     q, k, v, do = _kernel_ready(q), _kernel_ready(k), _kernel_ready(v), _kernel_ready(do)
-    delta = torch.empty_like(m)
+    ws = _lib.bwd_workspace(m)
     dq = torch.empty(q.shape, dtype=q.dtype, device=q.device)
     dk = torch.empty_like(dq)
     dv = torch.empty_like(dq)
-    _lib.attn_bwd(q, k, v, o, do, m, delta, dq, dk, dv, causal_mask, 1.0 / (D ** 0.5))
-    return dq, dk, dv, delta
+    _lib.attn_bwd(q, k, v, o, do, m, ws, dq, dk, dv, causal_mask, 1.0 / (D ** 0.5))
+    return dq, dk, dv, ws[0]

@@ -14,8 +14,9 @@
  *   - attention tensors are logically [B, H, S, D]; `*_strides` holds the four
  *     element strides in that order (batch, head, seq, dim).  The dim stride
  *     must be 1 (other strides are free).
- *   - lse and delta are dense fp32 [B, H, S] (natural-log log-sum-exp of the
- *     scaled, masked scores; delta = rowsum(dO * O)).
+ *   - lse is dense fp32 [B, H, S] (natural-log log-sum-exp of the scaled,
+ *     masked scores); the backward workspace is dense fp32 [2, B, H, S]
+ *     (delta = rowsum(dO * O), then lse * log2(e); see mi_attn_bwd).
  *   - rope tensors are logically [S, B, H, D] (the layout the model hands to
  *     RoPE); the cos/sin tables are [S, D/2] with two element strides.
  *   - dtypes: MI_F32, MI_F16, MI_BF16.  Attention runs on bf16/f16 MFMA when
@@ -76,8 +77,14 @@ mi_status mi_attn_fwd(mi_dtype dtype, int B, int H, int S, int D, int causal,
                       float* lse, void* stream);
 
 /*
- * Flash-attention backward: delta = rowsum(dO * O) into the caller's fp32
- * [B,H,S] workspace, then dQ, dK, dV.  lse is the forward's output.
+ * Backward workspace `ws`: 2*B*H*S fp32 values, caller-allocated, written by
+ * mi_attn_bwd_preprocess and read by the gradient launches:
+ *   ws[0 .. B*H*S)          delta[b,h,s] = rowsum(dO * O)  (the reference's D)
+ *   ws[B*H*S .. 2*B*H*S)    lse[b,h,s] * log2(e)           (exp2 argument scale)
+ * both indexed (b*H + h)*S + s.
+ *
+ * Flash-attention backward: the workspace, then dQ, dK, dV.  lse is the
+ * forward's output (natural log).
  * Replaces FlashAttn.backward's three launches, core/myFlashAttn.py:288-441
  * (`_attn_bwd_precompute` :330, `_attn_bwd_LoopQ` :365, `_attn_bwd_LoopKV` :409).
  */
@@ -88,7 +95,7 @@ mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal,
                       const void* v, const int64_t v_strides[4],
                       const void* o, const int64_t o_strides[4],
                       const void* dout, const int64_t dout_strides[4],
-                      const float* lse, float* delta,
+                      const float* lse, float* ws,
                       void* dq, const int64_t dq_strides[4],
                       void* dk, const int64_t dk_strides[4],
                       void* dv, const int64_t dv_strides[4],
@@ -107,23 +114,23 @@ mi_status mi_attn_bwd_grads(mi_dtype dtype, int B, int H, int S, int D, int caus
                             const void* k, const int64_t k_strides[4],
                             const void* v, const int64_t v_strides[4],
                             const void* dout, const int64_t dout_strides[4],
-                            const float* lse, const float* delta,
+                            const float* lse, const float* ws,
                             void* dq, const int64_t dq_strides[4],
                             void* dk, const int64_t dk_strides[4],
                             void* dv, const int64_t dv_strides[4],
                             void* stream);
 
 /*
- * delta = rowsum(dO * O) (fp32).
+ * The backward workspace: delta = rowsum(dO * O) (fp32) and lse * log2(e).
  * Replaces the `_attn_bwd_precompute` launch, core/myFlashAttn.py:323-346.
  */
 mi_status mi_attn_bwd_preprocess(mi_dtype dtype, int B, int H, int S, int D,
                                  const void* o, const int64_t o_strides[4],
                                  const void* dout, const int64_t dout_strides[4],
-                                 float* delta, void* stream);
+                                 const float* lse, float* ws, void* stream);
 
 /*
- * dK and dV: per key tile, loop over query tiles (needs lse and delta).
+ * dK and dV: per key tile, loop over query tiles (needs lse and the workspace).
  * Replaces the `_attn_bwd_LoopQ` launch, core/myFlashAttn.py:349-396.
  */
 mi_status mi_attn_bwd_dkdv(mi_dtype dtype, int B, int H, int S, int D, int causal,
@@ -132,13 +139,13 @@ mi_status mi_attn_bwd_dkdv(mi_dtype dtype, int B, int H, int S, int D, int causa
                            const void* k, const int64_t k_strides[4],
                            const void* v, const int64_t v_strides[4],
                            const void* dout, const int64_t dout_strides[4],
-                           const float* lse, const float* delta,
+                           const float* lse, const float* ws,
                            void* dk, const int64_t dk_strides[4],
                            void* dv, const int64_t dv_strides[4],
                            void* stream);
 
 /*
- * dQ: per query tile, loop over key tiles (needs lse and delta).
+ * dQ: per query tile, loop over key tiles (needs lse and the workspace).
  * Replaces the `_attn_bwd_LoopKV` launch, core/myFlashAttn.py:398-439.
  */
 mi_status mi_attn_bwd_dq(mi_dtype dtype, int B, int H, int S, int D, int causal,
@@ -147,7 +154,7 @@ mi_status mi_attn_bwd_dq(mi_dtype dtype, int B, int H, int S, int D, int causal,
                          const void* k, const int64_t k_strides[4],
                          const void* v, const int64_t v_strides[4],
                          const void* dout, const int64_t dout_strides[4],
-                         const float* lse, const float* delta,
+                         const float* lse, const float* ws,
                          void* dq, const int64_t dq_strides[4],
                          void* stream);
 
@@ -304,12 +311,12 @@ mi_status mi_adamw_step(mi_dtype grad_dtype, mi_dtype param_dtype, int64_t n, co
                         float eps, float clip, const float* grad_sumsq, void* stream);
 
 /*
- * mi_attn_bwd without the delta workspace argument, for callers that cannot
+ * mi_attn_bwd without the workspace argument, for callers that cannot
  * allocate device memory: code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc.  It has no counterpart in the reference
  * (whose backward allocates D itself, core/myFlashAttn.py:323).
- * delta lives in a library-owned static device array of
- * MI_ATTN_NOALLOC_MAX_ROWS floats (4 MiB) on each GPU the library runs on,
+ * The workspace lives in a library-owned static device array of
+ * 2 * MI_ATTN_NOALLOC_MAX_ROWS floats (8 MiB) on each GPU the library runs on,
  * held until the process ends; its address is looked up once per device on
  * the first call there.  B*H*S must not exceed MI_ATTN_NOALLOC_MAX_ROWS
  * (MI_ERR_INVALID_ARGUMENT otherwise, before anything is enqueued).  The call

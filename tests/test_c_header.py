@@ -18,7 +18,7 @@ C_SOURCE = r"""
 #include "mi_attn.h"
 
 int main(void) {
-  if ((mi_version() >> 16) != 1) return 1;
+  if ((mi_version() >> 16) != 2) return 1;
   if (strcmp(mi_status_str(MI_OK), "ok") != 0) return 2;
   const int64_t st[4] = {0, 0, 64, 1};
   char dummy[16];

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.lib()
     for name in _declared():
         assert hasattr(lib, name), name
-    assert lib.mi_version() >> 16 == 1
+    assert lib.mi_version() >> 16 == 2
 
 
 def test_status_strings():
@@ -106,7 +106,7 @@ def test_python_api_shape_errors():
 
 
 def test_attention_stats_and_gradient_checks():
-    """lse/delta must be dense fp32 [B, H, S] and dO must match q: checked before
+    """lse must be dense fp32 [B, H, S] and dO must match q: checked before
     any launch (the kernels index them as (b*H + h)*S + s)."""
     import torch
     from gpt_from_scratch_amd import flash_attn_backward

@@ -260,12 +260,14 @@ def test_backward_with_strided_grad(gpu):
 @pytest.mark.parametrize("layout", ["bhsd", "sbhd"])
 @pytest.mark.parametrize("D,extra", [(64, 1), (64, 8), (128, 1), (128, 8), (32, 8)])
 def test_preprocess_row_pitch(gpu, D, extra, layout):
-    """delta = rowsum(dO * O) through the C ABI with dO rows at a pitch of
+    """The backward workspace through the C ABI: delta = rowsum(dO * O) and
+    lse * log2(e), with dO rows at a pitch of
     D + extra elements: an odd pitch leaves rows unaligned (scalar path), a
     pitch of D + 8 keeps them 16-byte aligned (vector paths for D = 64, 128).
     dO is [B,H,S,*] or a permuted view of [S,B,H,*] (position-major, as the
     model's gradient arrives).
-    Against the float64 row sums of the same bf16 values, to fp32 rounding."""
+    Against the float64 row sums of the same bf16 values, to fp32 rounding; the
+    second half equals the fp32 product lse * log2(e) exactly."""
     import ctypes
     from gpt_from_scratch_amd import _lib
     B, H, S = 2, 3, 150
@@ -276,13 +278,17 @@ def test_preprocess_row_pitch(gpu, D, extra, layout):
         do = seeded((S, B, H, D + extra), 71 + D).to(gpu)[..., :D].permute(1, 2, 0, 3)
         assert do.stride(2) > do.stride(0)
     assert do.stride(3) == 1 and (do.stride(2) - D if layout == "bhsd" else do.stride(1) - D) == extra
-    delta = torch.empty(B, H, S, device=gpu)
+    lse = seeded((B, H, S), 72 + D, std=4.0, dtype=torch.float32).to(gpu)
+    ws = torch.empty(2, B, H, S, device=gpu)
     lib = _lib.lib()
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
     rc = lib.mi_attn_bwd_preprocess(2, B, H, S, D, ctypes.c_void_p(o.data_ptr()),
                                     _lib._strides(o, 4), ctypes.c_void_p(do.data_ptr()),
-                                    _lib._strides(do, 4), ctypes.c_void_p(delta.data_ptr()), st)
+                                    _lib._strides(do, 4), ctypes.c_void_p(lse.data_ptr()),
+                                    ctypes.c_void_p(ws.data_ptr()), st)
     assert rc == 0, lib.mi_last_error()
+    delta = ws[0]
+    assert torch.equal(ws[1], lse * 1.4426950408889634)
     # delta as defined by `_attn_bwd_precompute` (core/myFlashAttn.py:787)
     want = (do.cpu().double() * o.cpu().double()).sum(-1)
     err = (delta.cpu().double() - want).abs() / want.abs().clamp_min(1.0)
@@ -313,7 +319,7 @@ def test_backward_deterministic_writes_every_output_keeps_inputs(gpu, B, H, S, D
                    for _ in range(4))
     O = torch.empty_like(Q)
     M = torch.empty(B, H, S, device=gpu)
-    Dl = torch.empty_like(M)
+    Dl = torch.empty(2, B, H, S, device=gpu)
     dQ, dK, dV = (torch.full_like(Q, float("nan")) for _ in range(3))
     P = lambda t: ctypes.c_void_p(t.data_ptr())
     ST = lambda t: (ctypes.c_int64 * 4)(*t.stride())
@@ -321,7 +327,8 @@ def test_backward_deterministic_writes_every_output_keeps_inputs(gpu, B, H, S, D
     sc = 1 / math.sqrt(D)
     assert lib.mi_attn_fwd(2, B, H, S, D, 1, sc, P(Q), ST(Q), P(K), ST(K), P(V), ST(V), P(O),
                            ST(O), P(M), sp) == 0
-    assert lib.mi_attn_bwd_preprocess(2, B, H, S, D, P(O), ST(O), P(dO), ST(dO), P(Dl), sp) == 0
+    assert lib.mi_attn_bwd_preprocess(2, B, H, S, D, P(O), ST(O), P(dO), ST(dO), P(M), P(Dl),
+                                      sp) == 0
     before = [t.clone() for t in (Q, K, V, dO, M, Dl)]
     runs = []
     for _ in range(3):

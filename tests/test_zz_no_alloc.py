@@ -1,7 +1,7 @@
-"""mi_attn_bwd_noalloc (delta in the library's static device array) against
-mi_attn_bwd (caller's delta workspace): the same kernels, so dQ, dK and dV must
+"""mi_attn_bwd_noalloc (workspace in the library's static device array) against
+mi_attn_bwd (caller's workspace): the same kernels, so dQ, dK and dV must
 be bit-identical.  Two calls in a row, the second with a smaller input (the
-array keeps the first call's delta); D = 64 and D = 128, causal and not; the
+array keeps the first call's workspace); D = 64 and D = 128, causal and not; the
 size limit is refused before anything is enqueued."""
 import math
 
@@ -27,8 +27,8 @@ def test_noalloc_backward_matches_workspace_backward(gpu):
         q, k, v, o, do, lse = _inputs(gpu, B, H, S, D, 300 + S + D)
         scale = 1.0 / math.sqrt(D)
         want = [torch.empty_like(q) for _ in range(3)]
-        delta = torch.empty_like(lse)
-        _lib.attn_bwd(q, k, v, o, do, lse, delta, *want, causal, scale)
+        ws = _lib.bwd_workspace(lse)
+        _lib.attn_bwd(q, k, v, o, do, lse, ws, *want, causal, scale)
         got = [torch.full_like(q, float("nan")) for _ in range(3)]
         _lib.attn_bwd_noalloc(q, k, v, o, do, lse, *got, causal, scale)
         torch.cuda.synchronize()
@@ -37,7 +37,7 @@ def test_noalloc_backward_matches_workspace_backward(gpu):
 
 
 def test_noalloc_refuses_more_rows_than_its_array(gpu):
-    """Sizes beyond the static array are refused from the sizes alone (the
+    """Sizes beyond the static workspace are refused from the sizes alone (the
     tensor pointers are NULL, which the full validation would refuse too)."""
     from gpt_from_scratch_amd import _lib
     lib = _lib.lib()
