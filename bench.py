@@ -17,7 +17,15 @@ the dominant kernel, the RoPE bandwidth, the train step's fused operators and
 config-5 tokens/s, and the CPU baseline (the oracle's fp32 eager attention on
 the host cores).
 
+Every measured launch loop (the per-kernel passes, the RoPE, operator and
+D = 128 loops, the copy that calibrates the HBM byte counters) runs inside a
+roctx profiler region, so that ``rocprofv3 --selected-regions`` records the
+dispatches the printed averages come from and no others (not the clock
+warm-up, the timed steps or the train step).  ``--summarize DIR`` prints the
+per-kernel averages of the rocprofv3 CSV output under DIR.
+
 Usage: python bench.py [--steps K] [--warmup W] [--gpus 1]
+       python bench.py --summarize DIR
 """
 import argparse
 import ctypes
@@ -52,10 +60,46 @@ def parse_args():
                     help="skip the D = 128 attention measurements (configs 3 and 4)")
     ap.add_argument("--no-model-ops", action="store_true",
                     help="skip the config-5 model-operator kernel measurements")
-    ap.add_argument("--calibrate-copy", action="store_true",
-                    help="after the timed steps, run a plain elementwise kernel that reads and "
-                         "writes 256 MiB each (reference point for HBM byte counters)")
+    ap.add_argument("--summarize", metavar="DIR",
+                    help="print per-kernel averages from the rocprofv3 CSV files under DIR "
+                         "(kernel_stats / kernel_trace / counter_collection) and exit")
     return ap.parse_args()
+
+
+class _ProfilerRegions:
+    """roctxProfilerResume / roctxProfilerPause around the measured loops.
+    Without a profiler attached both calls do nothing; when the roctx library
+    is absent the regions are empty statements."""
+
+    def __init__(self):
+        self.lib = None
+        for name in ("librocprofiler-sdk-roctx.so.1", "/opt/rocm/lib/librocprofiler-sdk-roctx.so.1"):
+            try:
+                self.lib = ctypes.CDLL(name)
+                break
+            except OSError:
+                continue
+        if self.lib is not None:
+            for fn in (self.lib.roctxProfilerResume, self.lib.roctxProfilerPause):
+                fn.argtypes = [ctypes.c_uint64]
+                fn.restype = ctypes.c_int
+
+    def resume(self):
+        if self.lib is not None:
+            self.lib.roctxProfilerResume(0)
+
+    def pause(self):
+        """Called after the region's work has completed on the GPU."""
+        if self.lib is not None:
+            self.lib.roctxProfilerPause(0)
+
+
+REGIONS = _ProfilerRegions()
+
+
+def _progress(msg):
+    """A progress line on stderr (stdout carries only the JSON line)."""
+    print(f"bench: {msg}", file=sys.stderr, flush=True)
 
 
 def attn_flops(B, H, S, D):
@@ -108,27 +152,20 @@ def cpu_baseline(B, H, S, D, budget_s):
 
 
 def _time_calls(stream, fn, args, n, what):
-    """Average µs per call of `fn(*args)` over n back-to-back launches on `stream`."""
-    import torch
-    for _ in range(3):
-        if fn(*args) != 0:
-            raise RuntimeError(what)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(n):
-        fn(*args)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    return e0.elapsed_time(e1) / n * 1e3
+    """Average µs per call of `fn(*args)` over n back-to-back launches on
+    `stream` (after 3 untimed ones), inside a profiler region."""
+    return _time_rotating(stream, fn, [args], n, what)
 
 
 def _time_rotating(stream, fn, arglist, n, what):
-    """Average µs per call over n back-to-back launches cycling through arglist."""
+    """Average µs per call over n back-to-back launches cycling through arglist
+    (after 3 untimed ones), inside a profiler region."""
     import torch
-    for a in arglist[:3]:
-        if fn(*a) != 0:
-            raise RuntimeError(what)
+    torch.cuda.synchronize()
+    REGIONS.resume()
+    for i in range(3):
+        if fn(*arglist[i % len(arglist)]) != 0:
+            raise RuntimeError(f"{what}: {fn.__name__} failed")
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(stream)
@@ -136,6 +173,7 @@ def _time_rotating(stream, fn, arglist, n, what):
         fn(*arglist[i % len(arglist)])
     e1.record(stream)
     torch.cuda.synchronize()
+    REGIONS.pause()
     return e0.elapsed_time(e1) / n * 1e3
 
 
@@ -369,13 +407,16 @@ def gpt_train(dev, steps=20, warmup=3):
 
     cfg = GPTConfig()
     losses, tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup)
+    _progress("config 5: kernel train run done")
     _, eager_tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup,
                          attention=eager_attention, loss_fn=SoftmaxCrossEntropy.apply,
                          eager_ops=True)
+    _progress("config 5: eager train run done")
     # parity runs: 20 steps each from the initial parameters
     kern, _ = train(cfg, 8, 1024, steps=20, seed=5, device=dev)
     ref, _ = train(cfg, 8, 1024, steps=20, seed=5, device=dev, attention=eager_attention,
                    rope=eager_rope)
+    _progress("config 5: parity runs 1-2 done")
     rnd, _ = train(cfg, 8, 1024, steps=20, seed=5, device=dev,
                    attention=lambda q, k, v: eager_attention(q, k, v, round_p=True),
                    rope=eager_rope)
@@ -399,8 +440,104 @@ def gpt_train(dev, steps=20, warmup=3):
                 "loss_reference": [round(x, 5) for x in ref]}}
 
 
+def _short_kernel_name(name):
+    """A kernel's demangled name without its return type, namespaces of this
+    library and argument list (template arguments kept)."""
+    name = name.replace("void ", "", 1) if name.startswith("void ") else name
+    name = name.replace("mi::(anonymous namespace)::", "").replace("mi::", "")
+    depth = 0
+    for i, ch in enumerate(name):
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0 and i > 0:
+            return name[:i]
+    return name
+
+
+def summarize(root):
+    """Per-kernel averages from rocprofv3's CSV output under `root` (one or
+    more runs), one line per kernel and grid size:
+      * kernel_trace.csv: dispatch count, mean / min / max duration, the
+        scratch (private segment) bytes per lane, and the back-to-back time per
+        dispatch (over runs of consecutive dispatches of the same kernel and
+        grid: first start to last end / dispatches, i.e. with the dispatch gaps,
+        the way a loop of launches between two events measures it);
+      * kernel_stats.csv rows when there is no trace;
+      * counter_collection.csv: dispatch count and mean / min / max of each
+        counter per dispatch (FETCH_SIZE / WRITE_SIZE are in KiB)."""
+    import csv
+    from collections import defaultdict
+    traces, stats, counters = [], [], []
+    for dirpath, _, files in os.walk(root):
+        for f in sorted(files):
+            path = os.path.join(dirpath, f)
+            if f.endswith("kernel_trace.csv"):
+                traces.append(path)
+            elif f.endswith("kernel_stats.csv"):
+                stats.append(path)
+            elif f.endswith("counter_collection.csv"):
+                counters.append(path)
+
+    def key(row):
+        grid = row.get("Grid_Size_X") or row.get("Grid_Size") or "?"
+        return f"{_short_kernel_name(row['Kernel_Name'])} [grid {grid}]"
+
+    if traces:
+        disp = []
+        for path in traces:
+            for row in csv.DictReader(open(path)):
+                disp.append((int(row["Start_Timestamp"]), int(row["End_Timestamp"]), key(row),
+                             int(row.get("Scratch_Size") or 0)))
+        disp.sort()
+        dur, scratch = defaultdict(list), defaultdict(int)
+        span, span_n = defaultdict(int), defaultdict(int)
+        i = 0
+        while i < len(disp):
+            j = i
+            while j + 1 < len(disp) and disp[j + 1][2] == disp[i][2]:
+                j += 1
+            k = disp[i][2]
+            if j > i:
+                span[k] += disp[j][1] - disp[i][0]
+                span_n[k] += j - i + 1
+            i = j + 1
+        for start, end, k, scr in disp:
+            dur[k].append(end - start)
+            scratch[k] = max(scratch[k], scr)
+        print("| kernel [grid threads] | dispatches | avg µs | min µs | max µs | back-to-back µs "
+              "| scratch B/lane |")
+        print("|---|---|---|---|---|---|---|")
+        for k, d in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
+            b2b = f"{span[k] / span_n[k] / 1e3:.3f}" if span_n[k] else "-"
+            print(f"| {k} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} | {min(d) / 1e3:.3f} "
+                  f"| {max(d) / 1e3:.3f} | {b2b} | {scratch[k]} |")
+    elif stats:
+        for path in stats:
+            print("| kernel | calls | avg µs | min µs | max µs |")
+            print("|---|---|---|---|---|")
+            for r in csv.DictReader(open(path)):
+                print(f"| {_short_kernel_name(r['Name'])} | {r['Calls']} "
+                      f"| {float(r['AverageNs']) / 1e3:.3f} | {float(r['MinNs']) / 1e3:.3f} "
+                      f"| {float(r['MaxNs']) / 1e3:.3f} |")
+    if counters:
+        val = defaultdict(lambda: defaultdict(list))
+        for path in counters:
+            for row in csv.DictReader(open(path)):
+                val[row["Counter_Name"]][key(row)].append(float(row["Counter_Value"]))
+        for counter, per in sorted(val.items()):
+            print(f"\n| kernel [grid threads] | dispatches | {counter} mean | min | max |")
+            print("|---|---|---|---|---|")
+            for k, v in sorted(per.items(), key=lambda kv: -max(kv[1])):
+                print(f"| {k} | {len(v)} | {sum(v) / len(v):.1f} | {min(v):.1f} | {max(v):.1f} |")
+
+
 def main():
     args = parse_args()
+    if args.summarize:
+        summarize(args.summarize)
+        return
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only; --gpus {args.gpus} is not supported "
               "(attention has no cross-GPU exchange: heads and batches shard with no "
@@ -482,20 +619,26 @@ def main():
     t_end.record(stream)
     torch.cuda.synchronize()
     ms_per_step = t_start.elapsed_time(t_end) / args.steps
+    _progress(f"config 2 timed pass: {ms_per_step * 1e3:.1f} us per step")
 
     # Per-kernel durations: each kernel of the step launched K times back to
     # back on its own (its inputs are unchanged, so every launch redoes the same
     # work), with events only at the ends of each run; the intervals hold the
     # K - 1 dispatch gaps between launches, not the events' own overhead.
+    # These K launches of each kernel are the ones a profiler records
+    # (`rocprofv3 --selected-regions`), so its per-dispatch average is the
+    # duration the roofline below divides by, less the K - 1 gaps.
     per_kernel_us = {}
     for name, fn, a in calls:
         k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
+        REGIONS.resume()
         k0.record(stream)
         for _ in range(args.steps):
             fn(*a)
         k1.record(stream)
         torch.cuda.synchronize()
+        REGIONS.pause()
         per_kernel_us[name] = k0.elapsed_time(k1) / args.steps * 1e3
 
     kflops = {"attn_fwd": flops["fwd"], "attn_bwd": flops["bwd"]}
@@ -530,6 +673,8 @@ def main():
         lib.mi_rope_qk(*rope_args)
     r1.record(stream)
     torch.cuda.synchronize()
+    # (outside the profiler regions: a profiler's record of rope_qk is the
+    # HBM-cold pass below, the one the printed roofline is quoted on)
     rope_us = r0.elapsed_time(r1) / n_rope * 1e3
     rope_bytes = 4 * B * S * H * D * 2 + 2 * S * (D // 2) * 2
     rope_gbps = rope_bytes / (rope_us * 1e-6) / 1e9
@@ -548,17 +693,24 @@ def main():
     rope_cold_gbps = rope_bytes / (rope_cold_us * 1e-6) / 1e9
     del qkvs
 
+    _progress("config 2 per-kernel and RoPE passes done")
     model_ops = {} if args.no_model_ops else model_ops_bench(dev, lib)
+    _progress("model operators done")
 
-    if args.calibrate_copy:
-        # 64 Mi fp32 elements: exactly 256 MiB read and 256 MiB written by one
-        # elementwise kernel; its byte counters scale the attention kernels'.
-        src = torch.ones(64 * 1024 * 1024, dtype=torch.float32, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            torch.mul(src, 2.0, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
+    # Reference point for the HBM byte counters: 64 Mi int32 elements, exactly
+    # 256 MiB read and 256 MiB written by one elementwise kernel (torch's
+    # bitwise_not, which nothing else in this run launches, so a profiler can
+    # select it by name), in a profiler region of its own; its FETCH_SIZE /
+    # WRITE_SIZE scale the other kernels'.
+    src = torch.ones(64 * 1024 * 1024, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    REGIONS.resume()
+    for _ in range(3):
+        torch.bitwise_not(src, out=dst)
+    torch.cuda.synchronize()
+    REGIONS.pause()
+    del src, dst
 
     tflops = flops["total"] / (ms_per_step * 1e-3) / 1e12
     out = {
@@ -590,10 +742,12 @@ def main():
             "config3": attn_config_bench(dev, lib, 2, 16, 4096, 128, 3, 0.5, args.steps),
             "config4": attn_config_bench(dev, lib, 1, 32, 8192, 128, 4, 1.0, args.steps)}
         torch.cuda.empty_cache()
+        _progress("configs 3 and 4 done")
     if model_ops:
         out["model_ops"] = model_ops
     if not args.no_gpt:
         out["gpt_train"] = gpt_train(dev)
+        _progress("config 5 train step done")
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(B, H, S, D, args.cpu_seconds)
     print(json.dumps(out), flush=True)

@@ -63,3 +63,32 @@ def test_package_never_imports_oracle():
                 p = os.path.join(dirpath, f)
                 offenders += [(os.path.relpath(p, ROOT), line) for _, line in _oracle_imports(p)]
     assert offenders == []
+
+
+def test_summarize_reads_rocprof_csv(tmp_path):
+    """``bench.py --summarize DIR`` averages rocprofv3's per-dispatch CSV rows
+    per kernel and grid: durations (end - start, ns -> µs), the back-to-back
+    time of consecutive dispatches, scratch bytes and counter values."""
+    d = tmp_path / "host" / "123"
+    d.mkdir(parents=True)
+    (d / "run_kernel_trace.csv").write_text(
+        '"Kind","Kernel_Name","Start_Timestamp","End_Timestamp","Scratch_Size","Grid_Size_X"\n'
+        '"KERNEL_DISPATCH","void mi::(anonymous namespace)::k_bwd<mi::BF16, 64>(mi::AttnArgs, int)",'
+        '1000,56000,0,256\n'
+        '"KERNEL_DISPATCH","void mi::(anonymous namespace)::k_bwd<mi::BF16, 64>(mi::AttnArgs, int)",'
+        '60000,117000,0,256\n'
+        '"KERNEL_DISPATCH","k_fwd",120000,141000,16,512\n')
+    (d / "run_counter_collection.csv").write_text(
+        '"Dispatch_Id","Grid_Size","Kernel_Name","Counter_Name","Counter_Value"\n'
+        '1,256,"void mi::(anonymous namespace)::k_bwd<mi::BF16, 64>(mi::AttnArgs, int)",'
+        '"FETCH_SIZE",100.0\n'
+        '2,256,"void mi::(anonymous namespace)::k_bwd<mi::BF16, 64>(mi::AttnArgs, int)",'
+        '"FETCH_SIZE",102.0\n')
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--summarize",
+                        str(tmp_path)], capture_output=True, text=True, timeout=120)
+    assert r.returncode == 0, r.stderr
+    lines = r.stdout.splitlines()
+    # back-to-back: (117000 - 1000) ns over 2 dispatches
+    assert "| k_bwd<BF16, 64> [grid 256] | 2 | 56.000 | 55.000 | 57.000 | 58.000 | 0 |" in lines
+    assert "| k_fwd [grid 512] | 1 | 21.000 | 21.000 | 21.000 | - | 16 |" in lines
+    assert "| k_bwd<BF16, 64> [grid 256] | 2 | 101.0 | 100.0 | 102.0 |" in lines
