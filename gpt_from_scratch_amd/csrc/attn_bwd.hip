@@ -170,6 +170,34 @@ struct BwdCfg {
 // limit.
 __device__ __forceinline__ int bwd_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
 
+// Per-lane LDS element offsets of the two tile reads: 16-byte row reads (row
+// l%32, chunk 2ks + l/32) and transposing reads (row 4(l/32) + (l%16)/4,
+// column 32db + 16((l/16)%2) + 4(l%4)).  swz < 8 only changes the low three
+// bits of a chunk index, so chunk c + 8 sits 64 elements after chunk c: four
+// row offsets and two transposing offsets (plus immediates) cover every read.
+template <int D>
+struct LdsOffsets {
+  int r4[4], t2[2];
+  __device__ __forceinline__ int row(int ks) const { return r4[ks & 3] + 64 * (ks >> 2); }
+  __device__ __forceinline__ int tr(int db) const { return t2[db & 1] + 64 * (db >> 1); }
+};
+
+template <int D>
+__device__ __forceinline__ LdsOffsets<D> lds_offsets(int lane) {
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+  LdsOffsets<D> o;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) o.r4[ks] = l32 * D + (((2 * ks + g) ^ bwd_swz(l32)) << 3);
+#pragma unroll
+  for (int db = 0; db < 2; ++db) {
+    const int r = 4 * g + ((lane & 15) >> 2);
+    const int ch = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
+    o.t2[db] = r * D + ((ch ^ bwd_swz(r)) << 3) + 4 * (lane & 1);
+  }
+  return o;
+}
+
 struct BwdItem {
   int kind;  // 0: dK/dV, 1: dQ
   int tile;  // key tile (kind 0) or query tile (kind 1), OWN rows each
@@ -221,7 +249,8 @@ __device__ __forceinline__ int first_row(const BwdItem& it) {
   return (CAUSAL && it.kind == 0) ? it.tile * BwdCfg<D>::OWN : 0;
 }
 
-template <int D>
+// SKIP0: leave res.r[0] unloaded (the D = 128 dK/dV kind keeps K in LDS).
+template <int D, bool SKIP0 = false>
 __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& it,
                                               Resident<D>& res) {
   const int lane = threadIdx.x & 63;
@@ -241,7 +270,7 @@ __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& 
     const uint32_t neg = it.kind ? 0u : 0x80008000u;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
-      res.r[0][ks] = __builtin_amdgcn_raw_buffer_load_b128(r0, o0 + 32 * ks, 0, 0);
+      if (!SKIP0) res.r[0][ks] = __builtin_amdgcn_raw_buffer_load_b128(r0, o0 + 32 * ks, 0, 0);
       res.r[1][ks] = __builtin_amdgcn_raw_buffer_load_b128(r1, o1 + 32 * ks, 0, 0) ^ neg;
     }
     if (it.kind) {
@@ -320,6 +349,10 @@ __device__ __forceinline__ void dma_stage(const StageSrc<D>& s, int kind, int ro
 // dO^T and Q^T A operands are read transposed from the same tiles.
 // The dP accumulators start at +delta and the V rows are negated once per
 // item, so they hold delta - dO V^T and dS = -P * acc.
+// At D = 128 the wave's 32 K rows live in LDS (its own 8 KB region, in the
+// tiles' swizzle) rather than in registers: K, -V and the dK and dV
+// accumulators together need ~290 VGPRs, and holding all of them spilled
+// ~390 bytes per lane.  The region then stages the wave's dK and dV stores.
 // ---------------------------------------------------------------------------
 template <typename E, int D, bool CAUSAL>
 __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
@@ -334,18 +367,15 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
   const int kv0 = it.tile * C::OWN;
   const int kw = kv0 + 32 * wave;
   const bool wave_valid = kw < S;
+  const int b = it.bh / a.H;
+  const int h = it.bh % a.H;
+  constexpr bool K_IN_LDS = (D == 128);
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[K_IN_LDS ? C::OWN * D : 8];
+  uint16_t* const kw_lds = k_lds + (K_IN_LDS ? wave * 32 * D : 0);
 
   // per-lane LDS offsets: 16-byte row reads (row l32, chunk 2ks + g) and
   // transposing reads (row 4g + (lane%16)/4, column 32db + 16((lane/16)%2) + 4(lane%4))
-  int rro[C::KS], tro[C::DB];
-#pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) rro[ks] = l32 * D + (((2 * ks + g) ^ bwd_swz(l32)) << 3);
-#pragma unroll
-  for (int db = 0; db < C::DB; ++db) {
-    const int r = 4 * g + ((lane & 15) >> 2);
-    const int ch = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-    tro[db] = r * D + ((ch ^ bwd_swz(r)) << 3) + 4 * (lane & 1);
-  }
+  const LdsOffsets<D> lo = lds_offsets<D>(lane);
 
   const int q_begin = first_row<D, CAUSAL>(it);
   const int nq = (S - q_begin) / C::TILE;
@@ -362,8 +392,22 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
   // First tile's loads before the resident rows: one memory round trip for
   // both (the V negation waits for its rows, not for the tile).
   dma_stage<D>(src, 0, q_begin, bufs[0]);
+  if constexpr (K_IN_LDS) {
+    // the wave's 32 K rows: 8 one-KB slices of 4 rows, lane i writing chunk
+    // position i%16 of row 4m + i/16, i.e. fetching chunk (i%16) ^ swz(row)
+    if (wave_valid) {
+      const auto rk = tile_rsrc(head_ptr(a.k, b, h) + (int64_t)kw * a.k.ss,
+                                rows_extent(32, a.k.ss, D));
+#pragma unroll
+      for (int m = 0; m < 32 * D * 2 / 1024; ++m) {
+        const int r = m * C::RPS + lane / C::CPR;
+        const int col = ((lane % C::CPR) ^ bwd_swz(r)) << 3;
+        buffer_load_lds16(rk, (uint32_t)((r * a.k.ss + col) * 2), kw_lds + m * 512);
+      }
+    }
+  }
   Resident<D> res;
-  load_resident<D>(a, it, res);
+  load_resident<D, K_IN_LDS>(a, it, res);
   const u32x4(&kf)[C::KS] = res.r[0];
   const u32x4(&vn)[C::KS] = res.r[1];  // -V
   __syncthreads();
@@ -378,7 +422,8 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     constexpr bool LAST = decltype(last_tag)::value;
     constexpr int P = decltype(parity)::value;
     const int q0 = q_begin + j * C::TILE;
-    if (!LAST) dma_stage<D>(src, 0, q0 + C::TILE, bufs[P ^ 1]);
+    // (at D = 128 the last step is not peeled: a uniform branch skips its load)
+    if (!LAST && (D == 64 || j + 1 < nq)) dma_stage<D>(src, 0, q0 + C::TILE, bufs[P ^ 1]);
 
     if (wave_valid && (!MASKED || q0 + C::TILE - 1 >= kw)) {
       const uint16_t* Qs = bufs[P].t0;
@@ -400,12 +445,15 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
         }
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
-          const u32x4 qa = *(const u32x4*)(&Qs[32 * qb * D + rro[ks]]);
-          s = E::mfma(qa, kf[ks], s);
+          const u32x4 qa = *(const u32x4*)(&Qs[32 * qb * D + lo.row(ks)]);
+          if constexpr (K_IN_LDS)
+            s = E::mfma(qa, *(const u32x4*)(&kw_lds[lo.row(ks)]), s);
+          else
+            s = E::mfma(qa, kf[ks], s);
         }
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
-          const u32x4 da = *(const u32x4*)(&dOs[32 * qb * D + rro[ks]]);
+          const u32x4 da = *(const u32x4*)(&dOs[32 * qb * D + lo.row(ks)]);
           dp = E::mfma(da, vn[ks], dp);
         }
         const bool diag = MASKED && qbs == kw;
@@ -436,7 +484,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
           for (int db = 0; db < C::DB; ++db) {
-            const int off = (32 * qb + 16 * hh) * D + tro[db];
+            const int off = (32 * qb + 16 * hh) * D + lo.tr(db);
             dv[db] = E::mfma(tr_operand(&dOs[off], D), pb[qb][hh], dv[db]);
             dk[db] = E::mfma(tr_operand(&Qs[off], D), sb[qb][hh], dk[db]);
           }
@@ -459,21 +507,27 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     if (j < j_end) step(j++, masked_tag, std::false_type{}, P0{});
   };
   // nq >= 1: the matrix-core path needs S % 64 == 0.
-  const int n_diag = CAUSAL ? min(nq - 1, C::OWN / C::TILE) : 0;
-  if constexpr (CAUSAL) run(n_diag, std::true_type{});
-  run(nq - 1, std::false_type{});
-  const bool last_masked = CAUSAL && nq - 1 < C::OWN / C::TILE;
-  if (last_masked) {
-    if (j & 1) step(j, std::true_type{}, std::true_type{}, P1{});
-    else step(j, std::true_type{}, std::true_type{}, P0{});
+  if constexpr (D == 128) {
+    // Peeled last steps (four more copies of the step) raised the register
+    // pressure of the whole item past 256 and spilled; here the loop runs to
+    // nq and the step skips the load past the end.
+    if constexpr (CAUSAL) run(min(nq, C::OWN / C::TILE), std::true_type{});
+    run(nq, std::false_type{});
   } else {
-    if (j & 1) step(j, std::false_type{}, std::true_type{}, P1{});
-    else step(j, std::false_type{}, std::true_type{}, P0{});
+    const int n_diag = CAUSAL ? min(nq - 1, C::OWN / C::TILE) : 0;
+    if constexpr (CAUSAL) run(n_diag, std::true_type{});
+    run(nq - 1, std::false_type{});
+    const bool last_masked = CAUSAL && nq - 1 < C::OWN / C::TILE;
+    if (last_masked) {
+      if (j & 1) step(j, std::true_type{}, std::true_type{}, P1{});
+      else step(j, std::true_type{}, std::true_type{}, P0{});
+    } else {
+      if (j & 1) step(j, std::false_type{}, std::true_type{}, P1{});
+      else step(j, std::false_type{}, std::true_type{}, P0{});
+    }
   }
 
   if (!wave_valid) return;
-  const int b = it.bh / a.H;
-  const int h = it.bh % a.H;
   uint16_t* const dk_rows = (uint16_t*)a.dk.ptr + b * a.dk.sb + h * a.dk.sh + (int64_t)kw * a.dk.ss;
   uint16_t* const dv_rows = (uint16_t*)a.dv.ptr + b * a.dv.sb + h * a.dv.sh + (int64_t)kw * a.dv.ss;
   if constexpr (D == 64) {
@@ -483,21 +537,12 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     store_block_rows<E, D>(dk, a.scale, stage, dk_rows, a.dk.ss);
     store_block_rows<E, D>(dv, 1.f, stage, dv_rows, a.dv.ss);
   } else {
-    // D = 128 runs at the register limit; the staged store measured slower
-    // there, so the accumulators go out directly (8 bytes per lane and row).
-    const int l32 = lane & 31;
-#pragma unroll
-    for (int db = 0; db < C::DB; ++db)
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        u32x2 wk, wv;
-        wk[0] = E::pack2(dk[db][4 * jj + 0] * a.scale, dk[db][4 * jj + 1] * a.scale);
-        wk[1] = E::pack2(dk[db][4 * jj + 2] * a.scale, dk[db][4 * jj + 3] * a.scale);
-        wv[0] = E::pack2(dv[db][4 * jj + 0], dv[db][4 * jj + 1]);
-        wv[1] = E::pack2(dv[db][4 * jj + 2], dv[db][4 * jj + 3]);
-        *(u32x2*)(dk_rows + (int64_t)l32 * a.dk.ss + 32 * db + 8 * jj + 4 * g) = wk;
-        *(u32x2*)(dv_rows + (int64_t)l32 * a.dv.ss + 32 * db + 8 * jj + 4 * g) = wv;
-      }
+    // D = 128: the wave's K region (32 x D, its own) is idle after the last
+    // step.  (Written straight from the accumulators instead, 8 bytes per lane
+    // and row, the launch measured the same at configs 3 and 4 and 2% slower
+    // at B8 S1024.)
+    store_block_rows<E, D>(dk, a.scale, kw_lds, dk_rows, a.dk.ss);
+    store_block_rows<E, D>(dv, 1.f, kw_lds, dv_rows, a.dv.ss);
   }
 }
 
@@ -521,15 +566,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   const int qw = q0 + 32 * wave;
   const bool wave_valid = qw < S;
 
-  int rro[C::KS], tro[C::DB];
-#pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) rro[ks] = l32 * D + (((2 * ks + g) ^ bwd_swz(l32)) << 3);
-#pragma unroll
-  for (int db = 0; db < C::DB; ++db) {
-    const int r = 4 * g + ((lane & 15) >> 2);
-    const int ch = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-    tro[db] = r * D + ((ch ^ bwd_swz(r)) << 3) + 4 * (lane & 1);
-  }
+  const LdsOffsets<D> lo = lds_offsets<D>(lane);
 
   const int kv_end = CAUSAL ? min(q0 + C::OWN, S) : S;
   const int nkv = kv_end / C::TILE;
@@ -579,12 +616,12 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
         f32x16 s = f32x16{}, dp = ndl;
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
-          const u32x4 ka = *(const u32x4*)(&Ks[32 * kb * D + rro[ks]]);
+          const u32x4 ka = *(const u32x4*)(&Ks[32 * kb * D + lo.row(ks)]);
           s = E::mfma(ka, qf[ks], s);
         }
 #pragma unroll
         for (int ks = 0; ks < C::KS; ++ks) {
-          const u32x4 va = *(const u32x4*)(&Vs[32 * kb * D + rro[ks]]);
+          const u32x4 va = *(const u32x4*)(&Vs[32 * kb * D + lo.row(ks)]);
           dp = E::mfma(va, df[ks], dp);
         }
         const bool diag = MASKED && kvb == qw;
@@ -607,7 +644,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
           for (int db = 0; db < C::DB; ++db) {
-            const int off = (32 * kb + 16 * hh) * D + tro[db];
+            const int off = (32 * kb + 16 * hh) * D + lo.tr(db);
             acc[db] = E::mfma(tr_operand(&Ks[off], D), sb[kb][hh], acc[db]);
           }
         }
@@ -743,8 +780,8 @@ hipError_t launch_dq_e(const AttnArgs& a, hipStream_t st) {
 }
 
 // D = 128: two launches.  Both kinds sit at the 256-register limit of two waves
-// per SIMD there (the dK/dV kind spills), and one combined launch measured
-// 10-15% slower than the two.
+// per SIMD there, and one combined launch measured 10-15% slower than the two
+// (when the dK/dV kind still held K in registers and spilled).
 template <typename E>
 hipError_t launch_both_e(const AttnArgs& a, hipStream_t st) {
   if (a.D == 64) return launch_both_d<E, 64>(a, st);
