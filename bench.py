@@ -188,7 +188,8 @@ def model_ops_bench(dev, lib):
       * RMSNorm over [8192, 768] bf16 (core/normalization.py:13-25): forward
         reads x and w, writes y and the fp32 rstd; backward reads x, dy, w and
         rstd, writes dx and dw (its [parts, 768] fp32 partials stay in cache
-        and are not counted);
+        and are not counted); the same with the residual add fused in front
+        (core/transformer_layer.py:96, :102; the sum written as well);
       * SwiGLU over [8192, 2 x 3072] bf16 (core/mlp.py:24-28);
       * the optimizer step over the 190,460,160 parameters (core/optimizer.py:79-104)."""
     import torch
@@ -249,7 +250,27 @@ def model_ops_bench(dev, lib):
                      "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
                      "algorithmic_bytes": nbytes, "shape": f"[{rows}, {H}] bf16",
                      "traffic": read_traffic(name, "traffic_model_ops_c5.txt")}
-    del xs, dys, outs
+    # The residual add fused in front (core/transformer_layer.py:96, :102): the
+    # forward reads x and the branch output, writes the sum and y; the backward
+    # reads the sum, dy and the sum's other gradient, writes dx (dw as above).
+    sums = [torch.empty(rows, H, dtype=torch.bfloat16, device=dev) for _ in range(NC)]
+    afwd_args = [(dt, dt, rows, H, 1e-6, P(xs[i]), H, P(dys[i]), H, P(w), P(sums[i]), H,
+                  P(outs[i]), H, P(rstd), sp) for i in range(NC)]
+    abwd_args = [(dt, dt, rows, H, P(xs[i]), H, P(w), P(rstd), P(dys[i]), H,
+                  P(dys[(i + 1) % NC]), H, P(sums[i]), H, P(dw), P(ws), ws.numel(), sp)
+                 for i in range(NC)]
+    for name, fn, arglist, nbytes in (
+            ("rmsnorm_add_fwd", lib.mi_rmsnorm_add_fwd, afwd_args,
+             4 * rows * H * 2 + rows * 4 + H * 2),
+            ("rmsnorm_add_bwd", lib.mi_rmsnorm_add_bwd, abwd_args,
+             4 * rows * H * 2 + rows * 4 + 2 * H * 2)):
+        us = _time_rotating(stream, fn, arglist, 4 * NC, name)
+        gbps = nbytes / (us * 1e-6) / 1e9
+        out[name] = {"bound": "hbm", "avg_us": round(us, 2), "achieved": round(gbps, 1),
+                     "peak": PEAK_HBM_GBPS, "unit": "GB/s", "frac": round(gbps / PEAK_HBM_GBPS, 4),
+                     "algorithmic_bytes": nbytes, "shape": f"[{rows}, {H}] bf16 + residual",
+                     "traffic": read_traffic(name, "traffic_model_ops_c5.txt")}
+    del xs, dys, outs, sums
     torch.cuda.empty_cache()
 
     # SwiGLU on the gate_up projection [8192, 2 * 3072] bf16 (core/mlp.py:24-28):
@@ -412,6 +433,8 @@ def gpt_train(dev, steps=20, warmup=3):
                          attention=eager_attention, loss_fn=SoftmaxCrossEntropy.apply,
                          eager_ops=True)
     _progress("config 5: eager train run done")
+    _, sep_tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup,
+                       fuse_add_norm=False)
     # parity runs: 20 steps each from the initial parameters
     kern, _ = train(cfg, 8, 1024, steps=20, seed=5, device=dev)
     ref, _ = train(cfg, 8, 1024, steps=20, seed=5, device=dev, attention=eager_attention,
@@ -428,6 +451,7 @@ def gpt_train(dev, steps=20, warmup=3):
             "steps": steps, "tokens_per_s": round(tps, 1),
             "ms_per_step": round(8 * 1024 / tps * 1e3, 3),
             "tokens_per_s_eager": round(eager_tps, 1),
+            "tokens_per_s_separate_adds": round(sep_tps, 1),
             "eager": "attention as torch matmul/softmax (fp32 math); loss, RMSNorm, SwiGLU and "
                      "the AdamW step as the reference's eager torch ops",
             "loss_first": round(losses[0], 4), "loss_last": round(losses[-1], 4),

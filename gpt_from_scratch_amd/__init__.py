@@ -10,7 +10,7 @@ from .attention_block import AttentionBlock, attention_block
 from .cross_entropy import (VocabParallelCrossEntropy, _VocabParallelCrossEntropy,
                             vocab_parallel_cross_entropy)
 from .mlp import ParallelMLP, SwiGLU, swiglu
-from .normalization import FusedRMSNorm, RMSNorm, rms_norm
+from .normalization import FusedAddRMSNorm, FusedRMSNorm, RMSNorm, add_rms_norm, rms_norm
 from .optimizer import DistributedOptimizer
 from .flash_attn import FlashAttn, apply_flash_attn, flash_attn_backward, flash_attn_forward
 from .position_embeddings import RotaryEmbedding
@@ -21,6 +21,6 @@ __all__ = [
     "RotaryEmbedding", "RoPE", "RoPEQK", "TritonRoPE", "apply_rope", "apply_rope_qk",
     "AttentionBlock", "attention_block",
     "VocabParallelCrossEntropy", "_VocabParallelCrossEntropy", "vocab_parallel_cross_entropy",
-    "RMSNorm", "FusedRMSNorm", "rms_norm", "SwiGLU", "swiglu", "ParallelMLP",
+    "RMSNorm", "FusedRMSNorm", "rms_norm", "FusedAddRMSNorm", "add_rms_norm", "SwiGLU", "swiglu", "ParallelMLP",
     "DistributedOptimizer",
 ]

@@ -26,7 +26,8 @@ EXPORTED = ("mi_version", "mi_status_str", "mi_last_error", "mi_attn_fwd", "mi_a
             "mi_attn_bwd_preprocess", "mi_attn_bwd_grads", "mi_attn_bwd_dkdv", "mi_attn_bwd_dq",
             "mi_rope", "mi_rope_qk", "mi_xent_fwd", "mi_xent_bwd", "mi_rmsnorm_fwd",
             "mi_rmsnorm_bwd_workspace", "mi_rmsnorm_bwd", "mi_swiglu_fwd", "mi_swiglu_bwd",
-            "mi_adamw_workspace", "mi_grad_sumsq", "mi_adamw_step", "mi_attn_bwd_noalloc")
+            "mi_adamw_workspace", "mi_grad_sumsq", "mi_adamw_step", "mi_attn_bwd_noalloc",
+            "mi_rmsnorm_add_fwd", "mi_rmsnorm_add_bwd")
 
 # B*H*S limit of mi_attn_bwd_noalloc (its static workspace array), include/mi_attn.h
 NOALLOC_MAX_ROWS = 1 << 20
@@ -87,6 +88,11 @@ def _declare(lib):
     lib.mi_rmsnorm_bwd_workspace.argtypes = [i64, i64]
     lib.mi_rmsnorm_bwd.restype = i
     lib.mi_rmsnorm_bwd.argtypes = [i, i, i64, i64, p, i64, p, p, p, i64, p, i64, p, p, i64, p]
+    lib.mi_rmsnorm_add_fwd.restype = i
+    lib.mi_rmsnorm_add_fwd.argtypes = [i, i, i64, i64, f, p, i64, p, i64, p, p, i64, p, i64, p, p]
+    lib.mi_rmsnorm_add_bwd.restype = i
+    lib.mi_rmsnorm_add_bwd.argtypes = [i, i, i64, i64, p, i64, p, p, p, i64, p, i64, p, i64, p,
+                                       p, i64, p]
     lib.mi_swiglu_fwd.restype = i
     lib.mi_swiglu_fwd.argtypes = [i, i64, i64, p, i64, p, i64, p]
     lib.mi_swiglu_bwd.restype = i
@@ -314,6 +320,37 @@ def rmsnorm_bwd(x, weight, rstd, dy, dx, dweight, workspace):
                               _ptr(weight), _ptr(rstd), _ptr(dy), dys, _ptr(dx), dxs,
                               _ptr(dweight), _ptr(workspace), workspace.numel(), _stream(x))
     _check(st, "mi_rmsnorm_bwd")
+
+
+def rmsnorm_add_fwd(x, res, weight, eps: float, sum_out, y, rstd):
+    """Enqueue sum = x + res and the RMSNorm forward over it: sum (x's dtype),
+    y, rstd [rows] fp32."""
+    _require_gpu(x, res, weight, sum_out, y, rstd)
+    rows, xs = _rows(x)
+    rrows, rs = _rows(res)
+    srows, ss = _rows(sum_out)
+    assert rrows == rows and srows == rows and res.dtype == x.dtype == sum_out.dtype
+    _, ys = _rows(y)
+    st = lib().mi_rmsnorm_add_fwd(dtype_code(x), dtype_code(weight), rows, x.shape[-1],
+                                  float(eps), _ptr(x), xs, _ptr(res), rs, _ptr(weight),
+                                  _ptr(sum_out), ss, _ptr(y), ys, _ptr(rstd), _stream(x))
+    _check(st, "mi_rmsnorm_add_fwd")
+
+
+def rmsnorm_add_bwd(sum_in, weight, rstd, dy, dsum, dx, dweight, workspace):
+    """Enqueue the backward of rmsnorm_add_fwd: dx = norm backward over sum_in
+    plus dsum (the gradient of x and of res), dweight [hidden]."""
+    _require_gpu(sum_in, weight, rstd, dy, dsum, dx, dweight, workspace)
+    rows, xs = _rows(sum_in)
+    _, dys = _rows(dy)
+    drows, dss = _rows(dsum)
+    _, dxs = _rows(dx)
+    assert drows == rows and dsum.dtype == sum_in.dtype
+    st = lib().mi_rmsnorm_add_bwd(dtype_code(sum_in), dtype_code(weight), rows,
+                                  sum_in.shape[-1], _ptr(sum_in), xs, _ptr(weight), _ptr(rstd),
+                                  _ptr(dy), dys, _ptr(dsum), dss, _ptr(dx), dxs, _ptr(dweight),
+                                  _ptr(workspace), workspace.numel(), _stream(sum_in))
+    _check(st, "mi_rmsnorm_add_bwd")
 
 
 def swiglu_fwd(gate_up, out):

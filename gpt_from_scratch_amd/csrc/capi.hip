@@ -131,7 +131,7 @@ mi::AttnArgs grad_args(int B, int H, int S, int D, int causal, float scale, cons
 
 extern "C" {
 
-int mi_version(void) { return (2 << 16) | 0; }
+int mi_version(void) { return (2 << 16) | 1; }
 
 const char* mi_status_str(mi_status s) {
   switch (s) {
@@ -487,12 +487,36 @@ static bool rms_vec_ok(int64_t hidden, std::initializer_list<std::pair<const voi
   return true;
 }
 
-mi_status mi_rmsnorm_fwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
-                         float eps, const void* x, int64_t x_row_stride, const void* weight,
-                         void* y, int64_t y_row_stride, float* rstd, void* stream) {
+// A fused residual add's extra operand: `rows` rows of `hidden` x_dtype
+// elements, `stride` apart.
+static mi_status rms_add_operand(const char* name, mi_dtype x_dtype, int64_t hidden,
+                                 const void* p, int64_t stride) {
+  if (!p) return fail(MI_ERR_INVALID_ARGUMENT, "%s: null pointer", name);
+  if (stride < hidden)
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s row stride %lld < hidden %lld", name,
+                (long long)stride, (long long)hidden);
+  if (((uintptr_t)p) % elem_size(x_dtype))
+    return fail(MI_ERR_INVALID_ARGUMENT, "%s: misaligned", name);
+  return MI_OK;
+}
+
+static mi_status rms_fwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                         float eps, const void* x, int64_t x_row_stride, const void* res,
+                         int64_t res_row_stride, const void* weight, void* sum,
+                         int64_t sum_row_stride, void* y, int64_t y_row_stride, float* rstd,
+                         void* stream) {
   mi::RmsArgs a;
   if (mi_status st = rms_common(x_dtype, w_dtype, rows, hidden, x, x_row_stride, weight, a))
     return st;
+  const bool add = res != nullptr || sum != nullptr;
+  if (add) {
+    if (mi_status st = rms_add_operand("residual", x_dtype, hidden, res, res_row_stride)) return st;
+    if (mi_status st = rms_add_operand("sum", x_dtype, hidden, sum, sum_row_stride)) return st;
+    a.res = res;
+    a.res_stride = res_row_stride;
+    a.sum = sum;
+    a.sum_stride = sum_row_stride;
+  }
   if (!(eps >= 0.f) || !std::isfinite(eps))
     return fail(MI_ERR_INVALID_ARGUMENT, "eps must be a finite number >= 0");
   const int y_dtype = w_dtype == MI_F32 ? MI_F32 : x_dtype;
@@ -506,11 +530,31 @@ mi_status mi_rmsnorm_fwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64
   a.y = y;
   a.y_stride = y_row_stride;
   a.rstd = rstd;
-  const bool vec = rms_vec_ok(hidden, {{x, x_row_stride}, {y, y_row_stride}},
-                              {{x, elem_size(x_dtype)}, {y, elem_size(y_dtype)},
-                               {weight, elem_size(w_dtype)}});
+  bool vec = rms_vec_ok(hidden, {{x, x_row_stride}, {y, y_row_stride}},
+                        {{x, elem_size(x_dtype)}, {y, elem_size(y_dtype)},
+                         {weight, elem_size(w_dtype)}});
+  if (add)
+    vec = vec && rms_vec_ok(hidden, {{res, res_row_stride}, {sum, sum_row_stride}},
+                            {{res, elem_size(x_dtype)}, {sum, elem_size(x_dtype)}});
   return launched(mi::launch_rmsnorm_fwd(x_dtype, w_dtype, a, vec, (hipStream_t)stream),
-                  "rmsnorm_fwd");
+                  add ? "rmsnorm_add_fwd" : "rmsnorm_fwd");
+}
+
+mi_status mi_rmsnorm_fwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                         float eps, const void* x, int64_t x_row_stride, const void* weight,
+                         void* y, int64_t y_row_stride, float* rstd, void* stream) {
+  return rms_fwd(x_dtype, w_dtype, rows, hidden, eps, x, x_row_stride, nullptr, 0, weight,
+                 nullptr, 0, y, y_row_stride, rstd, stream);
+}
+
+mi_status mi_rmsnorm_add_fwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                             float eps, const void* x, int64_t x_row_stride, const void* res,
+                             int64_t res_row_stride, const void* weight, void* sum,
+                             int64_t sum_row_stride, void* y, int64_t y_row_stride, float* rstd,
+                             void* stream) {
+  if (!res || !sum) return fail(MI_ERR_INVALID_ARGUMENT, "residual / sum: null pointer");
+  return rms_fwd(x_dtype, w_dtype, rows, hidden, eps, x, x_row_stride, res, res_row_stride,
+                 weight, sum, sum_row_stride, y, y_row_stride, rstd, stream);
 }
 
 int64_t mi_rmsnorm_bwd_workspace(int64_t rows, int64_t hidden) {
@@ -518,14 +562,20 @@ int64_t mi_rmsnorm_bwd_workspace(int64_t rows, int64_t hidden) {
   return mi::rmsnorm_parts(rows) * hidden;
 }
 
-mi_status mi_rmsnorm_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+static mi_status rms_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
                          const void* x, int64_t x_row_stride, const void* weight,
-                         const float* rstd, const void* dy, int64_t dy_row_stride, void* dx,
+                         const float* rstd, const void* dy, int64_t dy_row_stride,
+                         const void* dsum, int64_t dsum_row_stride, void* dx,
                          int64_t dx_row_stride, void* dweight, float* workspace,
                          int64_t workspace_elems, void* stream) {
   mi::RmsArgs a;
   if (mi_status st = rms_common(x_dtype, w_dtype, rows, hidden, x, x_row_stride, weight, a))
     return st;
+  if (dsum) {
+    if (mi_status st = rms_add_operand("dsum", x_dtype, hidden, dsum, dsum_row_stride)) return st;
+    a.dsum = dsum;
+    a.dsum_stride = dsum_row_stride;
+  }
   const int y_dtype = w_dtype == MI_F32 ? MI_F32 : x_dtype;
   if (!rstd || !dy || !dx || !dweight || !workspace)
     return fail(MI_ERR_INVALID_ARGUMENT, "rstd / dy / dx / dweight / workspace: null pointer");
@@ -547,11 +597,35 @@ mi_status mi_rmsnorm_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64
   a.dw = dweight;
   a.partial = workspace;
   a.parts = (int)mi::rmsnorm_parts(rows);
-  const bool vec = rms_vec_ok(hidden, {{x, x_row_stride}, {dy, dy_row_stride}, {dx, dx_row_stride}},
-                              {{x, elem_size(x_dtype)}, {dy, elem_size(y_dtype)},
-                               {dx, elem_size(x_dtype)}, {weight, elem_size(w_dtype)}});
+  bool vec = rms_vec_ok(hidden, {{x, x_row_stride}, {dy, dy_row_stride}, {dx, dx_row_stride}},
+                        {{x, elem_size(x_dtype)}, {dy, elem_size(y_dtype)},
+                         {dx, elem_size(x_dtype)}, {weight, elem_size(w_dtype)}});
+  if (dsum)
+    vec = vec && rms_vec_ok(hidden, {{dsum, dsum_row_stride}}, {{dsum, elem_size(x_dtype)}});
   return launched(mi::launch_rmsnorm_bwd(x_dtype, w_dtype, a, vec, (hipStream_t)stream),
-                  "rmsnorm_bwd");
+                  dsum ? "rmsnorm_add_bwd" : "rmsnorm_bwd");
+}
+
+mi_status mi_rmsnorm_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                         const void* x, int64_t x_row_stride, const void* weight,
+                         const float* rstd, const void* dy, int64_t dy_row_stride, void* dx,
+                         int64_t dx_row_stride, void* dweight, float* workspace,
+                         int64_t workspace_elems, void* stream) {
+  return rms_bwd(x_dtype, w_dtype, rows, hidden, x, x_row_stride, weight, rstd, dy,
+                 dy_row_stride, nullptr, 0, dx, dx_row_stride, dweight, workspace,
+                 workspace_elems, stream);
+}
+
+mi_status mi_rmsnorm_add_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                             const void* sum, int64_t sum_row_stride, const void* weight,
+                             const float* rstd, const void* dy, int64_t dy_row_stride,
+                             const void* dsum, int64_t dsum_row_stride, void* dx,
+                             int64_t dx_row_stride, void* dweight, float* workspace,
+                             int64_t workspace_elems, void* stream) {
+  if (!dsum) return fail(MI_ERR_INVALID_ARGUMENT, "dsum: null pointer");
+  return rms_bwd(x_dtype, w_dtype, rows, hidden, sum, sum_row_stride, weight, rstd, dy,
+                 dy_row_stride, dsum, dsum_row_stride, dx, dx_row_stride, dweight, workspace,
+                 workspace_elems, stream);
 }
 
 static mi_status swiglu_common(mi_dtype dtype, int64_t rows, int64_t inter, const void* gu,

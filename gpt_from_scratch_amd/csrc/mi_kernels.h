@@ -94,6 +94,16 @@ struct RmsArgs {
   void* dw;        // [hidden], w's dtype
   float* partial;  // [parts, hidden] fp32 workspace of the backward
   int parts;
+  // Residual add fused in front (all null otherwise).  Forward: x is the
+  // residual stream, res the branch output; sum = round_x(x + res) is written
+  // and normalised.  Backward: x is that sum and dsum the gradient reaching
+  // the sum from its other use; dx = round_x(round_x(norm's dx) + dsum).
+  const void* res;
+  int64_t res_stride;
+  void* sum;
+  int64_t sum_stride;
+  const void* dsum;
+  int64_t dsum_stride;
 };
 
 // Number of dw partial rows the backward uses for `rows` rows (<= 256).

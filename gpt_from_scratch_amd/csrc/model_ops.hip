@@ -254,6 +254,12 @@ hipError_t launch_xent_bwd(int dtype, const XentArgs& a, hipStream_t st) {
 // parts of each column in a fixed order.  `parts` depends only on the row
 // count, so results are bitwise reproducible across devices.
 //
+// With the residual add fused in front (the two `residual + branch` adds of
+// TransformerLayer.forward, core/transformer_layer.py:91-105, each followed by
+// the next RMSNorm): the forward also reads the branch output, writes the sum
+// round_x(x + res) and normalises it; the backward adds the sum's other
+// gradient to dx, each rounded to x's dtype as autograd's two ops round.
+//
 // Fast path: H % 4 == 0, rows 4-element aligned, H <= 4096 (forward) or 2048
 // (backward).  One wave per row,
 // 4 consecutive elements per lane and chunk (8-byte loads for 16-bit types),
@@ -352,7 +358,7 @@ struct RmsBwdCfg {
   static constexpr bool CACHE_W = C <= 4;
 };
 
-template <int DT, int WDT, int C>
+template <int DT, int WDT, int C, bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_vec_kernel(RmsArgs a) {
   constexpr int YDT = RmsTypes<DT, WDT>::YDT;
   const int lane = threadIdx.x & 63;
@@ -360,21 +366,30 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_vec_kernel(RmsArgs a) {
   if (row >= a.rows) return;  // whole waves only; the kernel has no barrier
   const int nq = (int)(a.hidden / 4);
   const void* xr = row_ptr<DT>(a.x, row, a.x_stride);
-  float v[C][4], w[C][4];
+  const void* rr = ADD ? row_ptr<DT>(a.res, row, a.res_stride) : nullptr;
+  float v[C][4], w[C][4], rv[ADD ? C : 1][4];
   float ss = 0.f;
-  // x and w requested together: one memory round trip before the reduction
+  // x (and the branch) and w requested together: one memory round trip
+  // before the reduction; the whole row is read before any of it is written
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const int q = c * 64 + lane;
     if (q < nq) {
       ld4<DT>(xr, 4 * q, v[c]);
+      if constexpr (ADD) ld4<DT>(rr, 4 * q, rv[c]);
       ld4<WDT>(a.w, 4 * q, w[c]);
     }
   }
+  void* sr = ADD ? row_ptr<DT>(a.sum, row, a.sum_stride) : nullptr;
 #pragma unroll
   for (int c = 0; c < C; ++c) {
     const int q = c * 64 + lane;
     if (q < nq) {
+      if constexpr (ADD) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[c][e] = round_to<DT>(v[c][e] + rv[c][e]);
+        st4<DT>(sr, 4 * q, v[c]);
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) ss = __builtin_fmaf(v[c][e], v[c][e], ss);
     }
@@ -395,7 +410,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_vec_kernel(RmsArgs a) {
   if (lane == 0) a.rstd[row] = r;
 }
 
-template <int DT, int WDT>
+template <int DT, int WDT, bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_fwd_scalar_kernel(RmsArgs a) {
   constexpr int YDT = RmsTypes<DT, WDT>::YDT;
   typedef typename Store<DT>::type T;
@@ -404,10 +419,19 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_scalar_kernel(RmsArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
-  const T* xr = (const T*)a.x + row * a.x_stride;
+  // with ADD, the sum is written in the first pass (each element read, then
+  // written, by one lane) and the second pass reads it back
+  const T* xr = ADD ? (const T*)a.sum + row * a.sum_stride : (const T*)a.x + row * a.x_stride;
   float ss = 0.f;
   for (int64_t j = lane; j < a.hidden; j += 64) {
-    const float v = Store<DT>::ld(xr, j);
+    float v;
+    if constexpr (ADD) {
+      v = round_to<DT>(Store<DT>::ld((const T*)a.x + row * a.x_stride, j) +
+                       Store<DT>::ld((const T*)a.res + row * a.res_stride, j));
+      Store<DT>::st((T*)a.sum + row * a.sum_stride, j, v);
+    } else {
+      v = Store<DT>::ld(xr, j);
+    }
     ss = __builtin_fmaf(v, v, ss);
   }
   ss = wave_sum(ss);
@@ -419,7 +443,7 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_scalar_kernel(RmsArgs a) {
 }
 
 // dx for every row, and this workgroup's partial dw into partial[blockIdx.x].
-template <int DT, int WDT, int C>
+template <int DT, int WDT, int C, bool ADD>
 __global__ __launch_bounds__(64 * RmsBwdCfg<C>::W) void rmsnorm_bwd_vec_kernel(RmsArgs a) {
   constexpr int YDT = RmsTypes<DT, WDT>::YDT;
   constexpr int W = RmsBwdCfg<C>::W;
@@ -445,7 +469,8 @@ __global__ __launch_bounds__(64 * RmsBwdCfg<C>::W) void rmsnorm_bwd_vec_kernel(R
   for (int64_t row = (int64_t)blockIdx.x * W + wave; row < a.rows; row += stride) {
     const void* xr = row_ptr<DT>(a.x, row, a.x_stride);
     const void* dyr = row_ptr<YDT>(a.dy, row, a.dy_stride);
-    float x[C][4], dn[C][4];
+    const void* dsr = ADD ? row_ptr<DT>(a.dsum, row, a.dsum_stride) : nullptr;
+    float x[C][4], dn[C][4], ds[ADD ? C : 1][4];
 #pragma unroll
     for (int c = 0; c < C; ++c) {
       const int q = c * 64 + lane;
@@ -454,6 +479,7 @@ __global__ __launch_bounds__(64 * RmsBwdCfg<C>::W) void rmsnorm_bwd_vec_kernel(R
       if (q < nq) {
         ld4<DT>(xr, 4 * q, x[c]);
         ld4<YDT>(dyr, 4 * q, dn[c]);
+        if constexpr (ADD) ld4<DT>(dsr, 4 * q, ds[c]);
       }
     }
     const float r = a.rstd[row];
@@ -483,7 +509,10 @@ __global__ __launch_bounds__(64 * RmsBwdCfg<C>::W) void rmsnorm_bwd_vec_kernel(R
       if (q < nq) {
         float d[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) d[e] = __builtin_fmaf(r, dn[c][e], -x[c][e] * k);
+        for (int e = 0; e < 4; ++e) {
+          d[e] = __builtin_fmaf(r, dn[c][e], -x[c][e] * k);
+          if constexpr (ADD) d[e] = round_to<DT>(d[e]) + ds[c][e];
+        }
         st4<DT>(dxr, 4 * q, d);
       }
     }
@@ -510,7 +539,7 @@ __global__ __launch_bounds__(64 * RmsBwdCfg<C>::W) void rmsnorm_bwd_vec_kernel(R
   }
 }
 
-template <int DT, int WDT>
+template <int DT, int WDT, bool ADD>
 __global__ __launch_bounds__(256) void rmsnorm_bwd_dx_scalar_kernel(RmsArgs a) {
   constexpr int YDT = RmsTypes<DT, WDT>::YDT;
   typedef typename Store<DT>::type T;
@@ -530,10 +559,13 @@ __global__ __launch_bounds__(256) void rmsnorm_bwd_dx_scalar_kernel(RmsArgs a) {
   const float k = r * r * r * s / (float)a.hidden;
   T* dxr = (T*)a.dx + row * a.dx_stride;
   // every element of the row is read above before any is written below, so
-  // dx may alias dy (same stride)
+  // dx may alias dy (same stride); dsum is read by the lane that then writes
+  // the element, so dx may alias it too
   for (int64_t j = lane; j < a.hidden; j += 64) {
     const float dn = Store<YDT>::ld(dyr, j) * Store<WDT>::ld(wr, j);
-    Store<DT>::st(dxr, j, __builtin_fmaf(r, dn, -Store<DT>::ld(xr, j) * k));
+    float d = __builtin_fmaf(r, dn, -Store<DT>::ld(xr, j) * k);
+    if constexpr (ADD) d = round_to<DT>(d) + Store<DT>::ld((const T*)a.dsum + row * a.dsum_stride, j);
+    Store<DT>::st(dxr, j, d);
   }
 }
 
@@ -582,40 +614,40 @@ __global__ __launch_bounds__(1024) void rmsnorm_dw_reduce_kernel(RmsArgs a) {
 // holds dy and the dw partial in registers, H <= 64 * 4 * 8 (beyond, it spills).
 constexpr int64_t RMS_VEC_FWD_MAX = 4096, RMS_VEC_BWD_MAX = 2048;
 
-template <int DT, int WDT, int C>
+template <int DT, int WDT, int C, bool ADD>
 void launch_rms_vec(bool fwd, const RmsArgs& a, hipStream_t st) {
   if (fwd)
-    hipLaunchKernelGGL((rmsnorm_fwd_vec_kernel<DT, WDT, C>), dim3((unsigned)((a.rows + 3) / 4)),
-                       dim3(256), 0, st, a);
+    hipLaunchKernelGGL((rmsnorm_fwd_vec_kernel<DT, WDT, C, ADD>),
+                       dim3((unsigned)((a.rows + 3) / 4)), dim3(256), 0, st, a);
   else if constexpr (C <= 8)
-    hipLaunchKernelGGL((rmsnorm_bwd_vec_kernel<DT, WDT, C>), dim3((unsigned)a.parts),
+    hipLaunchKernelGGL((rmsnorm_bwd_vec_kernel<DT, WDT, C, ADD>), dim3((unsigned)a.parts),
                        dim3(64 * RmsBwdCfg<C>::W), 0, st, a);
 }
 
-template <int DT, int WDT>
+template <int DT, int WDT, bool ADD>
 hipError_t launch_rms_dt(bool fwd, const RmsArgs& a, bool vec, hipStream_t st) {
   const int64_t nq = a.hidden / 4;
   if (a.hidden > (fwd ? RMS_VEC_FWD_MAX : RMS_VEC_BWD_MAX)) vec = false;
   if (vec) {
     // smallest instantiated chunk count covering the row
-    if (nq <= 64) launch_rms_vec<DT, WDT, 1>(fwd, a, st);
-    else if (nq <= 128) launch_rms_vec<DT, WDT, 2>(fwd, a, st);
-    else if (nq <= 192) launch_rms_vec<DT, WDT, 3>(fwd, a, st);
-    else if (nq <= 256) launch_rms_vec<DT, WDT, 4>(fwd, a, st);
-    else if (nq <= 384) launch_rms_vec<DT, WDT, 6>(fwd, a, st);
-    else if (nq <= 512) launch_rms_vec<DT, WDT, 8>(fwd, a, st);
-    else if (nq <= 768) launch_rms_vec<DT, WDT, 12>(fwd, a, st);
-    else launch_rms_vec<DT, WDT, 16>(fwd, a, st);
+    if (nq <= 64) launch_rms_vec<DT, WDT, 1, ADD>(fwd, a, st);
+    else if (nq <= 128) launch_rms_vec<DT, WDT, 2, ADD>(fwd, a, st);
+    else if (nq <= 192) launch_rms_vec<DT, WDT, 3, ADD>(fwd, a, st);
+    else if (nq <= 256) launch_rms_vec<DT, WDT, 4, ADD>(fwd, a, st);
+    else if (nq <= 384) launch_rms_vec<DT, WDT, 6, ADD>(fwd, a, st);
+    else if (nq <= 512) launch_rms_vec<DT, WDT, 8, ADD>(fwd, a, st);
+    else if (nq <= 768) launch_rms_vec<DT, WDT, 12, ADD>(fwd, a, st);
+    else launch_rms_vec<DT, WDT, 16, ADD>(fwd, a, st);
   } else if (fwd) {
-    hipLaunchKernelGGL((rmsnorm_fwd_scalar_kernel<DT, WDT>), dim3((unsigned)((a.rows + 3) / 4)),
-                       dim3(256), 0, st, a);
+    hipLaunchKernelGGL((rmsnorm_fwd_scalar_kernel<DT, WDT, ADD>),
+                       dim3((unsigned)((a.rows + 3) / 4)), dim3(256), 0, st, a);
   } else {
     // dw partials first: dx may overwrite dy
     const int64_t rpp = (a.rows + a.parts - 1) / a.parts;
     hipLaunchKernelGGL((rmsnorm_dw_partial_scalar_kernel<DT, WDT>),
                        dim3((unsigned)((a.hidden + 255) / 256), (unsigned)a.parts), dim3(256), 0,
                        st, a, rpp);
-    hipLaunchKernelGGL((rmsnorm_bwd_dx_scalar_kernel<DT, WDT>),
+    hipLaunchKernelGGL((rmsnorm_bwd_dx_scalar_kernel<DT, WDT, ADD>),
                        dim3((unsigned)((a.rows + 3) / 4)), dim3(256), 0, st, a);
   }
   if (!fwd)
@@ -624,13 +656,21 @@ hipError_t launch_rms_dt(bool fwd, const RmsArgs& a, bool vec, hipStream_t st) {
   return hipGetLastError();
 }
 
+template <bool ADD>
+hipError_t launch_rms_add(bool fwd, int x_dtype, int w_dtype, const RmsArgs& a, bool vec,
+                          hipStream_t st) {
+  if (x_dtype == 2 && w_dtype == 2) return launch_rms_dt<2, 2, ADD>(fwd, a, vec, st);
+  if (x_dtype == 2 && w_dtype == 0) return launch_rms_dt<2, 0, ADD>(fwd, a, vec, st);
+  if (x_dtype == 1 && w_dtype == 1) return launch_rms_dt<1, 1, ADD>(fwd, a, vec, st);
+  if (x_dtype == 1 && w_dtype == 0) return launch_rms_dt<1, 0, ADD>(fwd, a, vec, st);
+  return launch_rms_dt<0, 0, ADD>(fwd, a, vec, st);
+}
+
 hipError_t launch_rms(bool fwd, int x_dtype, int w_dtype, const RmsArgs& a, bool vec,
                       hipStream_t st) {
-  if (x_dtype == 2 && w_dtype == 2) return launch_rms_dt<2, 2>(fwd, a, vec, st);
-  if (x_dtype == 2 && w_dtype == 0) return launch_rms_dt<2, 0>(fwd, a, vec, st);
-  if (x_dtype == 1 && w_dtype == 1) return launch_rms_dt<1, 1>(fwd, a, vec, st);
-  if (x_dtype == 1 && w_dtype == 0) return launch_rms_dt<1, 0>(fwd, a, vec, st);
-  return launch_rms_dt<0, 0>(fwd, a, vec, st);
+  const bool add = fwd ? a.res != nullptr : a.dsum != nullptr;
+  return add ? launch_rms_add<true>(fwd, x_dtype, w_dtype, a, vec, st)
+             : launch_rms_add<false>(fwd, x_dtype, w_dtype, a, vec, st);
 }
 
 }  // namespace

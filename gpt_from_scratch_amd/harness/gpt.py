@@ -48,7 +48,7 @@ import torch.nn.functional as F
 from ..attention_block import attention_block
 from ..cross_entropy import vocab_parallel_cross_entropy
 from ..mlp import swiglu
-from ..normalization import rms_norm
+from ..normalization import add_rms_norm, rms_norm
 from ..optimizer import DistributedOptimizer
 from ..flash_attn import apply_flash_attn
 from ..position_embeddings import RotaryEmbedding
@@ -155,7 +155,8 @@ class Block(nn.Module):
 class GPT(nn.Module):
     """input ids [B, S] -> logits [S, B, V]."""
 
-    def __init__(self, cfg: GPTConfig, device, attention=None, rope=None, eager_ops=False):
+    def __init__(self, cfg: GPTConfig, device, attention=None, rope=None, eager_ops=False,
+                 fuse_add_norm=True):
         super().__init__()
         self.cfg = cfg
         emb = torch.empty(cfg.vocab_size, cfg.hidden_size, device=device, dtype=torch.float32)
@@ -165,12 +166,24 @@ class GPT(nn.Module):
             [Block(cfg, device, attention, rope, eager_ops) for _ in range(cfg.num_layers)])
         self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager=eager_ops)
         self.head = _xavier(cfg.vocab_size, cfg.hidden_size, device)
+        self.eager_ops = eager_ops
+        self.fuse_add_norm = fuse_add_norm and not eager_ops
 
     def forward(self, ids):
         x = F.embedding(ids, self.embedding).transpose(0, 1).contiguous()  # [S, B, H]
-        for blk in self.blocks:
-            x = blk(x)
-        return F.linear(self.norm(x), self.head)
+        if not self.fuse_add_norm:
+            for blk in self.blocks:
+                x = blk(x)
+            return F.linear(self.norm(x), self.head)
+        # The same blocks with each residual add fused into the RMSNorm that
+        # reads its sum: this block's norm2, then the next block's norm1 (or
+        # the final norm); `h` is the normalised input of the next branch.
+        h = self.blocks[0].norm1(x)
+        for i, blk in enumerate(self.blocks):
+            x, h = add_rms_norm(x, blk.attn(h), blk.norm2.weight, blk.norm2.eps)
+            nxt = self.blocks[i + 1].norm1 if i + 1 < len(self.blocks) else self.norm
+            x, h = add_rms_norm(x, blk.mlp(h), nxt.weight, nxt.eps)
+        return F.linear(h, self.head)
 
 
 class SoftmaxCrossEntropy(torch.autograd.Function):
@@ -246,16 +259,17 @@ def synthetic_batch(batch, seq, vocab, seed, device):
 
 
 def train(cfg: GPTConfig, batch=8, seq=1024, steps=20, seed=5, device="cuda", attention=None,
-          rope=None, warmup=0, loss_fn=None, eager_ops=False):
+          rope=None, warmup=0, loss_fn=None, eager_ops=False, fuse_add_norm=True):
     """Build the model and optimizer from `seed`, run `warmup` untimed then
     `steps` timed train steps on one fixed synthetic batch.  Returns
     (losses, tokens_per_second).  `loss_fn(logits, target)` -> per-token loss
     defaults to the HIP cross entropy; `eager_ops` swaps the model's other HIP
     operators (RMSNorm, SwiGLU, the optimizer step) for the reference's eager
-    op sequences."""
+    op sequences; `fuse_add_norm=False` runs the residual adds as separate
+    torch adds in front of the RMSNorm kernels."""
     loss_fn = loss_fn or vocab_parallel_cross_entropy
     torch.manual_seed(seed)
-    model = GPT(cfg, device, attention, rope, eager_ops)
+    model = GPT(cfg, device, attention, rope, eager_ops, fuse_add_norm)
     if eager_ops:
         opt = MixedPrecisionAdamW(model)
     else:

@@ -74,6 +74,71 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.
     return FusedRMSNorm.apply(x, weight, eps)
 
 
+def _norm_weight(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
+    """The weight in the dtype the kernels take for x: x's own or fp32 (any
+    other pairing promotes both to fp32, as ``x.to(dtype) * weight`` does)."""
+    w = weight
+    if w.dtype != x.dtype and w.dtype != torch.float32:
+        w = w.float()
+    if x.dtype == torch.float32 and w.dtype != torch.float32:
+        w = w.float()
+    return w.contiguous()
+
+
+class FusedAddRMSNorm(torch.autograd.Function):
+    """(s, y) = (x + res, RMSNorm(x + res)): the residual add of
+    core/transformer_layer.py:96 / :102 and the RMSNorm that follows it
+    (core/normalization.py:13-25) in one kernel each way.  s is rounded to x's
+    dtype as torch's add rounds it; the backward adds the gradient of s to the
+    norm's dx, rounding each as autograd's two ops do, and returns that sum as
+    the gradient of both x and res."""
+
+    @staticmethod
+    def forward(ctx, x: torch.Tensor, res: torch.Tensor, weight: torch.Tensor, eps: float):
+        if weight.dim() != 1 or x.shape[-1] != weight.shape[0]:
+            raise ValueError(f"weight {tuple(weight.shape)} does not match the last dim of x "
+                             f"{tuple(x.shape)}")
+        if res.shape != x.shape or res.dtype != x.dtype:
+            raise ValueError(f"res {res.dtype} {tuple(res.shape)} must match x {x.dtype} "
+                             f"{tuple(x.shape)}")
+        _lib._require_gpu(x, res, weight)
+        w = _norm_weight(x, weight)
+        xr, rr = _rows_view(x), _rows_view(res)
+        s = torch.empty(x.shape, dtype=x.dtype, device=x.device)
+        y = torch.empty(x.shape, dtype=w.dtype if w.dtype == torch.float32 else x.dtype,
+                        device=x.device)
+        rstd = torch.empty(x.shape[:-1], dtype=torch.float32, device=x.device)
+        _lib.rmsnorm_add_fwd(xr, rr, w, eps, s, y, rstd)
+        ctx.save_for_backward(s, w, rstd)
+        ctx.weight_dtype = weight.dtype
+        ctx.set_materialize_grads(False)
+        return s, y
+
+    @staticmethod
+    def backward(ctx, ds, dy):
+        s, w, rstd = ctx.saved_tensors
+        if dy is None:  # only the sum is used: the norm contributes nothing
+            dx = ds.to(s.dtype)
+            return dx, dx, torch.zeros(w.shape, dtype=ctx.weight_dtype, device=w.device), None
+        dy = _rows_view(dy)
+        rows = rstd.numel()
+        dx = torch.empty(s.shape, dtype=s.dtype, device=s.device)
+        dw = torch.empty(w.shape, dtype=w.dtype, device=w.device)
+        ws = torch.empty(_lib.rmsnorm_workspace(rows, s.shape[-1]), dtype=torch.float32,
+                         device=s.device)
+        if ds is None:  # only the normalised output is used (e.g. after the last add)
+            _lib.rmsnorm_bwd(s, w, rstd, dy, dx, dw, ws)
+        else:
+            ds = _rows_view(ds.to(s.dtype))
+            _lib.rmsnorm_add_bwd(s, w, rstd, dy, ds, dx, dw, ws)
+        return dx, dx, dw.to(ctx.weight_dtype), None
+
+
+def add_rms_norm(x: torch.Tensor, res: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6):
+    """``s = x + res; return s, RMSNorm(s)`` in one kernel (and one backward)."""
+    return FusedAddRMSNorm.apply(x, res, weight, eps)
+
+
 class RMSNorm(nn.Module):
     """RMSNorm(hidden_size, eps=1e-6) with an fp32 weight of ones, as
     core/normalization.py:8-11 (on the current GPU unless `device` is given)."""

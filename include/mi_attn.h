@@ -257,6 +257,38 @@ mi_status mi_rmsnorm_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64
                          int64_t workspace_elems, void* stream);
 
 /*
+ * RMSNorm with the residual add in front: the `residual + branch` of
+ * TransformerLayer.forward (core/transformer_layer.py:96, :102) followed by the
+ * RMSNorm that reads the sum (the next post_attention_norm / input_norm, or the
+ * final norm), core/normalization.py:13-25.  Writes
+ *   sum = round_x(x + res)          (x's dtype: torch's add of two such tensors)
+ * and y, rstd of mi_rmsnorm_fwd over sum.  x (the residual stream), res (the
+ * branch output) and sum have x's dtype; sum may alias x or res (each row is
+ * read whole before any of it is written).
+ */
+mi_status mi_rmsnorm_add_fwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                             float eps, const void* x, int64_t x_row_stride, const void* res,
+                             int64_t res_row_stride, const void* weight, void* sum,
+                             int64_t sum_row_stride, void* y, int64_t y_row_stride, float* rstd,
+                             void* stream);
+
+/*
+ * Backward of mi_rmsnorm_add_fwd: mi_rmsnorm_bwd over `sum` (the forward's
+ * output, in place of x) with the gradient `dsum` that reaches the sum from its
+ * other use added to dx:
+ *   dx = round_x(round_x(r dn - sum r^3 mean(dn * sum)) + dsum),
+ * the two roundings of autograd's norm backward and gradient accumulation.
+ * dx is the gradient of both x and res.  dx may alias dsum, or dy under the
+ * condition of mi_rmsnorm_bwd.  workspace as mi_rmsnorm_bwd.
+ */
+mi_status mi_rmsnorm_add_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                             const void* sum, int64_t sum_row_stride, const void* weight,
+                             const float* rstd, const void* dy, int64_t dy_row_stride,
+                             const void* dsum, int64_t dsum_row_stride, void* dx,
+                             int64_t dx_row_stride, void* dweight, float* workspace,
+                             int64_t workspace_elems, void* stream);
+
+/*
  * SwiGLU on the fused gate_up projection: rows of 2*inter elements, gate in
  * columns [0, inter), up in [inter, 2*inter).  Replaces
  * `gate, up = gate_up.chunk(2, dim=-1); x = F.silu(gate) * up`,

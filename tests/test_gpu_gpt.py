@@ -67,3 +67,15 @@ def test_config5_end_to_end_eager_ops(gpu):
     diffs = [abs(a - b) for a, b in zip(kern, ref)]
     print(f"config5 tokens/s kernels {tps:.0f} eager {ref_tps:.0f}; max |dloss| {max(diffs):.5f}")
     assert max(diffs) < 0.05, diffs
+
+
+def test_config5_fused_add_norm_matches_separate_ops(gpu):
+    """The residual adds fused into the RMSNorms that read their sums give the
+    same losses, bit for bit, as separate torch adds in front of the RMSNorm
+    kernels (the same roundings in both directions)."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    cfg = GPTConfig()
+    fused, tps_f = train(cfg, batch=8, seq=1024, steps=4, seed=5, device=gpu)
+    sep, tps_s = train(cfg, batch=8, seq=1024, steps=4, seed=5, device=gpu, fuse_add_norm=False)
+    print(f"config5 tokens/s fused add+norm {tps_f:.0f}, separate adds {tps_s:.0f}")
+    assert fused == sep, (fused, sep)

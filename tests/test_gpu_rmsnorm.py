@@ -180,3 +180,107 @@ def test_row_broadcast_gradient(gpu):
     # the same broadcast tensor as a forward input
     y = rms_norm(x[:1].expand(rows, H), w, EPS)
     _check_forward(y, x[:1].expand(rows, H).contiguous(), w, EPS)
+
+
+def _add_norm_composition(x, r, w, ds, dy, eps=EPS):
+    """The reference's op pair on the same kernels: s = x + r (torch's add), y =
+    RMSNorm(s); autograd accumulates s's two gradients (ds and the norm's dx)."""
+    from gpt_from_scratch_amd import rms_norm
+    xg, rg, wg = (t.detach().clone().requires_grad_(True) for t in (x, r, w))
+    s = xg + rg
+    y = rms_norm(s, wg, eps)
+    torch.autograd.backward([s, y], [ds, dy])
+    return s.detach(), y.detach(), xg.grad, rg.grad, wg.grad
+
+
+def _add_norm_fused(x, r, w, ds, dy, eps=EPS):
+    from gpt_from_scratch_amd import add_rms_norm
+    xg, rg, wg = (t.detach().clone().requires_grad_(True) for t in (x, r, w))
+    s, y = add_rms_norm(xg, rg, wg, eps)
+    torch.autograd.backward([s, y], [ds, dy])
+    return s.detach(), y.detach(), xg.grad, rg.grad, wg.grad
+
+
+@pytest.mark.parametrize("xd,wd", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                   (torch.float32, torch.float32), (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("rows,H,pad", [(37, 768, 0), (19, 64, 0), (6, 3072, 0), (3, 5000, 0),
+                                        (21, 7, 0), (29, 768, 1)])
+def test_add_norm_matches_composition_and_oracle(gpu, xd, wd, rows, H, pad):
+    """mi_rmsnorm_add_fwd / _bwd against the two-op composition on the same
+    kernels (torch's add, then the RMSNorm kernels; autograd's accumulation of
+    the sum's gradients): the sum, y, both input gradients and dw bit for bit,
+    on the vector path and (H = 7, 5000, or rows padded by one element) the
+    scalar path.  y and the gradients also against the float64 oracle over the
+    rounded sum, within the RMSNorm bounds plus the accumulation's rounding."""
+    wide = seeded((rows, H + pad), 400 + H, std=1.5, dtype=xd).to(gpu)
+    x = wide[:, :H]
+    r = seeded((rows, H), 401 + H, std=0.7, dtype=xd).to(gpu)
+    w = (1.0 + 0.1 * seeded((H,), 402 + H, dtype=torch.float32)).to(wd).to(gpu)
+    yd = torch.float32 if wd == torch.float32 else xd
+    dy = seeded((rows, H), 403 + H, dtype=yd).to(gpu)
+    ds = seeded((rows, H), 404 + H, std=0.5, dtype=xd).to(gpu)
+    fs, fy, fdx, fdr, fdw = _add_norm_fused(x, r, w, ds, dy)
+    cs, cy, cdx, cdr, cdw = _add_norm_composition(x, r, w, ds, dy)
+    torch.cuda.synchronize()
+    assert fs.dtype == xd and fy.dtype == yd and fdx.dtype == xd and fdw.dtype == wd
+    for name, a, b in (("sum", fs, cs), ("y", fy, cy), ("dx", fdx, cdx), ("dres", fdr, cdr),
+                       ("dw", fdw, cdw)):
+        assert torch.equal(a, b), (name, float((a.float() - b.float()).abs().max()))
+    # the oracle over the rounded sum: y as RMSNorm's forward; dx - ds as its backward
+    _check_forward(fy, fs, w, EPS)
+    s64 = _np(fs)
+    rdx, _ = rmsnorm_backward(s64, _np(w), _np(dy), EPS, x_dtype=xd)
+    want = rdx + _np(ds)
+    got = _np(fdx)
+    u = U[xd]
+    bound = (np.abs(rdx) + np.abs(want)) * (u + 1e-5) + 1e-5 * np.abs(rdx).max() + 1e-30
+    assert (np.abs(got - want) <= bound).all(), np.abs(got - want).max()
+
+
+def test_add_norm_in_place_and_model_stack(gpu):
+    """The sum written over x (the residual stream updated in place) equals the
+    out-of-place result; and a stack of blocks whose residual adds are fused
+    into the following norms gives the same loss and parameter gradients, bit
+    for bit, as the same stack with separate adds and norms (the model's
+    layout [S, B, H], bf16 weights)."""
+    from gpt_from_scratch_amd import _lib, add_rms_norm, rms_norm
+    S, B, H = 128, 4, 768
+    x = seeded((S, B, H), 601, dtype=torch.bfloat16).to(gpu)
+    r = seeded((S, B, H), 602, dtype=torch.bfloat16).to(gpu)
+    w = (1 + 0.1 * seeded((H,), 603, dtype=torch.float32)).to(torch.bfloat16).to(gpu)
+    s, y = torch.empty_like(x), torch.empty_like(x)
+    rstd = torch.empty(S, B, dtype=torch.float32, device=gpu)
+    _lib.rmsnorm_add_fwd(x, r, w, EPS, s, y, rstd)
+    xi = x.clone()
+    y2, rstd2 = torch.empty_like(x), torch.empty_like(rstd)
+    _lib.rmsnorm_add_fwd(xi, r, w, EPS, xi, y2, rstd2)
+    assert torch.equal(xi, s) and torch.equal(y2, y) and torch.equal(rstd2, rstd)
+
+    torch.manual_seed(7)
+    ws = [(1 + 0.1 * torch.randn(H, device=gpu)).to(torch.bfloat16) for _ in range(5)]
+    mats = [(0.02 * torch.randn(H, H, device=gpu)).to(torch.bfloat16) for _ in range(4)]
+
+    def run(fused):
+        wp = [t.clone().requires_grad_(True) for t in ws]
+        mp = [t.clone().requires_grad_(True) for t in mats]
+        h0 = x.clone().requires_grad_(True)
+        if fused:
+            h = rms_norm(h0, wp[0], EPS)
+            xs = h0
+            for i in range(4):
+                xs, h = add_rms_norm(xs, torch.tanh(h @ mp[i]), wp[i + 1], EPS)
+        else:
+            xs = h0
+            h = rms_norm(xs, wp[0], EPS)
+            for i in range(4):
+                xs = xs + torch.tanh(h @ mp[i])
+                h = rms_norm(xs, wp[i + 1], EPS)
+        loss = (h.float() ** 2).mean()
+        loss.backward()
+        return loss.detach(), h0.grad, [t.grad for t in wp + mp]
+
+    l1, g1, p1 = run(True)
+    l2, g2, p2 = run(False)
+    assert torch.equal(l1, l2) and torch.equal(g1, g2)
+    for a, b in zip(p1, p2):
+        assert torch.equal(a, b)
