@@ -27,7 +27,7 @@ EXPORTED = ("mi_version", "mi_status_str", "mi_last_error", "mi_attn_fwd", "mi_a
             "mi_rope", "mi_rope_qk", "mi_xent_fwd", "mi_xent_bwd", "mi_rmsnorm_fwd",
             "mi_rmsnorm_bwd_workspace", "mi_rmsnorm_bwd", "mi_swiglu_fwd", "mi_swiglu_bwd",
             "mi_adamw_workspace", "mi_grad_sumsq", "mi_adamw_step", "mi_attn_bwd_noalloc",
-            "mi_rmsnorm_add_fwd", "mi_rmsnorm_add_bwd")
+            "mi_rmsnorm_add_fwd", "mi_rmsnorm_add_bwd", "mi_attn_bwd_rope")
 
 # B*H*S limit of mi_attn_bwd_noalloc (its static workspace array), include/mi_attn.h
 NOALLOC_MAX_ROWS = 1 << 20
@@ -57,6 +57,10 @@ def _declare(lib):
     lib.mi_attn_bwd.argtypes = [i, i, i, i, i, i, f,
                                 p, i64p, p, i64p, p, i64p, p, i64p, p, i64p,
                                 p, p, p, i64p, p, i64p, p, i64p, p]
+    lib.mi_attn_bwd_rope.restype = i
+    lib.mi_attn_bwd_rope.argtypes = [i, i, i, i, i, i, f,
+                                     p, i64p, p, i64p, p, i64p, p, i64p, p, i64p,
+                                     p, p, p, i64p, p, i64p, p, i64p, i, p, i64p, p, i64p, p]
     lib.mi_attn_bwd_noalloc.restype = i
     lib.mi_attn_bwd_noalloc.argtypes = [i, i, i, i, i, i, f,
                                         p, i64p, p, i64p, p, i64p, p, i64p, p, i64p,
@@ -237,6 +241,23 @@ def rope(x, cos, sin, out, inverse: bool):
                        _ptr(x), _strides(x, 4), _ptr(cos), _strides(cos, 2),
                        _ptr(sin), _strides(sin, 2), _ptr(out), _strides(out, 4), _stream(x))
     _check(st, "mi_rope")
+
+
+def attn_bwd_rope(q, k, v, o, do, lse, ws, dq, dk, dv, causal: bool, scale: float, cos, sin):
+    """attn_bwd with dq and dk inverse-rotated by the RoPE tables cos / sin
+    ([>= S, D/2]): the gradients with respect to the unrotated q, k."""
+    _check_attn_tensors(q, (("k", k), ("v", v), ("o", o), ("do", do), ("dq", dq), ("dk", dk),
+                            ("dv", dv)), (("lse", lse),), ws)
+    _require_gpu(q, k, v, o, do, lse, ws, dq, dk, dv, cos, sin)
+    B, H, S, D = q.shape
+    st = lib().mi_attn_bwd_rope(dtype_code(q), B, H, S, D, int(bool(causal)), float(scale),
+                                _ptr(q), _strides(q, 4), _ptr(k), _strides(k, 4),
+                                _ptr(v), _strides(v, 4), _ptr(o), _strides(o, 4),
+                                _ptr(do), _strides(do, 4), _ptr(lse), _ptr(ws),
+                                _ptr(dq), _strides(dq, 4), _ptr(dk), _strides(dk, 4),
+                                _ptr(dv), _strides(dv, 4), dtype_code(cos), _ptr(cos),
+                                _strides(cos, 2), _ptr(sin), _strides(sin, 2), _stream(q))
+    _check(st, "mi_attn_bwd_rope")
 
 
 def rope_qk(q, k, cos, sin, q_out, k_out, inverse: bool):

@@ -17,12 +17,13 @@ relayout copies, because every kernel here takes arbitrary strides:
 * the forward writes ``O`` straight into ``[S, B, H, D]``, so the result is a
   free ``[S, B, H*D]`` view;
 * the backward writes dQ, dK and dV straight into the slots of one
-  ``[S, B, 3, H, D]`` gradient buffer, and the inverse rotation of dQ and dK
-  runs in place there (each lane reads its pairs before it writes them).
+  ``[S, B, 3, H, D]`` gradient buffer, dQ and dK inverse-rotated by the
+  attention kernels as they store them (no separate RoPE pass).
 
 Results are bit-identical to ``apply_rope_qk`` followed by
-``apply_flash_attn`` and the reshape: the same kernels do the same arithmetic,
-only the addresses differ.
+``apply_flash_attn`` and the reshape: the same arithmetic in the same order
+(the rotation fused into the backward's stores is the RoPE kernel's, applied
+to the same rounded gradients); only the addresses differ.
 """
 from __future__ import annotations
 
@@ -81,11 +82,11 @@ class AttentionBlock(torch.autograd.Function):
         d_qkv = torch.empty((S, B, 3, heads, D), dtype=qkv5.dtype, device=qkv5.device)
         ws = _lib.bwd_workspace(lse)
         dq, dk, dv = d_qkv[:, :, 0], d_qkv[:, :, 1], d_qkv[:, :, 2]
-        _lib.attn_bwd(rot[:, :, 0].permute(bhsd), rot[:, :, 1].permute(bhsd),
-                      qkv5[:, :, 2].permute(bhsd), o.permute(bhsd), d_o.permute(bhsd), lse, ws,
-                      dq.permute(bhsd), dk.permute(bhsd), dv.permute(bhsd), causal, scale)
-        # gradients of the rotated q, k -> gradients of q, k: inverse rotation in place
-        _lib.rope_qk(dq, dk, cos, sin, dq, dk, inverse=True)
+        # dq, dk leave inverse-rotated: the gradients of q, k themselves
+        _lib.attn_bwd_rope(rot[:, :, 0].permute(bhsd), rot[:, :, 1].permute(bhsd),
+                           qkv5[:, :, 2].permute(bhsd), o.permute(bhsd), d_o.permute(bhsd), lse,
+                           ws, dq.permute(bhsd), dk.permute(bhsd), dv.permute(bhsd), causal,
+                           scale, cos, sin)
         return d_qkv.view(S, B, 3 * heads * D), None, None, None, None
 
 

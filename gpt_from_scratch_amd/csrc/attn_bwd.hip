@@ -198,6 +198,95 @@ __device__ __forceinline__ LdsOffsets<D> lds_offsets(int lane) {
   return o;
 }
 
+// The four angles i0 .. i0+3 of table row `pos` (contiguous angles, dtype
+// TDT: 0 fp32, 1 fp16, 2 bf16) with one vector load, kept packed until used.
+template <int TDT>
+struct Tab4 {
+  typedef typename std::conditional<TDT == 0, f32x4, u32x2>::type type;
+  static __device__ __forceinline__ type load(const void* tab, int64_t row_stride, int64_t pos,
+                                              int i0) {
+    if constexpr (TDT == 0)
+      return *(const f32x4*)((const float*)tab + pos * row_stride + i0);
+    else
+      return *(const u32x2*)((const uint16_t*)tab + pos * row_stride + i0);
+  }
+  static __device__ __forceinline__ float get(const type& q, int k) {
+    if constexpr (TDT == 0) {
+      return q[k];
+    } else {
+      const uint16_t h = (uint16_t)(q[k >> 1] >> (16 * (k & 1)));
+      return TDT == 2 ? BF16::to_f32(h) : F16::to_f32(h);
+    }
+  }
+};
+
+// store_block_rows with the inverse rotary rotation applied on the way out.
+// The block is staged in LDS rounded to E, exactly as an unfused dQ / dK is
+// stored; on the read back each lane holds 8 consecutive elements of row r,
+// i.e. the interleaved pairs (2i, 2i+1), i = 4c .. 4c+3, at sequence position
+// pos0 + r, and reads their angles with one vector load per table, rotates
+// them with rope_rotate (the RoPE kernel's arithmetic) and rounds again -- the
+// values the separate inverse RoPE pass over the stored gradient would write.
+// Tables: 16-bit, contiguous angles, rows 4-angle aligned (checked by the
+// host).
+template <typename E, int D, int TDT>
+__device__ __forceinline__ void store_block_rows_rope_t(const f32x16 (&acc)[D / 32], float sc,
+                                                        uint16_t* lds, uint16_t* grow,
+                                                        int64_t ss, const RopeTab& t, int pos0) {
+  constexpr int CPR = D / 8;
+  constexpr int RPI = 64 / CPR;
+  const int lane = threadIdx.x & 63;
+  const int l32 = lane & 31;
+  const int g = lane >> 5;
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {
+      const int c = 4 * db + jj;
+      u32x2 w;
+      w[0] = E::pack2(acc[db][4 * jj + 0] * sc, acc[db][4 * jj + 1] * sc);
+      w[1] = E::pack2(acc[db][4 * jj + 2] * sc, acc[db][4 * jj + 3] * sc);
+      *(u32x2*)(lds + l32 * D + ((c ^ (l32 & 7)) << 3) + 4 * g) = w;
+    }
+  // the angles after the accumulators are staged (and dead): loading them
+  // earlier would hold both at once
+  __builtin_amdgcn_sched_barrier(0);
+  typename Tab4<TDT>::type cs[32 / RPI], sn[32 / RPI];
+#pragma unroll
+  for (int p = 0; p < 32 / RPI; ++p) {
+    const int r = p * RPI + lane / CPR;
+    const int c = lane % CPR;
+    cs[p] = Tab4<TDT>::load(t.cos, t.cs_s, pos0 + r, 4 * c);
+    sn[p] = Tab4<TDT>::load(t.sin, t.ss_s, pos0 + r, 4 * c);
+  }
+#pragma unroll
+  for (int p = 0; p < 32 / RPI; ++p) {
+    const int r = p * RPI + lane / CPR;
+    const int c = lane % CPR;
+    const u32x4 v = *(const u32x4*)(lds + r * D + ((c ^ (r & 7)) << 3));
+    u32x4 o;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      float re, ro;
+      rope_rotate(E::to_f32((uint16_t)(v[k] & 0xffffu)), E::to_f32((uint16_t)(v[k] >> 16)),
+                  Tab4<TDT>::get(cs[p], k), Tab4<TDT>::get(sn[p], k), true, re, ro);
+      o[k] = E::pack2(re, ro);
+    }
+    *(u32x4*)(grow + (int64_t)r * ss + 8 * c) = o;
+  }
+}
+
+template <typename E, int D>
+__device__ __forceinline__ void store_block_rows_rope(const f32x16 (&acc)[D / 32], float sc,
+                                                      uint16_t* lds, uint16_t* grow, int64_t ss,
+                                                      const RopeTab& t, int pos0) {
+  // 16-bit tables only (the host runs fp32 tables as a separate pass)
+  if (t.tdt == 2)
+    store_block_rows_rope_t<E, D, 2>(acc, sc, lds, grow, ss, t, pos0);
+  else
+    store_block_rows_rope_t<E, D, 1>(acc, sc, lds, grow, ss, t, pos0);
+}
+
 struct BwdItem {
   int kind;  // 0: dK/dV, 1: dQ
   int tile;  // key tile (kind 0) or query tile (kind 1), OWN rows each
@@ -464,7 +553,9 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * jj + i;
             float p = fast_exp2(__builtin_fmaf(s[r], c, -l4[i]));
-            if (MASKED && diag && l32 > 8 * jj + 4 * g + i) p = 0.f;
+            // (key row l32 against query column 8jj + 4g + i, as l32 - 4g against
+            // a constant: one register instead of one per element)
+            if (MASKED && diag && l32 - 4 * g > 8 * jj + i) p = 0.f;
             s[r] = p;
             dp[r] = -(p * dp[r]);
           }
@@ -534,15 +625,21 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     // The staging buffers are idle after the last step's barrier: wave w
     // stages its rows (dK, then dV) through tile buffer w.
     uint16_t* stage = wave_stage_buf(bufs, wave);
-    store_block_rows<E, D>(dk, a.scale, stage, dk_rows, a.dk.ss);
+    // dV first: its accumulators are dead before dK's rotation needs registers
     store_block_rows<E, D>(dv, 1.f, stage, dv_rows, a.dv.ss);
+    if (a.rope.cos)
+      store_block_rows_rope<E, D>(dk, a.scale, stage, dk_rows, a.dk.ss, a.rope, kw);
+    else
+      store_block_rows<E, D>(dk, a.scale, stage, dk_rows, a.dk.ss);
   } else {
     // D = 128: the wave's K region (32 x D, its own) is idle after the last
     // step.  (Written straight from the accumulators instead, 8 bytes per lane
     // and row, the launch measured the same at configs 3 and 4 and 2% slower
-    // at B8 S1024.)
-    store_block_rows<E, D>(dk, a.scale, kw_lds, dk_rows, a.dk.ss);
+    // at B8 S1024.)  No fused rotation here: its code costs this kernel, at
+    // its register limit, a spilled value reloaded every step; the host runs
+    // the inverse RoPE as a separate pass at D = 128.
     store_block_rows<E, D>(dv, 1.f, kw_lds, dv_rows, a.dv.ss);
+    store_block_rows<E, D>(dk, a.scale, kw_lds, dk_rows, a.dk.ss);
   }
 }
 
@@ -628,7 +725,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           float p = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
-          if (MASKED && diag && 8 * (r >> 2) + 4 * g + (r & 3) > l32) p = 0.f;
+          if (MASKED && diag && 8 * (r >> 2) + (r & 3) > l32 - 4 * g) p = 0.f;
           dp[r] = p * dp[r];
         }
 #pragma unroll
@@ -680,9 +777,13 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   if (!wave_valid) return;
   const int b = it.bh / a.H;
   const int h = it.bh % a.H;
-  store_block_rows<E, D>(acc, a.scale, wave_stage_buf(bufs, wave),
-                         (uint16_t*)a.dq.ptr + b * a.dq.sb + h * a.dq.sh + (int64_t)qw * a.dq.ss,
-                         a.dq.ss);
+  uint16_t* const dq_rows =
+      (uint16_t*)a.dq.ptr + b * a.dq.sb + h * a.dq.sh + (int64_t)qw * a.dq.ss;
+  if (D == 64 && a.rope.cos)
+    store_block_rows_rope<E, D>(acc, a.scale, wave_stage_buf(bufs, wave), dq_rows, a.dq.ss,
+                                a.rope, qw);
+  else
+    store_block_rows<E, D>(acc, a.scale, wave_stage_buf(bufs, wave), dq_rows, a.dq.ss);
 }
 
 // One item per workgroup.  One LDS array per buffer and tensor, so that the

@@ -131,7 +131,7 @@ mi::AttnArgs grad_args(int B, int H, int S, int D, int causal, float scale, cons
 
 extern "C" {
 
-int mi_version(void) { return (2 << 16) | 1; }
+int mi_version(void) { return (2 << 16) | 2; }
 
 const char* mi_status_str(mi_status s) {
   switch (s) {
@@ -179,6 +179,15 @@ mi_status mi_attn_fwd(mi_dtype dtype, int B, int H, int S, int D, int causal, fl
   return launched(mi::launch_attn_fwd_valu(dtype, a, (hipStream_t)stream), "attn_fwd_valu");
 }
 
+static mi_status grads_impl(mi_dtype dtype, int B, int H, int S, int D, int causal, float scale,
+                            const void* q, const int64_t q_strides[4], const void* k,
+                            const int64_t k_strides[4], const void* v,
+                            const int64_t v_strides[4], const void* dout,
+                            const int64_t dout_strides[4], const float* lse, const float* ws,
+                            void* dq, const int64_t dq_strides[4], void* dk,
+                            const int64_t dk_strides[4], void* dv, const int64_t dv_strides[4],
+                            const mi::RopeTab* rope, void* stream);
+
 mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal, float scale,
                       const void* q, const int64_t q_strides[4], const void* k,
                       const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
@@ -212,6 +221,27 @@ mi_status mi_attn_bwd_grads(mi_dtype dtype, int B, int H, int S, int D, int caus
                             void* dq, const int64_t dq_strides[4], void* dk,
                             const int64_t dk_strides[4], void* dv, const int64_t dv_strides[4],
                             void* stream) {
+  return grads_impl(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v, v_strides,
+                    dout, dout_strides, lse, ws, dq, dq_strides, dk, dk_strides, dv, dv_strides,
+                    nullptr, stream);
+}
+
+static mi_status rope_common(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, int D,
+                             int inverse, int nt, const void* const* ins,
+                             const int64_t* const* in_st, void* const* outs,
+                             const int64_t* const* out_st, const void* cos_tab,
+                             const int64_t cos_strides[2], const void* sin_tab,
+                             const int64_t sin_strides[2], void* stream);
+
+// `rope` != nullptr: dQ and dK leave inverse-rotated (mi_attn_bwd_rope).
+static mi_status grads_impl(mi_dtype dtype, int B, int H, int S, int D, int causal, float scale,
+                            const void* q, const int64_t q_strides[4], const void* k,
+                            const int64_t k_strides[4], const void* v,
+                            const int64_t v_strides[4], const void* dout,
+                            const int64_t dout_strides[4], const float* lse, const float* ws,
+                            void* dq, const int64_t dq_strides[4], void* dk,
+                            const int64_t dk_strides[4], void* dv, const int64_t dv_strides[4],
+                            const mi::RopeTab* rope, void* stream) {
   mi_status st;
   if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
   if ((st = check_grad_inputs(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
@@ -230,14 +260,80 @@ mi_status mi_attn_bwd_grads(mi_dtype dtype, int B, int H, int S, int D, int caus
     a.dq = targ(dq, dq_strides);
     a.dk = targ(dk, dk_strides);
     a.dv = targ(dv, dv_strides);
-    return launched(mi::launch_attn_bwd_mfma(dtype, a, (hipStream_t)stream), "attn_bwd_mfma");
+    // The D = 64 kernels' stores rotate with one vector load of four 16-bit
+    // angles per table: rows of contiguous angles, every row start aligned to
+    // four of them.
+    const int tsz = rope ? elem_size((mi_dtype)rope->tdt) : 0;
+    const bool fuse_rope =
+        rope && D == 64 && rope->tdt != MI_F32 && rope->cs_i == 1 && rope->ss_i == 1 && rope->cs_s % 4 == 0 &&
+        rope->ss_s % 4 == 0 && ((uintptr_t)rope->cos) % (4 * tsz) == 0 &&
+        ((uintptr_t)rope->sin) % (4 * tsz) == 0;
+    if (fuse_rope) a.rope = *rope;
+    if ((st = launched(mi::launch_attn_bwd_mfma(dtype, a, (hipStream_t)stream),
+                       "attn_bwd_mfma")) != MI_OK || !rope || fuse_rope)
+      return st;
+  } else {
+    if ((st = mi_attn_bwd_dkdv(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
+                               v_strides, dout, dout_strides, lse, ws, dk, dk_strides, dv,
+                               dv_strides, stream)) != MI_OK)
+      return st;
+    if ((st = mi_attn_bwd_dq(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
+                             v_strides, dout, dout_strides, lse, ws, dq, dq_strides,
+                             stream)) != MI_OK)
+      return st;
+    if (!rope) return MI_OK;
   }
-  if ((st = mi_attn_bwd_dkdv(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
-                             v_strides, dout, dout_strides, lse, ws, dk, dk_strides, dv,
-                             dv_strides, stream)) != MI_OK)
+  // kernels or tables without the fused rotation: the inverse RoPE pass over
+  // dQ and dK in place ([B, H, S, D] strides reordered to the RoPE kernel's
+  // [S, B, H, D])
+  const int64_t qs[4] = {dq_strides[2], dq_strides[0], dq_strides[1], dq_strides[3]};
+  const int64_t ks[4] = {dk_strides[2], dk_strides[0], dk_strides[1], dk_strides[3]};
+  const int64_t cst[2] = {rope->cs_s, rope->cs_i}, sst[2] = {rope->ss_s, rope->ss_i};
+  const void* ins[2] = {dq, dk};
+  const int64_t* ist[2] = {qs, ks};
+  void* outs[2] = {dq, dk};
+  return rope_common(dtype, (mi_dtype)rope->tdt, S, B, H, D, 1, 2, ins, ist, outs, ist,
+                     rope->cos, cst, rope->sin, sst, stream);
+}
+
+mi_status mi_attn_bwd_rope(mi_dtype dtype, int B, int H, int S, int D, int causal, float scale,
+                           const void* q, const int64_t q_strides[4], const void* k,
+                           const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
+                           const void* o, const int64_t o_strides[4], const void* dout,
+                           const int64_t dout_strides[4], const float* lse, float* ws, void* dq,
+                           const int64_t dq_strides[4], void* dk, const int64_t dk_strides[4],
+                           void* dv, const int64_t dv_strides[4], mi_dtype tab_dtype,
+                           const void* cos_tab, const int64_t cos_strides[2],
+                           const void* sin_tab, const int64_t sin_strides[2], void* stream) {
+  mi_status st;
+  if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
+  if ((st = check_attn_tensor("o", o, o_strides)) != MI_OK) return st;
+  if ((st = check_attn_tensor("dq", dq, dq_strides)) != MI_OK) return st;
+  if ((st = check_grad_inputs(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
+                              dout_strides, lse, ws)) != MI_OK)
     return st;
-  return mi_attn_bwd_dq(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
-                        v_strides, dout, dout_strides, lse, ws, dq, dq_strides, stream);
+  if ((st = check_attn_tensor("dk", dk, dk_strides)) != MI_OK) return st;
+  if ((st = check_attn_tensor("dv", dv, dv_strides)) != MI_OK) return st;
+  if (!dtype_ok(tab_dtype)) return fail(MI_ERR_INVALID_ARGUMENT, "unknown table dtype %d", tab_dtype);
+  if (D % 2) return fail(MI_ERR_INVALID_ARGUMENT, "HEAD_DIM must be even (got %d)", D);
+  if (!cos_tab || !sin_tab || !cos_strides || !sin_strides)
+    return fail(MI_ERR_INVALID_ARGUMENT, "cos/sin: null pointer");
+  if (((uintptr_t)cos_tab) % elem_size(tab_dtype) || ((uintptr_t)sin_tab) % elem_size(tab_dtype))
+    return fail(MI_ERR_INVALID_ARGUMENT, "cos/sin: misaligned");
+  mi::RopeTab rope;
+  rope.cos = cos_tab;
+  rope.sin = sin_tab;
+  rope.cs_s = cos_strides[0];
+  rope.cs_i = cos_strides[1];
+  rope.ss_s = sin_strides[0];
+  rope.ss_i = sin_strides[1];
+  rope.tdt = tab_dtype;
+  if ((st = mi_attn_bwd_preprocess(dtype, B, H, S, D, o, o_strides, dout, dout_strides, lse, ws,
+                                   stream)) != MI_OK)
+    return st;
+  return grads_impl(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v, v_strides,
+                    dout, dout_strides, lse, ws, dq, dq_strides, dk, dk_strides, dv, dv_strides,
+                    &rope, stream);
 }
 
 mi_status mi_attn_bwd_preprocess(mi_dtype dtype, int B, int H, int S, int D, const void* o,

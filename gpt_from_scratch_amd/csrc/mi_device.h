@@ -97,6 +97,22 @@ __device__ __forceinline__ uint16_t f32_to_f16(float x) {
   return (uint16_t)(F16::pack2(x, 0.f) & 0xffffu);
 }
 
+// Rotary rotation of one interleaved pair (core/rope_triton.py:128-133) in
+// fp32 with explicit fused multiply-adds, so that every kernel applying it
+// (RoPE itself, and the attention backward's dQ/dK stores) rounds the same:
+//   forward: (e, o) -> (e c - o s, e s + o c)
+//   inverse: (e, o) -> (e c + o s, o c - e s)
+__device__ __forceinline__ void rope_rotate(float e, float o, float c, float s, bool inverse,
+                                            float& re, float& ro) {
+  if (inverse) {
+    re = __builtin_fmaf(e, c, o * s);
+    ro = __builtin_fmaf(o, c, -(e * s));
+  } else {
+    re = __builtin_fmaf(e, c, -(o * s));
+    ro = __builtin_fmaf(e, s, o * c);
+  }
+}
+
 // Storage-type traits for kernels that are generic over fp32 / f16 / bf16.
 template <int DT> struct Store;  // DT: 0 = f32, 1 = f16, 2 = bf16 (mi_dtype values)
 template <> struct Store<0> {

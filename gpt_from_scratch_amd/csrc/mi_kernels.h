@@ -14,6 +14,16 @@ struct TensorArg {
   int64_t sb, sh, ss;
 };
 
+// Rotary tables for an inverse rotation fused into the attention backward's
+// dQ / dK stores: cos / sin [>= S rows, D/2 angles], element strides, table
+// dtype (mi_dtype values).  cos == nullptr: no rotation.
+struct RopeTab {
+  const void* cos;
+  const void* sin;
+  int64_t cs_s, cs_i, ss_s, ss_i;
+  int tdt;
+};
+
 struct AttnArgs {
   TensorArg q, k, v, o, dout, dq, dk, dv;
   float* lse;
@@ -23,6 +33,7 @@ struct AttnArgs {
   float scale;       // softmax scale (1/sqrt(D) in the model)
   float scale_log2;  // scale * log2(e)
   int causal;
+  RopeTab rope;        // backward only: dQ and dK stored inverse-rotated
 };
 
 // Kernel-family launchers.  Each returns hipSuccess or the launch error.

@@ -5,7 +5,8 @@
 // angles come from cos/sin tables [S, D/2] (:118-123), and
 //   forward: (e, o) -> (e*c - o*s, e*s + o*c)             (:131-133)
 //   inverse: (e, o) -> (e*c + o*s, o*c - e*s)             (:128-130)
-// computed in fp32 and rounded once to the output type.
+// computed in fp32 (rope_rotate, explicit fused multiply-adds) and rounded
+// once to the output type.
 //
 // One launch covers q and k (apply_rope_qk, :147-148).  The vector path gives
 // each lane the same 16 bytes (8 bf16/f16 or 4 fp32 values = 4 or 2 pairs) of
@@ -33,16 +34,6 @@ __device__ __forceinline__ float ldx(const void* p, int64_t i) {
   return Store<DT>::ld((const typename Store<DT>::type*)p, i);
 }
 
-__device__ __forceinline__ void rotate(float e, float o, float cs, float sn, int inverse, float& re,
-                                       float& ro) {
-  if (inverse) {
-    re = e * cs + o * sn;
-    ro = o * cs - e * sn;
-  } else {
-    re = e * cs - o * sn;
-    ro = e * sn + o * cs;
-  }
-}
 
 // NP consecutive table entries (one vector load: 8 or 16 bytes for 4 pairs,
 // 4 or 8 bytes for 2 pairs).
@@ -137,7 +128,7 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a, RopeDivs dv, 
           o = F16::to_f32((uint16_t)(x[u][t][p] >> 16));
         }
         float re, ro;
-        rotate(e, o, cs[u][p], sn[u][p], a.inverse, re, ro);
+        rope_rotate(e, o, cs[u][p], sn[u][p], a.inverse != 0, re, ro);
         if constexpr (XDT == 0) {
           y[2 * p] = __float_as_uint(re);
           y[2 * p + 1] = __float_as_uint(ro);
@@ -178,7 +169,7 @@ __global__ __launch_bounds__(256) void rope_pair_kernel(RopeArgs a, RopeDivs dv,
   const float cs = ldx<TDT>(a.cos_tab, s * a.cs_s + (int64_t)i * a.cs_i);
   const float sn = ldx<TDT>(a.sin_tab, s * a.ss_s + (int64_t)i * a.ss_i);
   float re, ro;
-  rotate(e, o, cs, sn, a.inverse, re, ro);
+  rope_rotate(e, o, cs, sn, a.inverse != 0, re, ro);
   Store<XDT>::st(out, (int64_t)(2 * i) * T.os_d, re);
   Store<XDT>::st(out, (int64_t)(2 * i + 1) * T.os_d, ro);
 }

@@ -102,6 +102,37 @@ mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal,
                       void* stream);
 
 /*
+ * mi_attn_bwd for attention on rotated q, k whose gradients are wanted with
+ * respect to the unrotated ones: dQ and dK leave inverse-rotated by the RoPE
+ * tables (interleaved pairs, the rotation of mi_rope with inverse = 1,
+ * evaluated on dQ and dK rounded to `dtype` first, so the result equals
+ * mi_attn_bwd followed by mi_rope_qk(inverse = 1) on dq, dk in place, bit for
+ * bit).  On the matrix-core path at D = 64 with 16-bit tables whose angles
+ * are contiguous and whose row starts are 4-angle aligned (the model's), the
+ * rotation is applied as the kernels store dQ and dK, saving the separate read
+ * and write of both; otherwise the two run one after the other.  cos / sin:
+ * [>= S rows, D/2 angles], strides in elements, dtype tab_dtype.  Replaces the attention block's backward pair,
+ * FlashAttn.backward (core/myFlashAttn.py:288-441) then TritonRoPE.backward
+ * on dq and dk (core/rope_triton.py:50-72), as driven by the autograd of
+ * core/transformer_layer.py:42-61.
+ */
+mi_status mi_attn_bwd_rope(mi_dtype dtype, int B, int H, int S, int D, int causal,
+                           float scale,
+                           const void* q, const int64_t q_strides[4],
+                           const void* k, const int64_t k_strides[4],
+                           const void* v, const int64_t v_strides[4],
+                           const void* o, const int64_t o_strides[4],
+                           const void* dout, const int64_t dout_strides[4],
+                           const float* lse, float* ws,
+                           void* dq, const int64_t dq_strides[4],
+                           void* dk, const int64_t dk_strides[4],
+                           void* dv, const int64_t dv_strides[4],
+                           mi_dtype tab_dtype,
+                           const void* cos_tab, const int64_t cos_strides[2],
+                           const void* sin_tab, const int64_t sin_strides[2],
+                           void* stream);
+
+/*
  * mi_attn_bwd is mi_attn_bwd_preprocess followed by mi_attn_bwd_grads.  The
  * latter produces dQ, dK and dV in one launch where the matrix-core path
  * applies (dK/dV and dQ work interleaved in one grid) and otherwise runs

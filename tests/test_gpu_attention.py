@@ -372,3 +372,42 @@ def test_running_max_moves_every_tile(gpu, S, D, causal):
         worst = budget_ratio(got, want[name], budget[name])
         print(f"S{S} D{D} causal={causal} {name}: worst error {worst:.3f} of the budget")
         assert worst <= 1.0, f"{name}: error reaches {worst:.3f} of the rounding budget"
+
+
+@pytest.mark.parametrize("dtype,D,tab", [(torch.bfloat16, 64, torch.bfloat16),
+                                         (torch.bfloat16, 128, torch.float32),
+                                         (torch.float16, 64, torch.float16),
+                                         (torch.float32, 64, torch.float32)])
+def test_bwd_rope_equals_bwd_then_inverse_rope(gpu, dtype, D, tab):
+    """mi_attn_bwd_rope (the inverse rotation fused into the dQ / dK stores on
+    the matrix-core path; fp32 takes the VALU kernels and a separate pass)
+    against mi_attn_bwd followed by mi_rope_qk(inverse) on dq, dk in place: dQ,
+    dK and dV bit for bit, with q, k, v, dO as the model's strided views and the
+    gradients written into the slots of one [S, B, 3, H, D] buffer."""
+    from gpt_from_scratch_amd import _lib, flash_attn_forward
+    from gpt_from_scratch_amd.position_embeddings import RotaryEmbedding
+    S, B, H = 256, 2, 4
+    qkv = seeded((S, B, 3, H, D), 700 + D, dtype=dtype).to(gpu)
+    do = seeded((S, B, H, D), 701 + D, dtype=dtype).to(gpu)
+    rot = RotaryEmbedding(D, S, device=gpu)
+    cos, sin = (t.to(tab) for t in (rot.cos_cached, rot.sin_cached))
+    bhsd = (1, 2, 0, 3)
+    q, k, v = (qkv[:, :, i].permute(bhsd) for i in range(3))
+    o, lse = flash_attn_forward(q, k, v, True)
+    scale = 1.0 / D ** 0.5
+    outs = []
+    for fused in (True, False):
+        g = torch.full((S, B, 3, H, D), float("nan"), dtype=dtype, device=gpu)
+        dq, dk, dv = (g[:, :, i] for i in range(3))
+        ws = _lib.bwd_workspace(lse)
+        if fused:
+            _lib.attn_bwd_rope(q, k, v, o, do.permute(bhsd), lse, ws, dq.permute(bhsd),
+                               dk.permute(bhsd), dv.permute(bhsd), True, scale, cos, sin)
+        else:
+            _lib.attn_bwd(q, k, v, o, do.permute(bhsd), lse, ws, dq.permute(bhsd),
+                          dk.permute(bhsd), dv.permute(bhsd), True, scale)
+            _lib.rope_qk(dq, dk, cos, sin, dq, dk, inverse=True)
+        torch.cuda.synchronize()
+        outs.append(g)
+    assert not torch.isnan(outs[0]).any()
+    assert torch.equal(outs[0], outs[1])
