@@ -158,28 +158,41 @@ struct BwdCfg {
 
 // LDS layout of a streamed tile: TILE rows of D elements, no padding; the
 // 16-byte chunk c of row r sits at chunk position c ^ swz(r), with
-//   swz(r) = 2*(r & 3) + ((r >> 2) & 1).
-// The tiles are read two ways: 16-byte row reads (consecutive rows, one chunk
-// each: swz takes eight distinct values on eight rows) and transposing reads
-// (four consecutive rows and two adjacent chunks per 16 lanes: swz >> 1 takes
-// four distinct values there, and the operand's second read 8 rows on relies
-// on swz repeating every 8 rows).  The gfx950 LDS serves a 16-byte read for 16
-// lanes per cycle over 64 banks, so the row reads see a 2-way conflict between
-// rows r and r + 8; removing it needs a swizzle that differs between them, i.e.
-// a second offset for the transposing reads, in kernels at their register
-// limit.
-__device__ __forceinline__ int bwd_swz(int r) { return ((r & 3) << 1) | ((r >> 2) & 1); }
+//   swz(r) = 2*(r & 3) + ((r >> 2) & 1)        (D = 128)
+//   swz(r) = that ^ 2*((r >> 3) & 1)           (D = 64)
+// The tiles are read two ways: 16-byte row reads (16 consecutive rows per LDS
+// cycle, one chunk each) and transposing reads (four consecutive rows and two
+// adjacent chunks per 16 lanes: swz >> 1 takes four distinct values there).
+// The gfx950 LDS has 64 four-byte banks and serves a 16-byte read for 16 lanes
+// per cycle.  At D = 64 a 256-byte bank line holds two rows, so the row reads
+// of rows r..r+15 are conflict-free when swz takes eight distinct values on
+// the eight rows of each parity: the term in bit 3 of r gives that (without
+// it rows r and r + 8 collide, a 2-way conflict), at the price of a second
+// offset for the transposing read 8 rows on.  At D = 128 a row fills a bank
+// line and three bits of swizzle cannot separate 16 rows; the 2-way conflict
+// stays, and the swizzle repeats every 8 rows.
+template <int D>
+__device__ __forceinline__ int bwd_swz(int r) {
+  const int s = ((r & 3) << 1) | ((r >> 2) & 1);
+  return D == 64 ? s ^ (((r >> 3) & 1) << 1) : s;
+}
 
 // Per-lane LDS element offsets of the two tile reads: 16-byte row reads (row
-// l%32, chunk 2ks + l/32) and transposing reads (row 4(l/32) + (l%16)/4,
-// column 32db + 16((l/16)%2) + 4(l%4)).  swz < 8 only changes the low three
-// bits of a chunk index, so chunk c + 8 sits 64 elements after chunk c: four
-// row offsets and two transposing offsets (plus immediates) cover every read.
+// l%32, chunk 2ks + l/32) and transposing reads (rows 4(l/32) + (l%16)/4 and,
+// for the operand's second half, those + 8; column 32db + 16((l/16)%2) +
+// 4(l%4)).  swz < 8 only changes the low three bits of a chunk index, so
+// chunk c + 8 sits 64 elements after chunk c, and swz repeats every 16 rows:
+// four row offsets and two (D = 128: the second half is 8 rows on, same
+// swizzle) or four transposing offsets, plus immediates, cover every read.
 template <int D>
 struct LdsOffsets {
-  int r4[4], t2[2];
+  int r4[4], t2[2], t2h[D == 64 ? 2 : 1];
   __device__ __forceinline__ int row(int ks) const { return r4[ks & 3] + 64 * (ks >> 2); }
   __device__ __forceinline__ int tr(int db) const { return t2[db & 1] + 64 * (db >> 1); }
+  __device__ __forceinline__ int tr_hi(int db) const {
+    if constexpr (D == 64) return t2h[db & 1] + 64 * (db >> 1);
+    else return tr(db) + 8 * D;
+  }
 };
 
 template <int D>
@@ -188,14 +201,23 @@ __device__ __forceinline__ LdsOffsets<D> lds_offsets(int lane) {
   const int g = lane >> 5;
   LdsOffsets<D> o;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) o.r4[ks] = l32 * D + (((2 * ks + g) ^ bwd_swz(l32)) << 3);
+  for (int ks = 0; ks < 4; ++ks) o.r4[ks] = l32 * D + (((2 * ks + g) ^ bwd_swz<D>(l32)) << 3);
 #pragma unroll
   for (int db = 0; db < 2; ++db) {
     const int r = 4 * g + ((lane & 15) >> 2);
     const int ch = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-    o.t2[db] = r * D + ((ch ^ bwd_swz(r)) << 3) + 4 * (lane & 1);
+    o.t2[db] = r * D + ((ch ^ bwd_swz<D>(r)) << 3) + 4 * (lane & 1);
+    if constexpr (D == 64)
+      o.t2h[db] = (r + 8) * D + ((ch ^ bwd_swz<D>(r + 8)) << 3) + 4 * (lane & 1);
   }
   return o;
+}
+
+// The transposed A operand from its two halves (rows k0..k0+7 and k0+8..+15).
+__device__ __forceinline__ u32x4 tr_operand2(const uint16_t* lo, const uint16_t* hi) {
+  const u32x2 a = ds_read_tr16(lo);
+  const u32x2 b = ds_read_tr16(hi);
+  return u32x4{a[0], a[1], b[0], b[1]};
 }
 
 // The four angles i0 .. i0+3 of table row `pos` (contiguous angles, dtype
@@ -400,7 +422,7 @@ __device__ __forceinline__ StageSrc<D> stage_src(const AttnArgs& a, const BwdIte
 #pragma unroll
   for (int m = 0; m < C::SPW; ++m) {
     const int r = (wave + 4 * m) * C::RPS + lane / C::CPR;
-    const int col = ((lane % C::CPR) ^ bwd_swz(r)) << 3;
+    const int col = ((lane % C::CPR) ^ bwd_swz<D>(r)) << 3;
     s.off0[m] = (uint32_t)((r * t0.ss + col) * 2);
     s.off1[m] = (uint32_t)((r * t1.ss + col) * 2);
   }
@@ -490,7 +512,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
 #pragma unroll
       for (int m = 0; m < 32 * D * 2 / 1024; ++m) {
         const int r = m * C::RPS + lane / C::CPR;
-        const int col = ((lane % C::CPR) ^ bwd_swz(r)) << 3;
+        const int col = ((lane % C::CPR) ^ bwd_swz<D>(r)) << 3;
         buffer_load_lds16(rk, (uint32_t)((r * a.k.ss + col) * 2), kw_lds + m * 512);
       }
     }
@@ -575,9 +597,11 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
           for (int db = 0; db < C::DB; ++db) {
-            const int off = (32 * qb + 16 * hh) * D + lo.tr(db);
-            dv[db] = E::mfma(tr_operand(&dOs[off], D), pb[qb][hh], dv[db]);
-            dk[db] = E::mfma(tr_operand(&Qs[off], D), sb[qb][hh], dk[db]);
+            const int off = (32 * qb + 16 * hh) * D;
+            dv[db] = E::mfma(tr_operand2(&dOs[off + lo.tr(db)], &dOs[off + lo.tr_hi(db)]),
+                             pb[qb][hh], dv[db]);
+            dk[db] = E::mfma(tr_operand2(&Qs[off + lo.tr(db)], &Qs[off + lo.tr_hi(db)]),
+                             sb[qb][hh], dk[db]);
           }
         }
       }
@@ -741,8 +765,9 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
           for (int db = 0; db < C::DB; ++db) {
-            const int off = (32 * kb + 16 * hh) * D + lo.tr(db);
-            acc[db] = E::mfma(tr_operand(&Ks[off], D), sb[kb][hh], acc[db]);
+            const int off = (32 * kb + 16 * hh) * D;
+            acc[db] = E::mfma(tr_operand2(&Ks[off + lo.tr(db)], &Ks[off + lo.tr_hi(db)]),
+                              sb[kb][hh], acc[db]);
           }
         }
       }

@@ -104,8 +104,10 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a, RopeDivs dv, 
       const RopeTensor& T = a.t[t];
       const int64_t in_off = s * T.is_s + b * T.is_b + h * T.is_h + (int64_t)cidx * VEC;
       out_off[u][t] = s * T.os_s + b * T.os_b + h * T.os_h + (int64_t)cidx * VEC;
-      x[u][t] = (XDT == 0) ? *(const u32x4*)((const float*)T.in + in_off)
-                           : *(const u32x4*)((const uint16_t*)T.in + in_off);
+      // read once: non-temporal (9.3 against 9.45 us for the C2 q/k pair from HBM)
+      x[u][t] = (XDT == 0)
+                    ? __builtin_nontemporal_load((const u32x4*)((const float*)T.in + in_off))
+                    : __builtin_nontemporal_load((const u32x4*)((const uint16_t*)T.in + in_off));
     }
   }
 #pragma unroll
