@@ -12,7 +12,7 @@ Printed: ONE JSON line with the metric of BASELINE.json (algorithmic TFLOP/s of
 fwd+bwd, causal counted as half of dense: 7*B*H*S^2*D flops per step) from a
 timed pass of K steps with events only at its ends (after at least 50 ms of
 untimed steps for the GPU to reach steady clocks, then W untimed steps), the per-kernel
-durations from K back-to-back launches of each kernel alone, the roofline of
+durations from max(K, 100) back-to-back launches of each kernel alone, the roofline of
 the dominant kernel, the RoPE bandwidth, the train step's fused operators and
 config-5 tokens/s, and the CPU baseline (the oracle's fp32 eager attention on
 the host cores).
@@ -645,25 +645,27 @@ def main():
     ms_per_step = t_start.elapsed_time(t_end) / args.steps
     _progress(f"config 2 timed pass: {ms_per_step * 1e3:.1f} us per step")
 
-    # Per-kernel durations: each kernel of the step launched K times back to
-    # back on its own (its inputs are unchanged, so every launch redoes the same
-    # work), with events only at the ends of each run; the intervals hold the
-    # K - 1 dispatch gaps between launches, not the events' own overhead.
-    # These K launches of each kernel are the ones a profiler records
-    # (`rocprofv3 --selected-regions`), so its per-dispatch average is the
-    # duration the roofline below divides by, less the K - 1 gaps.
+    # Per-kernel durations: each kernel of the step launched back to back on
+    # its own (its inputs are unchanged, so every launch redoes the same work),
+    # with events only at the ends of each run; the intervals hold the dispatch
+    # gaps between launches.
+    # These launches of each kernel (at least 100, so that the events' own
+    # cost at the ends is spread thin) are the ones a profiler records
+    # (`rocprofv3 --selected-regions`): its per-dispatch average is the
+    # duration the roofline below divides by, less the dispatch gaps.
+    n_kernel = max(args.steps, 100)
     per_kernel_us = {}
     for name, fn, a in calls:
         k0, k1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
         REGIONS.resume()
         k0.record(stream)
-        for _ in range(args.steps):
+        for _ in range(n_kernel):
             fn(*a)
         k1.record(stream)
         torch.cuda.synchronize()
         REGIONS.pause()
-        per_kernel_us[name] = k0.elapsed_time(k1) / args.steps * 1e3
+        per_kernel_us[name] = k0.elapsed_time(k1) / n_kernel * 1e3
 
     kflops = {"attn_fwd": flops["fwd"], "attn_bwd": flops["bwd"]}
     kernels = {}

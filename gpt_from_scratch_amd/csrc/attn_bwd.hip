@@ -169,46 +169,70 @@ struct BwdCfg {
 // the eight rows of each parity: the term in bit 3 of r gives that (without
 // it rows r and r + 8 collide, a 2-way conflict), at the price of a second
 // offset for the transposing read 8 rows on.  At D = 128 a row fills a bank
-// line and three bits of swizzle cannot separate 16 rows; the 2-way conflict
-// stays, and the swizzle repeats every 8 rows.
-template <int D>
+// line, so 16 rows need 16 positions: SW16 adds bit 3 of r as bit 3 of the
+// swizzle (the dQ kind; the dK/dV kind, at its register limit, cannot hold the
+// extra offsets, keeps the 3-bit swizzle repeating every 8 rows and its 2-way
+// conflict).  Each kind writes and reads its own staged tiles, so the two may
+// differ.
+template <int D, bool SW16 = false>
 __device__ __forceinline__ int bwd_swz(int r) {
   const int s = ((r & 3) << 1) | ((r >> 2) & 1);
-  return D == 64 ? s ^ (((r >> 3) & 1) << 1) : s;
+  if constexpr (D == 64) return s ^ (((r >> 3) & 1) << 1);
+  else if constexpr (SW16) return s | (((r >> 3) & 1) << 3);
+  else return s;
 }
 
 // Per-lane LDS element offsets of the two tile reads: 16-byte row reads (row
 // l%32, chunk 2ks + l/32) and transposing reads (rows 4(l/32) + (l%16)/4 and,
 // for the operand's second half, those + 8; column 32db + 16((l/16)%2) +
-// 4(l%4)).  swz < 8 only changes the low three bits of a chunk index, so
+// 4(l%4)).  A 3-bit swz only changes the low three bits of a chunk index, so
 // chunk c + 8 sits 64 elements after chunk c, and swz repeats every 16 rows:
 // four row offsets and two (D = 128: the second half is 8 rows on, same
 // swizzle) or four transposing offsets, plus immediates, cover every read.
-template <int D>
+// With SW16 bit 3 of the position is bit 3 of the chunk XOR bit 3 of the row:
+// eight row offsets; the transposing reads' first half (rows < 8) is as
+// without, the second half flips bit 3 (+64 elements for chunks < 8, -64 above).
+template <int D, bool SW16 = false>
 struct LdsOffsets {
-  int r4[4], t2[2], t2h[D == 64 ? 2 : 1];
-  __device__ __forceinline__ int row(int ks) const { return r4[ks & 3] + 64 * (ks >> 2); }
+  static constexpr bool R8 = D == 128 && SW16;
+  int r4[R8 ? 8 : 4], t2[2], t2h[D == 64 || R8 ? 2 : 1];
+  __device__ __forceinline__ int row(int ks) const {
+    if constexpr (R8) return r4[ks];
+    else return r4[ks & 3] + 64 * (ks >> 2);
+  }
   __device__ __forceinline__ int tr(int db) const { return t2[db & 1] + 64 * (db >> 1); }
   __device__ __forceinline__ int tr_hi(int db) const {
     if constexpr (D == 64) return t2h[db & 1] + 64 * (db >> 1);
+    else if constexpr (R8) return t2h[db & 1] + 64 * (1 - (db >> 1));
     else return tr(db) + 8 * D;
   }
 };
 
-template <int D>
-__device__ __forceinline__ LdsOffsets<D> lds_offsets(int lane) {
+template <int D, bool SW16 = false>
+__device__ __forceinline__ LdsOffsets<D, SW16> lds_offsets(int lane) {
   const int l32 = lane & 31;
   const int g = lane >> 5;
-  LdsOffsets<D> o;
+  LdsOffsets<D, SW16> o;
+  if constexpr (LdsOffsets<D, SW16>::R8) {
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) o.r4[ks] = l32 * D + (((2 * ks + g) ^ bwd_swz<D>(l32)) << 3);
+    for (int ks = 0; ks < 8; ++ks)
+      o.r4[ks] = l32 * D + (((2 * ks + g) ^ bwd_swz<D, SW16>(l32)) << 3);
+  } else {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks)
+      o.r4[ks] = l32 * D + (((2 * ks + g) ^ bwd_swz<D, SW16>(l32)) << 3);
+  }
 #pragma unroll
   for (int db = 0; db < 2; ++db) {
     const int r = 4 * g + ((lane & 15) >> 2);
     const int ch = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-    o.t2[db] = r * D + ((ch ^ bwd_swz<D>(r)) << 3) + 4 * (lane & 1);
+    o.t2[db] = r * D + ((ch ^ bwd_swz<D, SW16>(r)) << 3) + 4 * (lane & 1);
     if constexpr (D == 64)
       o.t2h[db] = (r + 8) * D + ((ch ^ bwd_swz<D>(r + 8)) << 3) + 4 * (lane & 1);
+    else if constexpr (LdsOffsets<D, SW16>::R8)
+      // rows r + 8 (< 16): low three bits as row r, bit 3 of the chunk
+      // flipped; the +64 / -64 of that flip is tr_hi's immediate
+      o.t2h[db] = (r + 8) * D + ((ch ^ (bwd_swz<D, SW16>(r + 8) & 7)) << 3) + 4 * (lane & 1);
   }
   return o;
 }
@@ -402,7 +426,7 @@ __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& 
   }
 }
 
-template <int D>
+template <int D, bool SW16 = false>
 __device__ __forceinline__ StageSrc<D> stage_src(const AttnArgs& a, const BwdItem& it) {
   using C = BwdCfg<D>;
   const int lane = threadIdx.x & 63;
@@ -422,7 +446,7 @@ __device__ __forceinline__ StageSrc<D> stage_src(const AttnArgs& a, const BwdIte
 #pragma unroll
   for (int m = 0; m < C::SPW; ++m) {
     const int r = (wave + 4 * m) * C::RPS + lane / C::CPR;
-    const int col = ((lane % C::CPR) ^ bwd_swz<D>(r)) << 3;
+    const int col = ((lane % C::CPR) ^ bwd_swz<D, SW16>(r)) << 3;
     s.off0[m] = (uint32_t)((r * t0.ss + col) * 2);
     s.off1[m] = (uint32_t)((r * t1.ss + col) * 2);
   }
@@ -687,11 +711,12 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   const int qw = q0 + 32 * wave;
   const bool wave_valid = qw < S;
 
-  const LdsOffsets<D> lo = lds_offsets<D>(lane);
+  // D = 128: the 4-bit swizzle (conflict-free row reads), see bwd_swz
+  const LdsOffsets<D, D == 128> lo = lds_offsets<D, D == 128>(lane);
 
   const int kv_end = CAUSAL ? min(q0 + C::OWN, S) : S;
   const int nkv = kv_end / C::TILE;
-  const StageSrc<D> src = stage_src<D>(a, it);
+  const StageSrc<D> src = stage_src<D, D == 128>(a, it);
 
   f32x16 acc[C::DB];
 #pragma unroll
