@@ -255,3 +255,33 @@ def test_rows_view_of_model_op_tensors():
     for f in (mlp_rows, norm_rows):
         c = f(b)
         assert c.is_contiguous() and torch.equal(c, b)
+
+
+def test_new_entry_points_reject_bad_arguments():
+    """mi_rmsnorm_add_fwd / _bwd and mi_attn_bwd_rope validate before any launch."""
+    lib = _lib.lib()
+    fake = ctypes.c_void_p(16)
+    # fused add + RMSNorm: the residual and the sum are required, with full rows
+    assert lib.mi_rmsnorm_add_fwd(2, 2, 4, 768, 1e-6, fake, 768, None, 768, fake, fake, 768,
+                                  fake, 768, fake, None) == 1
+    assert b"residual" in lib.mi_last_error()
+    assert lib.mi_rmsnorm_add_fwd(2, 2, 4, 768, 1e-6, fake, 768, fake, 700, fake, fake, 768,
+                                  fake, 768, fake, None) == 1
+    assert b"row stride" in lib.mi_last_error()
+    need = lib.mi_rmsnorm_bwd_workspace(4, 768)
+    assert lib.mi_rmsnorm_add_bwd(2, 2, 4, 768, fake, 768, fake, fake, fake, 768, None, 768,
+                                  fake, 768, fake, fake, need, None) == 1
+    assert b"dsum" in lib.mi_last_error()
+    assert lib.mi_rmsnorm_add_bwd(2, 2, 4, 768, fake, 768, fake, fake, fake, 768, fake, 768,
+                                  fake, 768, fake, fake, need - 1, None) == 1
+    assert b"workspace" in lib.mi_last_error()
+    # backward with the fused inverse rotation: the tables are checked like the tensors
+    st = _i4(0, 0, 64, 1)
+    t2 = (ctypes.c_int64 * 2)(32, 1)
+    args = [2, 1, 1, 64, 64, 1, 0.125] + [fake, st] * 5 + [fake, fake] + [fake, st] * 3
+    assert lib.mi_attn_bwd_rope(*args, 7, fake, t2, fake, t2, None) == 1
+    assert b"table dtype" in lib.mi_last_error()
+    assert lib.mi_attn_bwd_rope(*args, 2, None, t2, fake, t2, None) == 1
+    assert b"cos/sin" in lib.mi_last_error()
+    odd = [2, 1, 1, 64, 63, 1, 0.125] + args[7:]
+    assert lib.mi_attn_bwd_rope(*odd, 2, fake, t2, fake, t2, None) != 0
