@@ -374,13 +374,15 @@ def test_running_max_moves_every_tile(gpu, S, D, causal):
         assert worst <= 1.0, f"{name}: error reaches {worst:.3f} of the rounding budget"
 
 
-@pytest.mark.parametrize("dtype,D,tab", [(torch.bfloat16, 64, torch.bfloat16),
-                                         (torch.bfloat16, 128, torch.float32),
-                                         (torch.float16, 64, torch.float16),
-                                         (torch.float32, 64, torch.float32)])
-def test_bwd_rope_equals_bwd_then_inverse_rope(gpu, dtype, D, tab):
+@pytest.mark.parametrize("dtype,D,tab,pad", [(torch.bfloat16, 64, torch.bfloat16, 0),
+                                             (torch.bfloat16, 64, torch.bfloat16, 1),
+                                             (torch.bfloat16, 128, torch.float32, 0),
+                                             (torch.float16, 64, torch.float16, 0),
+                                             (torch.float32, 64, torch.float32, 0)])
+def test_bwd_rope_equals_bwd_then_inverse_rope(gpu, dtype, D, tab, pad):
     """mi_attn_bwd_rope (the inverse rotation fused into the dQ / dK stores on
-    the matrix-core path; fp32 takes the VALU kernels and a separate pass)
+    the matrix-core path at D = 64 with aligned 16-bit tables; D = 128, fp32
+    tables, rows not 4-angle aligned (pad) and fp32 take a separate pass)
     against mi_attn_bwd followed by mi_rope_qk(inverse) on dq, dk in place: dQ,
     dK and dV bit for bit, with q, k, v, dO as the model's strided views and the
     gradients written into the slots of one [S, B, 3, H, D] buffer."""
@@ -391,6 +393,11 @@ def test_bwd_rope_equals_bwd_then_inverse_rope(gpu, dtype, D, tab):
     do = seeded((S, B, H, D), 701 + D, dtype=dtype).to(gpu)
     rot = RotaryEmbedding(D, S, device=gpu)
     cos, sin = (t.to(tab) for t in (rot.cos_cached, rot.sin_cached))
+    if pad:  # rows D/2 + 1 apart: not 4-angle aligned, so the separate pass runs
+        wide = [torch.zeros(S, D // 2 + 1, dtype=tab, device=gpu) for _ in range(2)]
+        for w_, t_ in zip(wide, (cos, sin)):
+            w_[:, :D // 2] = t_
+        cos, sin = (w_[:, :D // 2] for w_ in wide)
     bhsd = (1, 2, 0, 3)
     q, k, v = (qkv[:, :, i].permute(bhsd) for i in range(3))
     o, lse = flash_attn_forward(q, k, v, True)
