@@ -8,8 +8,10 @@
 //             0 after the shift, :33-41); the log-sum-exp lse_r = m_r + log(sum)
 //             is kept for the backward instead of the whole softmax (:54-56);
 //   backward: dz_rj = (exp(z_rj - lse_r) - [j == t_r]) * dloss_r   (:59-72).
-// One workgroup per row.  The reference computes in the logits' dtype; here the
-// row statistics and the softmax are fp32 and only the outputs are rounded.
+// The forward runs one workgroup per row; the backward too, except for dense
+// rows (below), which it streams as one flat run of vectors.  The reference
+// computes in the logits' dtype; here the row statistics and the softmax are
+// fp32 and only the outputs are rounded.
 //
 // Logits rows of a vocabulary of odd length are not 16-byte aligned, so each
 // row is split into a scalar head up to the first 16-byte boundary, a body of
@@ -205,6 +207,108 @@ __global__ __launch_bounds__(XT) void xent_bwd_kernel(const void* logits, int64_
   }
 }
 
+// Dense rows (both row strides == vocab, both buffers 16-byte aligned, fewer
+// than 2^31 elements): the [rows, vocab] matrix as one run of 16-byte vectors,
+// consecutive across the grid on every pass -- the access pattern a plain copy
+// streams at -- instead of one row per workgroup (thousands of separate
+// read and write streams at once).  With vocab >= 64 * 8 + 8 a wave's 64
+// consecutive vectors touch at most two rows, A and A + 1; their statistics
+// are wave-uniform scalar loads, and a lane picks one set for its vector,
+// per element only for the one vector that straddles the row boundary.
+// At config 5's [8192, 50257] bf16: 308-324 us (~5.3 TB/s) against 356 us for
+// the per-row kernel; 1024 workgroups (one vector per lane) 473 us, 2048 with
+// one 330-340, with four 312-328, 8192 with one 318-330.
+constexpr int XENT_FLAT_GRID = 2048;
+constexpr int XENT_FLAT_U = 2;
+constexpr int64_t XENT_FLAT_MIN_VOCAB = 1024;
+
+template <int DT>
+__global__ __launch_bounds__(XT) void xent_bwd_flat_kernel(const void* logits, uint32_t n,
+                                                           uint32_t rows, FastDiv vocab,
+                                                           const int64_t* target,
+                                                           const float* lse,
+                                                           const void* grad_loss, void* grad) {
+  typedef typename Store<DT>::type T;
+  constexpr int N = Vec16<DT>::N;
+  const uint32_t V = vocab.d;
+  // statistics of row r: lse in exp2 units, dloss, flat index of the target
+  // (-1 for a masked target, which no element matches)
+  auto stats = [&](uint32_t r, float& l2, float& gl, int64_t& tf) __attribute__((always_inline)) {
+    l2 = lse[r] * kLog2e;
+    gl = Store<DT>::ld((const T*)grad_loss, r);
+    const int64_t t = target[r];
+    tf = (t >= 0 && t < (int64_t)V) ? (int64_t)r * V + t : -1;
+  };
+  auto value = [&](float x, int64_t f, float l2, float gl, int64_t tf) __attribute__((always_inline)) {
+    const float p = fast_exp2(__builtin_fmaf(x, kLog2e, -l2));
+    return (f == tf ? p - 1.f : p) * gl;
+  };
+  const uint32_t nv = n / N;
+  const uint32_t stride = gridDim.x * XT;
+  const u32x4* zv = (const u32x4*)logits;
+  u32x4* gv = (u32x4*)grad;
+  // XENT_FLAT_U vectors per lane in flight, a grid apart
+  for (uint32_t q0 = blockIdx.x * XT + threadIdx.x; q0 - threadIdx.x % 64 < nv;
+       q0 += XENT_FLAT_U * stride) {
+    u32x4 v[XENT_FLAT_U];
+#pragma unroll
+    for (int u = 0; u < XENT_FLAT_U; ++u)
+      if (q0 + u * stride < nv) v[u] = __builtin_nontemporal_load(zv + q0 + u * stride);
+#pragma unroll
+    for (int u = 0; u < XENT_FLAT_U; ++u) {
+      const uint32_t q = q0 + u * stride;
+      // rows of this wave's first vector (A) and the next one (B)
+      const uint32_t f0 = __builtin_amdgcn_readfirstlane(q * N);
+      if (f0 >= n) break;  // wave-uniform
+      const uint32_t ra = fdiv(f0, vocab);
+      const uint32_t rb = min(ra + 1, rows - 1);
+      float l2a, gla, l2b, glb;
+      int64_t tfa, tfb;
+      stats(ra, l2a, gla, tfa);
+      stats(rb, l2b, glb, tfb);
+      if (q >= nv) continue;
+      const uint32_t f = q * N;
+      const uint32_t bnd = (ra + 1) * V;  // first element of row A + 1
+      float y[N];
+      if (f + N <= bnd || f >= bnd) {
+        const bool b = f >= bnd;
+        const float l2 = b ? l2b : l2a, gl = b ? glb : gla;
+        const int64_t tf = b ? tfb : tfa;
+#pragma unroll
+        for (int e = 0; e < N; ++e) y[e] = value(elem<DT>(v[u], e), (int64_t)f + e, l2, gl, tf);
+      } else {
+#pragma unroll
+        for (int e = 0; e < N; ++e) {
+          const bool b = f + e >= bnd;
+          y[e] = value(elem<DT>(v[u], e), (int64_t)f + e, b ? l2b : l2a, b ? glb : gla,
+                       b ? tfb : tfa);
+        }
+      }
+      u32x4 o;
+      if constexpr (DT == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = __float_as_uint(y[e]);
+      } else if constexpr (DT == 2) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = BF16::pack2(y[2 * e], y[2 * e + 1]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = F16::pack2(y[2 * e], y[2 * e + 1]);
+      }
+      __builtin_nontemporal_store(o, gv + q);
+    }
+  }
+  // the last n % N elements, one per lane of the first workgroup
+  if (blockIdx.x == 0 && threadIdx.x < n - nv * N) {
+    const uint32_t fl = nv * N + threadIdx.x;
+    const uint32_t r = fdiv(fl, vocab);
+    float l2, gl;
+    int64_t tf;
+    stats(r, l2, gl, tf);
+    Store<DT>::st((T*)grad, fl, value(Store<DT>::ld((const T*)logits, fl), fl, l2, gl, tf));
+  }
+}
+
 }  // namespace
 
 hipError_t launch_xent_fwd(int dtype, const XentArgs& a, hipStream_t st) {
@@ -228,6 +332,25 @@ hipError_t launch_xent_bwd(int dtype, const XentArgs& a, hipStream_t st) {
   const int esz = dtype == 0 ? 4 : 2;
   const int vec_ok = ((uintptr_t)a.logits % 16 == (uintptr_t)a.grad % 16) &&
                      ((a.row_stride * esz) % 16 == (a.grad_row_stride * esz) % 16);
+  const int64_t n = a.rows * a.vocab;
+  if (a.row_stride == a.vocab && a.grad_row_stride == a.vocab && (uintptr_t)a.logits % 16 == 0 &&
+      (uintptr_t)a.grad % 16 == 0 && a.vocab >= XENT_FLAT_MIN_VOCAB && n < (int64_t)1 << 31) {
+    const FastDiv fv = make_fastdiv((uint32_t)a.vocab);
+    const int N = 16 / esz;
+    const int64_t want = (n / N + XT - 1) / XT;
+    const dim3 fgrid((unsigned)(want < XENT_FLAT_GRID ? (want > 0 ? want : 1) : XENT_FLAT_GRID));
+    const uint32_t un = (uint32_t)n, ur = (uint32_t)a.rows;
+    if (dtype == 0)
+      hipLaunchKernelGGL(xent_bwd_flat_kernel<0>, fgrid, block, 0, st, a.logits, un, ur, fv,
+                         a.target, a.lse, a.grad_loss, a.grad);
+    else if (dtype == 1)
+      hipLaunchKernelGGL(xent_bwd_flat_kernel<1>, fgrid, block, 0, st, a.logits, un, ur, fv,
+                         a.target, a.lse, a.grad_loss, a.grad);
+    else
+      hipLaunchKernelGGL(xent_bwd_flat_kernel<2>, fgrid, block, 0, st, a.logits, un, ur, fv,
+                         a.target, a.lse, a.grad_loss, a.grad);
+    return hipGetLastError();
+  }
   if (dtype == 0)
     hipLaunchKernelGGL(xent_bwd_kernel<0>, grid, block, 0, st, a.logits, a.row_stride, a.vocab,
                        a.target, a.lse, a.grad_loss, a.grad, a.grad_row_stride, vec_ok);
@@ -857,7 +980,10 @@ namespace {
 
 constexpr int ADAM_PARTS = 4096;  // workgroups of the norm pass = partial sums
 constexpr int ADAM_T = 256;
-constexpr int ADAM_STEP_GRID = 1024;  // measured best for read + write streams
+// Two workgroups per CU: at config 5's 190 M parameters 978 us, against 1115
+// at 1024 workgroups, 1183 at 2048, 1010 at 384 and 1030 at 768 (its eight
+// streams of 16-byte vectors keep fewer DRAM pages open with fewer waves).
+constexpr int ADAM_STEP_GRID = 512;
 
 // 16 bytes of the gradient as floats (8 16-bit or 4 fp32 elements)
 template <int GT>

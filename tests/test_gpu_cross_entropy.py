@@ -152,3 +152,28 @@ def test_minus_inf_logits(gpu, dtype):
     ref_grad = cross_entropy_backward(z.double().numpy(), t.numpy(), dl.double().numpy())
     _check("loss", loss, ref_loss, dtype, 4e-6)
     _check("grad", grad, ref_grad, dtype, 4e-6 * np.abs(dl.double().numpy())[:, None])
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("rows,V", [(5, 1027), (3, 1024), (17, 2053), (2, 4096)])
+def test_dense_rows_flat_backward(gpu, dtype, rows, V):
+    """Dense rows of a vocabulary >= 1024 take the backward's flat path (the
+    matrix as one run of 16-byte vectors): vectors that straddle a row boundary,
+    the last n % 8 (or n % 4) elements, masked targets (-1, V, -100) and a
+    target on a row's first and last element, out of place and in place."""
+    z = seeded((rows, V), 801 + V, std=2.0, dtype=dtype)
+    t = torch.randint(0, V, (rows,), generator=torch.Generator().manual_seed(V + rows))
+    t[0] = 0
+    t[-1] = V - 1
+    if rows > 2:
+        t[1] = -1
+        t[2] = V
+    if rows > 4:
+        t[3] = -100
+    dl = seeded((rows,), 802, dtype=dtype)
+    ref_grad = cross_entropy_backward(z.double().numpy(), t.numpy(), dl.double().numpy())
+    floor = 4e-6 * np.abs(dl.double().numpy())[:, None]
+    _, grad = _run(z.to(gpu), t.to(gpu), dl.to(gpu))
+    _check("grad", grad, ref_grad, dtype, floor)
+    _, grad_in = _run(z.to(gpu), t.to(gpu), dl.to(gpu), inplace=True)
+    assert torch.equal(grad_in, grad)
