@@ -25,7 +25,12 @@ namespace mi {
 
 namespace {
 
-constexpr int XT = 256;  // threads per workgroup
+constexpr int XT = 256;  // threads per workgroup (backward)
+// Forward: XFT threads per row, XFU 16-byte vectors per thread in flight.  At
+// config 5's [8192, 50257] bf16, 512 x 4 (or x 2) took ~124 us, against 131
+// for 256 x 4 or x 8, 138 for 128 x 8 and 144 for 1024 x 2.
+constexpr int XFT = 512;
+constexpr int XFU = 4;
 
 template <int DT>
 struct Vec16 {
@@ -81,7 +86,7 @@ __device__ __forceinline__ void row_split(const void* row, int64_t vocab, int64_
 }
 
 template <int DT>
-__global__ __launch_bounds__(XT) void xent_fwd_kernel(const void* logits, int64_t row_stride,
+__global__ __launch_bounds__(XFT) void xent_fwd_kernel(const void* logits, int64_t row_stride,
                                                       int64_t vocab, const int64_t* target,
                                                       void* loss, float* lse_out) {
   typedef typename Store<DT>::type T;
@@ -91,26 +96,25 @@ __global__ __launch_bounds__(XT) void xent_fwd_kernel(const void* logits, int64_
   int64_t head, nvec, tail0;
   row_split<DT>(z, vocab, head, nvec, tail0);
   MaxSum ms;
-  for (int64_t i = tid; i < head; i += XT) {
+  for (int64_t i = tid; i < head; i += XFT) {
     const float x = Store<DT>::ld(z, i);
     ms.add_group(&x, 1);
   }
-  for (int64_t i = tail0 + tid; i < vocab; i += XT) {
+  for (int64_t i = tail0 + tid; i < vocab; i += XFT) {
     const float x = Store<DT>::ld(z, i);
     ms.add_group(&x, 1);
   }
   const u32x4* zv = (const u32x4*)(z + head);
   constexpr int N = Vec16<DT>::N;
-  // U vectors per thread in flight; the last partial round is guarded
-  constexpr int U = 4;
-  for (int64_t i0 = tid; i0 < nvec; i0 += U * XT) {
-    u32x4 v[U];
+  // XFU vectors per thread in flight; the last partial round is guarded
+  for (int64_t i0 = tid; i0 < nvec; i0 += XFU * XFT) {
+    u32x4 v[XFU];
 #pragma unroll
-    for (int u = 0; u < U; ++u)
-      if (i0 + u * XT < nvec) v[u] = __builtin_nontemporal_load(zv + i0 + u * XT);
+    for (int u = 0; u < XFU; ++u)
+      if (i0 + u * XFT < nvec) v[u] = __builtin_nontemporal_load(zv + i0 + u * XFT);
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      if (i0 + u * XT < nvec) {
+    for (int u = 0; u < XFU; ++u) {
+      if (i0 + u * XFT < nvec) {
         float x[N];
 #pragma unroll
         for (int e = 0; e < N; ++e) x[e] = elem<DT>(v[u], e);
@@ -122,7 +126,7 @@ __global__ __launch_bounds__(XT) void xent_fwd_kernel(const void* logits, int64_
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1)
     ms.merge(__shfl_xor(ms.m, off, 64), __shfl_xor(ms.s, off, 64));
-  __shared__ float sm[XT / 64], ss[XT / 64];
+  __shared__ float sm[XFT / 64], ss[XFT / 64];
   if ((tid & 63) == 0) {
     sm[tid >> 6] = ms.m;
     ss[tid >> 6] = ms.s;
@@ -130,7 +134,7 @@ __global__ __launch_bounds__(XT) void xent_fwd_kernel(const void* logits, int64_
   __syncthreads();
   if (tid == 0) {
     MaxSum t;
-    for (int w = 0; w < XT / 64; ++w) t.merge(sm[w], ss[w]);
+    for (int w = 0; w < XFT / 64; ++w) t.merge(sm[w], ss[w]);
     const int64_t tg = target[r];
     const float zt = (tg >= 0 && tg < vocab) ? Store<DT>::ld(z, tg) - t.m : 0.f;
     const float logs = __logf(t.s);
@@ -312,7 +316,7 @@ __global__ __launch_bounds__(XT) void xent_bwd_flat_kernel(const void* logits, u
 }  // namespace
 
 hipError_t launch_xent_fwd(int dtype, const XentArgs& a, hipStream_t st) {
-  const dim3 grid((unsigned)a.rows), block(XT);
+  const dim3 grid((unsigned)a.rows), block(XFT);
   if (dtype == 0)
     hipLaunchKernelGGL(xent_fwd_kernel<0>, grid, block, 0, st, a.logits, a.row_stride, a.vocab,
                        a.target, a.loss, a.lse);
