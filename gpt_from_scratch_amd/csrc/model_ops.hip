@@ -27,8 +27,9 @@ namespace {
 
 constexpr int XT = 256;  // threads per workgroup (backward)
 // Forward: XFT threads per row, XFU 16-byte vectors per thread in flight.  At
-// config 5's [8192, 50257] bf16, 512 x 4 (or x 2) took ~124 us, against 131
-// for 256 x 4 or x 8, 138 for 128 x 8 and 144 for 1024 x 2.
+// config 5's [8192, 50257] bf16, timed right after a backward pass, 512 x 4 (or
+// x 2) took ~124 us, against 131 for 256 x 4 or x 8, 138 for 128 x 8 and 144
+// for 1024 x 2.
 constexpr int XFT = 512;
 constexpr int XFU = 4;
 
