@@ -74,21 +74,25 @@ __device__ __forceinline__ void load_angles(const void* tab, int64_t i, float (&
 // 16-byte vector path: requires unit dim strides, D % VEC == 0, 16-byte
 // aligned rows, unit pair stride in the tables and table rows (and bases)
 // aligned to the angle vector.  NTEN tensors (q, or q and k) per lane.  A
-// workgroup covers U * 256 consecutive items, lane i items i, i + 256, ...
-// (each pass of 256 lanes reads whole 1 KiB segments); every lane issues all
+// workgroup covers U * ROPE_T consecutive items, lane i items i, i + ROPE_T, ...
+// (each pass of its lanes reads whole 1 KiB segments); every lane issues all
 // its loads (tables and the U chunks of both tensors) before its first store,
 // so U * NTEN 16-byte loads per lane are in flight at once.
+// Threads per workgroup of the vector path: at config 2 from HBM 9.2 us,
+// against 9.5-9.8 us with 128, 512 or 1024 threads.
+constexpr uint32_t ROPE_T = 256;
+
 template <int XDT, int TDT, int NTEN, int U>
-__global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a, RopeDivs dv, uint32_t total) {
+__global__ __launch_bounds__(ROPE_T) void rope_vec_kernel(RopeArgs a, RopeDivs dv, uint32_t total) {
   constexpr int VEC = (XDT == 0) ? 4 : 8;  // elements per lane and tensor
   constexpr int NP = VEC / 2;               // pairs per lane
-  const uint32_t first = blockIdx.x * (256u * U) + threadIdx.x;
+  const uint32_t first = blockIdx.x * (ROPE_T * U) + threadIdx.x;
   u32x4 x[U][NTEN];
   float cs[U][NP], sn[U][NP];
   int64_t out_off[U][NTEN];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const uint32_t item = first + 256u * u;
+    const uint32_t item = first + ROPE_T * u;
     if (item >= total) continue;
     uint32_t r = fdiv(item, dv.C);
     const uint32_t cidx = item - r * dv.C.d;
@@ -112,7 +116,7 @@ __global__ __launch_bounds__(256) void rope_vec_kernel(RopeArgs a, RopeDivs dv, 
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    if (first + 256u * u >= total) continue;
+    if (first + ROPE_T * u >= total) continue;
 #pragma unroll
     for (int t = 0; t < NTEN; ++t) {
       u32x4 y;
@@ -192,7 +196,7 @@ hipError_t rope_launch(const RopeArgs& a, bool vec, hipStream_t st) {
     // flight at once): 9.3 us from HBM against 10.7 us for the grid-stride loop
     // over 2048 workgroups; two items 10.6, six 10.2, eight 12.2 us
     constexpr int U = 4;
-    const dim3 grid((uint32_t)((total + 256 * U - 1) / (256 * U))), block(256);
+    const dim3 grid((uint32_t)((total + ROPE_T * U - 1) / (ROPE_T * U))), block(ROPE_T);
     if (a.ntensors == 2)
       hipLaunchKernelGGL((rope_vec_kernel<XDT, TDT, 2, U>), grid, block, 0, st, a, dv, (uint32_t)total);
     else
