@@ -403,7 +403,9 @@ def gpt_train(dev, steps=20, warmup=3):
     the same fp32 run against one that rounds P to bf16 before P V, as the
     reference's kernel does (core/myFlashAttn.py:717).  A kernel that rounds
     like the reference moves the loss by about as much; the bound allows three
-    times that plus 1e-3."""
+    times that plus 1e-3.  Also reported: the kernel step with the residual
+    adds as separate torch adds, and with the projections' weight gradients
+    left to autograd's accumulation into the flat gradient buffer."""
     import torch
     from gpt_from_scratch_amd.harness import GPTConfig, SoftmaxCrossEntropy, train
 
@@ -435,6 +437,8 @@ def gpt_train(dev, steps=20, warmup=3):
     _progress("config 5: eager train run done")
     _, sep_tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup,
                        fuse_add_norm=False)
+    _, autograd_tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup,
+                            gemm_grad_accumulate=False)
     # parity runs: 20 steps each from the initial parameters
     kern, _ = train(cfg, 8, 1024, steps=20, seed=5, device=dev)
     ref, _ = train(cfg, 8, 1024, steps=20, seed=5, device=dev, attention=eager_attention,
@@ -452,6 +456,7 @@ def gpt_train(dev, steps=20, warmup=3):
             "ms_per_step": round(8 * 1024 / tps * 1e3, 3),
             "tokens_per_s_eager": round(eager_tps, 1),
             "tokens_per_s_separate_adds": round(sep_tps, 1),
+            "tokens_per_s_autograd_grad_adds": round(autograd_tps, 1),
             "eager": "attention as torch matmul/softmax (fp32 math); loss, RMSNorm, SwiGLU and "
                      "the AdamW step as the reference's eager torch ops",
             "loss_first": round(losses[0], 4), "loss_last": round(losses[-1], 4),

@@ -55,6 +55,39 @@ from ..position_embeddings import RotaryEmbedding
 from ..rope import apply_rope_qk
 
 
+class _LinearGradInto(torch.autograd.Function):
+    """``F.linear(x, w)`` whose weight gradient the GEMM accumulates itself into
+    ``w.grad`` when that already exists (the optimizer's flat gradient buffer):
+    ``w.grad.addmm_(gy^T, x)``, beta = 1 in the GEMM's epilogue, instead of a
+    separate gradient tensor that autograd then adds into the buffer with one
+    more pass over it.  Without a usable ``w.grad`` (none yet, another dtype or
+    layout, or a double backward) the gradient is returned as F.linear's is."""
+
+    @staticmethod
+    def forward(ctx, x, w):
+        ctx.save_for_backward(x, w)
+        return F.linear(x, w)
+
+    @staticmethod
+    def backward(ctx, gy):
+        x, w = ctx.saved_tensors
+        gx = gy.matmul(w) if ctx.needs_input_grad[0] else None
+        if not ctx.needs_input_grad[1]:
+            return gx, None
+        gy2 = gy.reshape(-1, gy.shape[-1])
+        x2 = x.reshape(-1, x.shape[-1])
+        g = w.grad
+        if (g is None or torch.is_grad_enabled() or g.dtype != gy.dtype or g.shape != w.shape
+                or not g.is_contiguous()):
+            return gx, gy2.t().matmul(x2)
+        g.addmm_(gy2.t(), x2)
+        return gx, None
+
+
+def _linear_into_grad(x, w):
+    return _LinearGradInto.apply(x, w)
+
+
 @dataclasses.dataclass
 class GPTConfig:
     """Defaults follow train.py:15-26 and BASELINE config 5 (vocab 50257)."""
@@ -93,8 +126,9 @@ class RMSNorm(nn.Module):
 
 
 class Attention(nn.Module):
-    def __init__(self, cfg: GPTConfig, device, attention=None, rope=None):
+    def __init__(self, cfg: GPTConfig, device, attention=None, rope=None, linear=F.linear):
         super().__init__()
+        self.lin = linear
         self.heads = cfg.num_attention_heads
         self.head_dim = cfg.hidden_size // cfg.num_attention_heads
         self.qkv = _xavier(3 * cfg.hidden_size, cfg.hidden_size, device)
@@ -111,41 +145,43 @@ class Attention(nn.Module):
         S, B, _ = x.shape
         if self.fused:
             cos, sin = self.rotary(x, seq_len=S)
-            return F.linear(attention_block(F.linear(x, self.qkv), cos, sin, self.heads),
+            return self.lin(attention_block(self.lin(x, self.qkv), cos, sin, self.heads),
                             self.out)
-        qkv = F.linear(x, self.qkv).view(S, B, 3, self.heads, self.head_dim)
+        qkv = self.lin(x, self.qkv).view(S, B, 3, self.heads, self.head_dim)
         q, k, v = qkv.unbind(2)
         cos, sin = self.rotary(q, seq_len=S)
         q, k = self.rope(q, k, cos, sin)
         o = self.attention(q.permute(1, 2, 0, 3), k.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3))
         o = o.permute(2, 0, 1, 3).reshape(S, B, -1)
-        return F.linear(o, self.out)
+        return self.lin(o, self.out)
 
 
 class SwiGLU(nn.Module):
     """The HIP activation kernels by default; `eager=True` runs the reference's ops."""
 
-    def __init__(self, cfg: GPTConfig, device, eager=False):
+    def __init__(self, cfg: GPTConfig, device, eager=False, linear=F.linear):
         super().__init__()
         self.eager = eager
+        self.lin = linear
         self.gate_up = _xavier(2 * cfg.intermediate_size, cfg.hidden_size, device)
         self.down = _xavier(cfg.hidden_size, cfg.intermediate_size, device)
 
     def forward(self, x):
-        gate_up = F.linear(x, self.gate_up)
+        gate_up = self.lin(x, self.gate_up)
         if not self.eager:
-            return F.linear(swiglu(gate_up), self.down)
+            return self.lin(swiglu(gate_up), self.down)
         gate, up = gate_up.chunk(2, dim=-1)
-        return F.linear(F.silu(gate) * up, self.down)
+        return self.lin(F.silu(gate) * up, self.down)
 
 
 class Block(nn.Module):
-    def __init__(self, cfg: GPTConfig, device, attention=None, rope=None, eager_ops=False):
+    def __init__(self, cfg: GPTConfig, device, attention=None, rope=None, eager_ops=False,
+                 linear=F.linear):
         super().__init__()
         self.norm1 = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager=eager_ops)
-        self.attn = Attention(cfg, device, attention, rope)
+        self.attn = Attention(cfg, device, attention, rope, linear)
         self.norm2 = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager=eager_ops)
-        self.mlp = SwiGLU(cfg, device, eager=eager_ops)
+        self.mlp = SwiGLU(cfg, device, eager=eager_ops, linear=linear)
 
     def forward(self, x):
         x = x + self.attn(self.norm1(x))
@@ -156,14 +192,18 @@ class GPT(nn.Module):
     """input ids [B, S] -> logits [S, B, V]."""
 
     def __init__(self, cfg: GPTConfig, device, attention=None, rope=None, eager_ops=False,
-                 fuse_add_norm=True):
+                 fuse_add_norm=True, gemm_grad_accumulate=True):
         super().__init__()
         self.cfg = cfg
+        # the projections' weight gradients accumulated by their GEMMs (not with
+        # eager_ops, which keeps the reference's ops throughout)
+        self.lin = _linear_into_grad if gemm_grad_accumulate and not eager_ops else F.linear
         emb = torch.empty(cfg.vocab_size, cfg.hidden_size, device=device, dtype=torch.float32)
         nn.init.xavier_uniform_(emb)
         self.embedding = nn.Parameter(emb)
         self.blocks = nn.ModuleList(
-            [Block(cfg, device, attention, rope, eager_ops) for _ in range(cfg.num_layers)])
+            [Block(cfg, device, attention, rope, eager_ops, self.lin)
+             for _ in range(cfg.num_layers)])
         self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager=eager_ops)
         self.head = _xavier(cfg.vocab_size, cfg.hidden_size, device)
         self.eager_ops = eager_ops
@@ -174,7 +214,7 @@ class GPT(nn.Module):
         if not self.fuse_add_norm:
             for blk in self.blocks:
                 x = blk(x)
-            return F.linear(self.norm(x), self.head)
+            return self.lin(self.norm(x), self.head)
         # The same blocks with each residual add fused into the RMSNorm that
         # reads its sum: this block's norm2, then the next block's norm1 (or
         # the final norm); `h` is the normalised input of the next branch.
@@ -183,7 +223,7 @@ class GPT(nn.Module):
             x, h = add_rms_norm(x, blk.attn(h), blk.norm2.weight, blk.norm2.eps)
             nxt = self.blocks[i + 1].norm1 if i + 1 < len(self.blocks) else self.norm
             x, h = add_rms_norm(x, blk.mlp(h), nxt.weight, nxt.eps)
-        return F.linear(h, self.head)
+        return self.lin(h, self.head)
 
 
 class SoftmaxCrossEntropy(torch.autograd.Function):
@@ -259,17 +299,19 @@ def synthetic_batch(batch, seq, vocab, seed, device):
 
 
 def train(cfg: GPTConfig, batch=8, seq=1024, steps=20, seed=5, device="cuda", attention=None,
-          rope=None, warmup=0, loss_fn=None, eager_ops=False, fuse_add_norm=True):
+          rope=None, warmup=0, loss_fn=None, eager_ops=False, fuse_add_norm=True,
+          gemm_grad_accumulate=True):
     """Build the model and optimizer from `seed`, run `warmup` untimed then
     `steps` timed train steps on one fixed synthetic batch.  Returns
     (losses, tokens_per_second).  `loss_fn(logits, target)` -> per-token loss
     defaults to the HIP cross entropy; `eager_ops` swaps the model's other HIP
     operators (RMSNorm, SwiGLU, the optimizer step) for the reference's eager
     op sequences; `fuse_add_norm=False` runs the residual adds as separate
-    torch adds in front of the RMSNorm kernels."""
+    torch adds in front of the RMSNorm kernels; `gemm_grad_accumulate=False`
+    leaves the projections' weight gradients to autograd's accumulation."""
     loss_fn = loss_fn or vocab_parallel_cross_entropy
     torch.manual_seed(seed)
-    model = GPT(cfg, device, attention, rope, eager_ops, fuse_add_norm)
+    model = GPT(cfg, device, attention, rope, eager_ops, fuse_add_norm, gemm_grad_accumulate)
     if eager_ops:
         opt = MixedPrecisionAdamW(model)
     else:

@@ -79,3 +79,36 @@ def test_config5_fused_add_norm_matches_separate_ops(gpu):
     sep, tps_s = train(cfg, batch=8, seq=1024, steps=4, seed=5, device=gpu, fuse_add_norm=False)
     print(f"config5 tokens/s fused add+norm {tps_f:.0f}, separate adds {tps_s:.0f}")
     assert fused == sep, (fused, sep)
+
+
+def test_config5_gemm_grad_accumulate_matches_autograd(gpu):
+    """The projections' weight gradients accumulated by their GEMMs into the
+    optimizer's flat gradient buffer (addmm with beta = 1) give the same losses,
+    bit for bit, as autograd's separate gradient plus in-place add into the
+    zeroed buffer (x + 0 = x)."""
+    torch.backends.cuda.matmul.allow_tf32 = False
+    cfg = GPTConfig()
+    acc, tps_a = train(cfg, batch=8, seq=1024, steps=4, seed=5, device=gpu)
+    sep, tps_s = train(cfg, batch=8, seq=1024, steps=4, seed=5, device=gpu,
+                       gemm_grad_accumulate=False)
+    print(f"config5 tokens/s GEMM-accumulated weight grads {tps_a:.0f}, autograd adds {tps_s:.0f}")
+    assert acc == sep, (acc, sep)
+
+
+def test_linear_grad_into_falls_back_without_buffer(gpu):
+    """Without an existing .grad the weight gradient is returned to autograd
+    (a leaf gets it as with F.linear); with one, it is accumulated in place."""
+    from gpt_from_scratch_amd.harness.gpt import _linear_into_grad
+    g = torch.Generator(device=gpu).manual_seed(3)
+    x = torch.randn(5, 3, 64, generator=g, device=gpu).to(torch.bfloat16).requires_grad_(True)
+    w = torch.randn(32, 64, generator=g, device=gpu).to(torch.bfloat16).requires_grad_(True)
+    gy = torch.randn(5, 3, 32, generator=g, device=gpu).to(torch.bfloat16)
+    y = _linear_into_grad(x, w)
+    y.backward(gy)
+    xr, wr = x.detach().clone().requires_grad_(True), w.detach().clone().requires_grad_(True)
+    torch.nn.functional.linear(xr, wr).backward(gy)
+    assert torch.equal(x.grad, xr.grad)
+    torch.testing.assert_close(w.grad.float(), wr.grad.float(), rtol=2 ** -7, atol=1e-3)
+    first = w.grad.clone()
+    _linear_into_grad(x.detach(), w).backward(gy)  # accumulated into the existing grad
+    torch.testing.assert_close(w.grad.float(), 2 * first.float(), rtol=2 ** -7, atol=1e-2)
