@@ -300,7 +300,7 @@ def synthetic_batch(batch, seq, vocab, seed, device):
 
 def train(cfg: GPTConfig, batch=8, seq=1024, steps=20, seed=5, device="cuda", attention=None,
           rope=None, warmup=0, loss_fn=None, eager_ops=False, fuse_add_norm=True,
-          gemm_grad_accumulate=True):
+          gemm_grad_accumulate=True, regions=None):
     """Build the model and optimizer from `seed`, run `warmup` untimed then
     `steps` timed train steps on one fixed synthetic batch.  Returns
     (losses, tokens_per_second).  `loss_fn(logits, target)` -> per-token loss
@@ -308,7 +308,8 @@ def train(cfg: GPTConfig, batch=8, seq=1024, steps=20, seed=5, device="cuda", at
     operators (RMSNorm, SwiGLU, the optimizer step) for the reference's eager
     op sequences; `fuse_add_norm=False` runs the residual adds as separate
     torch adds in front of the RMSNorm kernels; `gemm_grad_accumulate=False`
-    leaves the projections' weight gradients to autograd's accumulation."""
+    leaves the projections' weight gradients to autograd's accumulation;
+    `regions` (resume() / pause()) brackets the timed steps for a profiler."""
     loss_fn = loss_fn or vocab_parallel_cross_entropy
     torch.manual_seed(seed)
     model = GPT(cfg, device, attention, rope, eager_ops, fuse_add_norm, gemm_grad_accumulate)
@@ -332,10 +333,33 @@ def train(cfg: GPTConfig, batch=8, seq=1024, steps=20, seed=5, device="cuda", at
     for _ in range(warmup):
         one_step()
     torch.cuda.synchronize()
+    if regions is not None:
+        regions.resume()
     losses = []
     t0 = time.perf_counter()
     for _ in range(steps):
         losses.append(one_step())
     torch.cuda.synchronize()
     dt = time.perf_counter() - t0
+    if regions is not None:
+        regions.pause()
     return [float(x) for x in losses], batch * seq * steps / dt
+
+
+if __name__ == "__main__":
+    # `python -m gpt_from_scratch_amd.harness.gpt --steps 10 --warmup 3`: the
+    # config-5 train step alone, timed steps inside profiler regions
+    import argparse
+    import json
+
+    from ..profiler_regions import ProfilerRegions
+
+    ap = argparse.ArgumentParser(description="config-5 GPT train step on the HIP kernels")
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    args = ap.parse_args()
+    losses, tps = train(GPTConfig(), 8, 1024, steps=args.steps, seed=5, device="cuda",
+                        warmup=args.warmup, regions=ProfilerRegions())
+    print(json.dumps({"tokens_per_s": round(tps, 1), "ms_per_step": round(8 * 1024 / tps * 1e3, 3),
+                      "steps": args.steps, "warmup": args.warmup,
+                      "loss_last": round(losses[-1], 4)}), flush=True)
