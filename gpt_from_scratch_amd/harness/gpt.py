@@ -344,22 +344,3 @@ def train(cfg: GPTConfig, batch=8, seq=1024, steps=20, seed=5, device="cuda", at
     if regions is not None:
         regions.pause()
     return [float(x) for x in losses], batch * seq * steps / dt
-
-
-if __name__ == "__main__":
-    # `python -m gpt_from_scratch_amd.harness.gpt --steps 10 --warmup 3`: the
-    # config-5 train step alone, timed steps inside profiler regions
-    import argparse
-    import json
-
-    from ..profiler_regions import ProfilerRegions
-
-    ap = argparse.ArgumentParser(description="config-5 GPT train step on the HIP kernels")
-    ap.add_argument("--steps", type=int, default=10)
-    ap.add_argument("--warmup", type=int, default=3)
-    args = ap.parse_args()
-    losses, tps = train(GPTConfig(), 8, 1024, steps=args.steps, seed=5, device="cuda",
-                        warmup=args.warmup, regions=ProfilerRegions())
-    print(json.dumps({"tokens_per_s": round(tps, 1), "ms_per_step": round(8 * 1024 / tps * 1e3, 3),
-                      "steps": args.steps, "warmup": args.warmup,
-                      "loss_last": round(losses[-1], 4)}), flush=True)
