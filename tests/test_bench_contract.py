@@ -92,3 +92,12 @@ def test_summarize_reads_rocprof_csv(tmp_path):
     assert "| k_bwd<BF16, 64> [grid 256] | 2 | 56.000 | 55.000 | 57.000 | 58.000 | 0 |" in lines
     assert "| k_fwd [grid 512] | 1 | 21.000 | 21.000 | 21.000 | - | 16 |" in lines
     assert "| k_bwd<BF16, 64> [grid 256] | 2 | 101.0 | 100.0 | 102.0 |" in lines
+
+
+def test_profiler_regions_are_harmless_without_a_profiler():
+    """roctxProfilerResume / Pause without a profiler attached (or without the
+    roctx library) do nothing and raise nothing."""
+    from gpt_from_scratch_amd.profiler_regions import ProfilerRegions
+    r = ProfilerRegions()
+    r.resume()
+    r.pause()
