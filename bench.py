@@ -297,6 +297,30 @@ def model_ops_bench(dev, lib):
                      "traffic": read_traffic(name, "traffic_model_ops_c5.txt")}
     del grad, master, m1, m2, prm
     torch.cuda.empty_cache()
+
+    # What plain streaming reaches on this board, as a yardstick for the
+    # fractions above: torch's device-to-device copy of 1 GiB (1 GiB read and
+    # 1 GiB written, far past the cache), i.e. the mixed read/write ceiling of a
+    # library kernel that does no arithmetic.
+    src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev).normal_(generator=gen)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(5):
+        dst.copy_(src)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) / 5 * 1e3
+    nbytes = 2 * src.numel() * 2
+    gbps = nbytes / (us * 1e-6) / 1e9
+    out["copy_reference"] = {"kernel": "torch Tensor.copy_ (not this build's)", "avg_us": round(us, 2),
+                             "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                             "frac": round(gbps / PEAK_HBM_GBPS, 4), "bytes": nbytes}
+    del src, dst
+    torch.cuda.empty_cache()
     return out
 
 
