@@ -427,6 +427,11 @@ def gpt_train(dev, steps=20, warmup=3):
         return rot(q), rot(k)
 
     cfg = GPTConfig()
+    # Start from an empty allocator cache, as a training process does: with the
+    # blocks the earlier measurements left cached, the first train run measured
+    # 473-517k tokens/s against 551-554k (the later variants were unaffected).
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
     losses, tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup)
     _progress("config 5: kernel train run done")
     _, eager_tps = train(cfg, 8, 1024, steps=steps, seed=5, device=dev, warmup=warmup,
