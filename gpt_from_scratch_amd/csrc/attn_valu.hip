@@ -44,6 +44,7 @@ __global__ __launch_bounds__(64) void attn_fwd_valu_kernel(AttnArgs a) {
   const T* kp = (const T*)a.k.ptr + b * a.k.sb + h * a.k.sh;
   const T* vp = (const T*)a.v.ptr + b * a.v.sb + h * a.v.sh;
 
+  constexpr int SUNROLL = D <= 64 ? VT : 4;
   float q[D], o[D];
 #pragma unroll
   for (int d = 0; d < D; ++d) {
@@ -59,9 +60,12 @@ __global__ __launch_bounds__(64) void attn_fwd_valu_kernel(AttnArgs a) {
     stage_rows<DT, D>(Kt, kp, a.k.ss, kv0, S);
     stage_rows<DT, D>(Vt, vp, a.v.ss, kv0, S);
     __syncthreads();
+    // Scores of the tile in registers: the j loops unroll fully up to D = 64
+    // (a partially unrolled loop indexes s[] at run time and puts it in
+    // scratch memory); at D = 128, q and o alone fill the register file.
     float s[VT];
     float mx = -INFINITY;
-#pragma unroll 4
+#pragma unroll SUNROLL
     for (int j = 0; j < VT; ++j) {
       const int kv = kv0 + j;
       float acc = 0.f;
@@ -77,7 +81,7 @@ __global__ __launch_bounds__(64) void attn_fwd_valu_kernel(AttnArgs a) {
     l *= alpha;
 #pragma unroll
     for (int d = 0; d < D; ++d) o[d] *= alpha;
-#pragma unroll 4
+#pragma unroll SUNROLL
     for (int j = 0; j < VT; ++j) {
       const float p = exp2f(s[j] - m_new);
       l += p;
