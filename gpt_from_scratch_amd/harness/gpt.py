@@ -140,16 +140,28 @@ class Attention(nn.Module):
         # With the HIP kernels on both sides, the block runs fused: no relayout
         # copies of q/k/v, O or the qkv gradient.
         self.fused = attention is None and rope is None
+        self._tables_key = None
+        self._tables = None
+
+    def tables(self, x, S):
+        """RotaryEmbedding's tables in x's dtype.  It casts its fp32 tables on
+        every call (position_embeddings.py, as the reference's does); the
+        tables never change, so the cast is kept per (dtype, length)."""
+        key = (x.dtype, S)
+        if key != self._tables_key:
+            self._tables = self.rotary(x, seq_len=S)
+            self._tables_key = key
+        return self._tables
 
     def forward(self, x):  # x: [S, B, H]
         S, B, _ = x.shape
         if self.fused:
-            cos, sin = self.rotary(x, seq_len=S)
+            cos, sin = self.tables(x, S)
             return self.lin(attention_block(self.lin(x, self.qkv), cos, sin, self.heads),
                             self.out)
         qkv = self.lin(x, self.qkv).view(S, B, 3, self.heads, self.head_dim)
         q, k, v = qkv.unbind(2)
-        cos, sin = self.rotary(q, seq_len=S)
+        cos, sin = self.tables(q, S)
         q, k = self.rope(q, k, cos, sin)
         o = self.attention(q.permute(1, 2, 0, 3), k.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3))
         o = o.permute(2, 0, 1, 3).reshape(S, B, -1)
