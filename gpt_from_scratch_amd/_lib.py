@@ -27,7 +27,8 @@ EXPORTED = ("mi_version", "mi_status_str", "mi_last_error", "mi_attn_fwd", "mi_a
             "mi_rope", "mi_rope_qk", "mi_xent_fwd", "mi_xent_bwd", "mi_rmsnorm_fwd",
             "mi_rmsnorm_bwd_workspace", "mi_rmsnorm_bwd", "mi_swiglu_fwd", "mi_swiglu_bwd",
             "mi_adamw_workspace", "mi_grad_sumsq", "mi_adamw_step", "mi_attn_bwd_noalloc",
-            "mi_rmsnorm_add_fwd", "mi_rmsnorm_add_bwd", "mi_attn_bwd_rope")
+            "mi_rmsnorm_add_fwd", "mi_rmsnorm_add_bwd", "mi_attn_bwd_rope",
+            "mi_rmsnorm_bwd_acc", "mi_rmsnorm_add_bwd_acc")
 
 # B*H*S limit of mi_attn_bwd_noalloc (its static workspace array), include/mi_attn.h
 NOALLOC_MAX_ROWS = 1 << 20
@@ -97,6 +98,10 @@ def _declare(lib):
     lib.mi_rmsnorm_add_bwd.restype = i
     lib.mi_rmsnorm_add_bwd.argtypes = [i, i, i64, i64, p, i64, p, p, p, i64, p, i64, p, i64, p,
                                        p, i64, p]
+    lib.mi_rmsnorm_bwd_acc.restype = i
+    lib.mi_rmsnorm_bwd_acc.argtypes = lib.mi_rmsnorm_bwd.argtypes
+    lib.mi_rmsnorm_add_bwd_acc.restype = i
+    lib.mi_rmsnorm_add_bwd_acc.argtypes = lib.mi_rmsnorm_add_bwd.argtypes
     lib.mi_swiglu_fwd.restype = i
     lib.mi_swiglu_fwd.argtypes = [i, i64, i64, p, i64, p, i64, p]
     lib.mi_swiglu_bwd.restype = i
@@ -331,16 +336,18 @@ def rmsnorm_workspace(rows: int, hidden: int) -> int:
     return int(lib().mi_rmsnorm_bwd_workspace(rows, hidden))
 
 
-def rmsnorm_bwd(x, weight, rstd, dy, dx, dweight, workspace):
-    """Enqueue the RMSNorm backward: dx (x's shape and dtype), dweight [hidden]."""
+def rmsnorm_bwd(x, weight, rstd, dy, dx, dweight, workspace, accumulate=False):
+    """Enqueue the RMSNorm backward: dx (x's shape and dtype), dweight [hidden]
+    (added to its contents with `accumulate`)."""
     _require_gpu(x, weight, rstd, dy, dx, dweight, workspace)
     rows, xs = _rows(x)
     _, dys = _rows(dy)
     _, dxs = _rows(dx)
-    st = lib().mi_rmsnorm_bwd(dtype_code(x), dtype_code(weight), rows, x.shape[-1], _ptr(x), xs,
-                              _ptr(weight), _ptr(rstd), _ptr(dy), dys, _ptr(dx), dxs,
-                              _ptr(dweight), _ptr(workspace), workspace.numel(), _stream(x))
-    _check(st, "mi_rmsnorm_bwd")
+    fn = lib().mi_rmsnorm_bwd_acc if accumulate else lib().mi_rmsnorm_bwd
+    st = fn(dtype_code(x), dtype_code(weight), rows, x.shape[-1], _ptr(x), xs,
+            _ptr(weight), _ptr(rstd), _ptr(dy), dys, _ptr(dx), dxs,
+            _ptr(dweight), _ptr(workspace), workspace.numel(), _stream(x))
+    _check(st, "mi_rmsnorm_bwd_acc" if accumulate else "mi_rmsnorm_bwd")
 
 
 def rmsnorm_add_fwd(x, res, weight, eps: float, sum_out, y, rstd):
@@ -358,20 +365,21 @@ def rmsnorm_add_fwd(x, res, weight, eps: float, sum_out, y, rstd):
     _check(st, "mi_rmsnorm_add_fwd")
 
 
-def rmsnorm_add_bwd(sum_in, weight, rstd, dy, dsum, dx, dweight, workspace):
+def rmsnorm_add_bwd(sum_in, weight, rstd, dy, dsum, dx, dweight, workspace, accumulate=False):
     """Enqueue the backward of rmsnorm_add_fwd: dx = norm backward over sum_in
-    plus dsum (the gradient of x and of res), dweight [hidden]."""
+    plus dsum (the gradient of x and of res), dweight [hidden] (added to its
+    contents with `accumulate`)."""
     _require_gpu(sum_in, weight, rstd, dy, dsum, dx, dweight, workspace)
     rows, xs = _rows(sum_in)
     _, dys = _rows(dy)
     drows, dss = _rows(dsum)
     _, dxs = _rows(dx)
     assert drows == rows and dsum.dtype == sum_in.dtype
-    st = lib().mi_rmsnorm_add_bwd(dtype_code(sum_in), dtype_code(weight), rows,
-                                  sum_in.shape[-1], _ptr(sum_in), xs, _ptr(weight), _ptr(rstd),
-                                  _ptr(dy), dys, _ptr(dsum), dss, _ptr(dx), dxs, _ptr(dweight),
-                                  _ptr(workspace), workspace.numel(), _stream(sum_in))
-    _check(st, "mi_rmsnorm_add_bwd")
+    fn = lib().mi_rmsnorm_add_bwd_acc if accumulate else lib().mi_rmsnorm_add_bwd
+    st = fn(dtype_code(sum_in), dtype_code(weight), rows, sum_in.shape[-1], _ptr(sum_in), xs,
+            _ptr(weight), _ptr(rstd), _ptr(dy), dys, _ptr(dsum), dss, _ptr(dx), dxs,
+            _ptr(dweight), _ptr(workspace), workspace.numel(), _stream(sum_in))
+    _check(st, "mi_rmsnorm_add_bwd_acc" if accumulate else "mi_rmsnorm_add_bwd")
 
 
 def swiglu_fwd(gate_up, out):

@@ -131,7 +131,7 @@ mi::AttnArgs grad_args(int B, int H, int S, int D, int causal, float scale, cons
 
 extern "C" {
 
-int mi_version(void) { return (2 << 16) | 2; }
+int mi_version(void) { return (2 << 16) | 3; }
 
 const char* mi_status_str(mi_status s) {
   switch (s) {
@@ -663,7 +663,7 @@ static mi_status rms_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64
                          const float* rstd, const void* dy, int64_t dy_row_stride,
                          const void* dsum, int64_t dsum_row_stride, void* dx,
                          int64_t dx_row_stride, void* dweight, float* workspace,
-                         int64_t workspace_elems, void* stream) {
+                         int64_t workspace_elems, void* stream, bool dw_acc = false) {
   mi::RmsArgs a;
   if (mi_status st = rms_common(x_dtype, w_dtype, rows, hidden, x, x_row_stride, weight, a))
     return st;
@@ -691,6 +691,7 @@ static mi_status rms_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64
   a.dx = dx;
   a.dx_stride = dx_row_stride;
   a.dw = dweight;
+  a.dw_acc = dw_acc ? 1 : 0;
   a.partial = workspace;
   a.parts = (int)mi::rmsnorm_parts(rows);
   bool vec = rms_vec_ok(hidden, {{x, x_row_stride}, {dy, dy_row_stride}, {dx, dx_row_stride}},
@@ -722,6 +723,28 @@ mi_status mi_rmsnorm_add_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, i
   return rms_bwd(x_dtype, w_dtype, rows, hidden, sum, sum_row_stride, weight, rstd, dy,
                  dy_row_stride, dsum, dsum_row_stride, dx, dx_row_stride, dweight, workspace,
                  workspace_elems, stream);
+}
+
+mi_status mi_rmsnorm_bwd_acc(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                             const void* x, int64_t x_row_stride, const void* weight,
+                             const float* rstd, const void* dy, int64_t dy_row_stride, void* dx,
+                             int64_t dx_row_stride, void* dweight, float* workspace,
+                             int64_t workspace_elems, void* stream) {
+  return rms_bwd(x_dtype, w_dtype, rows, hidden, x, x_row_stride, weight, rstd, dy,
+                 dy_row_stride, nullptr, 0, dx, dx_row_stride, dweight, workspace,
+                 workspace_elems, stream, true);
+}
+
+mi_status mi_rmsnorm_add_bwd_acc(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows,
+                                 int64_t hidden, const void* sum, int64_t sum_row_stride,
+                                 const void* weight, const float* rstd, const void* dy,
+                                 int64_t dy_row_stride, const void* dsum, int64_t dsum_row_stride,
+                                 void* dx, int64_t dx_row_stride, void* dweight, float* workspace,
+                                 int64_t workspace_elems, void* stream) {
+  if (!dsum) return fail(MI_ERR_INVALID_ARGUMENT, "dsum: null pointer");
+  return rms_bwd(x_dtype, w_dtype, rows, hidden, sum, sum_row_stride, weight, rstd, dy,
+                 dy_row_stride, dsum, dsum_row_stride, dx, dx_row_stride, dweight, workspace,
+                 workspace_elems, stream, true);
 }
 
 static mi_status swiglu_common(mi_dtype dtype, int64_t rows, int64_t inter, const void* gu,

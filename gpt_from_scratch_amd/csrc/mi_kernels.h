@@ -105,6 +105,7 @@ struct RmsArgs {
   void* dw;        // [hidden], w's dtype
   float* partial;  // [parts, hidden] fp32 workspace of the backward
   int parts;
+  int dw_acc = 0;  // backward: dw += round_w(reduction) instead of dw = ...
   // Residual add fused in front (all null otherwise).  Forward: x is the
   // residual stream, res the branch output; sum = round_x(x + res) is written
   // and normalised.  Backward: x is that sum and dsum the gradient reaching

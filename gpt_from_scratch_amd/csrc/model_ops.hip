@@ -734,7 +734,9 @@ __global__ __launch_bounds__(256) void rmsnorm_dw_partial_scalar_kernel(RmsArgs 
 constexpr int DW_COLS = 16;
 
 // dw[col] = sum_p partial[p][col], p in increasing order within 16 strided
-// groups, then the 16 group sums in order.
+// groups, then the 16 group sums in order.  With dw_acc the sum, rounded to w's
+// dtype, is added to dw[col] (rounded again): autograd's accumulation of a
+// weight gradient into an existing .grad, two roundings included.
 template <int WDT>
 __global__ __launch_bounds__(16 * DW_COLS) void rmsnorm_dw_reduce_kernel(RmsArgs a) {
   typedef typename Store<WDT>::type TW;
@@ -752,6 +754,7 @@ __global__ __launch_bounds__(16 * DW_COLS) void rmsnorm_dw_reduce_kernel(RmsArgs
     float u = 0.f;
 #pragma unroll
     for (int k = 0; k < 16; ++k) u += red[k][cl];
+    if (a.dw_acc) u = Store<WDT>::ld((const TW*)a.dw, col) + round_to<WDT>(u);
     Store<WDT>::st((TW*)a.dw, col, u);
   }
 }

@@ -110,15 +110,16 @@ def _xavier(out_features, in_features, device):
 class RMSNorm(nn.Module):
     """The HIP kernels by default; `eager=True` runs the reference's op sequence."""
 
-    def __init__(self, hidden_size, eps, device, eager=False):
+    def __init__(self, hidden_size, eps, device, eager=False, grad_into=False):
         super().__init__()
         self.eps = eps
         self.eager = eager
+        self.grad_into = grad_into  # weight gradient added into .grad by the kernel
         self.weight = nn.Parameter(torch.ones(hidden_size, device=device, dtype=torch.float32))
 
     def forward(self, x):
         if not self.eager:
-            return rms_norm(x, self.weight, self.eps)
+            return rms_norm(x, self.weight, self.eps, self.grad_into)
         dtype = x.dtype
         xf = x.float()
         xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
@@ -188,11 +189,11 @@ class SwiGLU(nn.Module):
 
 class Block(nn.Module):
     def __init__(self, cfg: GPTConfig, device, attention=None, rope=None, eager_ops=False,
-                 linear=F.linear):
+                 linear=F.linear, grad_into=False):
         super().__init__()
-        self.norm1 = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager=eager_ops)
+        self.norm1 = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager_ops, grad_into)
         self.attn = Attention(cfg, device, attention, rope, linear)
-        self.norm2 = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager=eager_ops)
+        self.norm2 = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager_ops, grad_into)
         self.mlp = SwiGLU(cfg, device, eager=eager_ops, linear=linear)
 
     def forward(self, x):
@@ -207,16 +208,18 @@ class GPT(nn.Module):
                  fuse_add_norm=True, gemm_grad_accumulate=True):
         super().__init__()
         self.cfg = cfg
-        # the projections' weight gradients accumulated by their GEMMs (not with
-        # eager_ops, which keeps the reference's ops throughout)
-        self.lin = _linear_into_grad if gemm_grad_accumulate and not eager_ops else F.linear
+        # the projections' weight gradients accumulated by their GEMMs, and the
+        # norms' by their backward kernels, into the optimizer's gradient buffer
+        # (not with eager_ops, which keeps the reference's ops throughout)
+        into = gemm_grad_accumulate and not eager_ops
+        self.lin = _linear_into_grad if into else F.linear
         emb = torch.empty(cfg.vocab_size, cfg.hidden_size, device=device, dtype=torch.float32)
         nn.init.xavier_uniform_(emb)
         self.embedding = nn.Parameter(emb)
         self.blocks = nn.ModuleList(
-            [Block(cfg, device, attention, rope, eager_ops, self.lin)
+            [Block(cfg, device, attention, rope, eager_ops, self.lin, into)
              for _ in range(cfg.num_layers)])
-        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager=eager_ops)
+        self.norm = RMSNorm(cfg.hidden_size, cfg.rms_norm_eps, device, eager_ops, into)
         self.head = _xavier(cfg.vocab_size, cfg.hidden_size, device)
         self.eager_ops = eager_ops
         self.fuse_add_norm = fuse_add_norm and not eager_ops
@@ -232,9 +235,10 @@ class GPT(nn.Module):
         # the final norm); `h` is the normalised input of the next branch.
         h = self.blocks[0].norm1(x)
         for i, blk in enumerate(self.blocks):
-            x, h = add_rms_norm(x, blk.attn(h), blk.norm2.weight, blk.norm2.eps)
+            x, h = add_rms_norm(x, blk.attn(h), blk.norm2.weight, blk.norm2.eps,
+                                blk.norm2.grad_into)
             nxt = self.blocks[i + 1].norm1 if i + 1 < len(self.blocks) else self.norm
-            x, h = add_rms_norm(x, blk.mlp(h), nxt.weight, nxt.eps)
+            x, h = add_rms_norm(x, blk.mlp(h), nxt.weight, nxt.eps, nxt.grad_into)
         return self.lin(h, self.head)
 
 
@@ -320,7 +324,8 @@ def train(cfg: GPTConfig, batch=8, seq=1024, steps=20, seed=5, device="cuda", at
     operators (RMSNorm, SwiGLU, the optimizer step) for the reference's eager
     op sequences; `fuse_add_norm=False` runs the residual adds as separate
     torch adds in front of the RMSNorm kernels; `gemm_grad_accumulate=False`
-    leaves the projections' weight gradients to autograd's accumulation;
+    leaves the projections' and the norms' weight gradients to autograd's
+    accumulation;
     `regions` (resume() / pause()) brackets the timed steps for a profiler."""
     loss_fn = loss_fn or vocab_parallel_cross_entropy
     torch.manual_seed(seed)

@@ -33,11 +33,29 @@ def _rows_view(t: torch.Tensor) -> torch.Tensor:
         return t.contiguous()
 
 
+def _grad_target(w: torch.Tensor, weight_dtype) -> torch.Tensor | None:
+    """The weight's existing .grad, when the backward may add its weight
+    gradient there itself (as autograd's accumulation would, same rounding): w
+    is the weight (not a converted copy), its gradient has w's dtype, shape and
+    a dense layout, and no double backward is being recorded.  None otherwise."""
+    if not w.is_leaf or torch.is_grad_enabled():
+        return None
+    g = w.grad
+    if g is None or g.dtype != w.dtype or w.dtype != weight_dtype or g.shape != w.shape \
+            or not g.is_contiguous():
+        return None
+    return g
+
+
 class FusedRMSNorm(torch.autograd.Function):
-    """y = round_x(x * rsqrt(mean(x^2, -1) + eps)) * weight."""
+    """y = round_x(x * rsqrt(mean(x^2, -1) + eps)) * weight.  With `grad_into`,
+    the backward adds the weight gradient into the weight's existing .grad
+    (mi_rmsnorm_bwd_acc) and returns none for it, as the model harness's
+    projections do with their GEMMs; gradient hooks on the weight then see no
+    gradient, so the drop-in default leaves it to autograd."""
 
     @staticmethod
-    def forward(ctx, x: torch.Tensor, weight: torch.Tensor, eps: float):
+    def forward(ctx, x: torch.Tensor, weight: torch.Tensor, eps: float, grad_into: bool = False):
         if weight.dim() != 1 or x.shape[-1] != weight.shape[0]:
             raise ValueError(f"weight {tuple(weight.shape)} does not match the last dim of x "
                              f"{tuple(x.shape)}")
@@ -55,6 +73,7 @@ class FusedRMSNorm(torch.autograd.Function):
         _lib.rmsnorm_fwd(xr, w, eps, y, rstd)
         ctx.save_for_backward(xr, w, rstd)
         ctx.weight_dtype = weight.dtype
+        ctx.grad_into = grad_into
         return y
 
     @staticmethod
@@ -63,15 +82,20 @@ class FusedRMSNorm(torch.autograd.Function):
         dy = _rows_view(dy)
         rows = rstd.numel()
         dx = torch.empty(xr.shape, dtype=xr.dtype, device=xr.device)
-        dw = torch.empty(w.shape, dtype=w.dtype, device=w.device)
         ws = torch.empty(_lib.rmsnorm_workspace(rows, xr.shape[-1]), dtype=torch.float32,
                          device=xr.device)
+        g = _grad_target(w, ctx.weight_dtype) if ctx.grad_into else None
+        if g is not None:
+            _lib.rmsnorm_bwd(xr, w, rstd, dy, dx, g, ws, accumulate=True)
+            return dx, None, None, None
+        dw = torch.empty(w.shape, dtype=w.dtype, device=w.device)
         _lib.rmsnorm_bwd(xr, w, rstd, dy, dx, dw, ws)
-        return dx, dw.to(ctx.weight_dtype), None
+        return dx, dw.to(ctx.weight_dtype), None, None
 
 
-def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    return FusedRMSNorm.apply(x, weight, eps)
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+             grad_into: bool = False) -> torch.Tensor:
+    return FusedRMSNorm.apply(x, weight, eps, grad_into)
 
 
 def _norm_weight(x: torch.Tensor, weight: torch.Tensor) -> torch.Tensor:
@@ -94,7 +118,8 @@ class FusedAddRMSNorm(torch.autograd.Function):
     the gradient of both x and res."""
 
     @staticmethod
-    def forward(ctx, x: torch.Tensor, res: torch.Tensor, weight: torch.Tensor, eps: float):
+    def forward(ctx, x: torch.Tensor, res: torch.Tensor, weight: torch.Tensor, eps: float,
+                grad_into: bool = False):
         if weight.dim() != 1 or x.shape[-1] != weight.shape[0]:
             raise ValueError(f"weight {tuple(weight.shape)} does not match the last dim of x "
                              f"{tuple(x.shape)}")
@@ -111,6 +136,7 @@ class FusedAddRMSNorm(torch.autograd.Function):
         _lib.rmsnorm_add_fwd(xr, rr, w, eps, s, y, rstd)
         ctx.save_for_backward(s, w, rstd)
         ctx.weight_dtype = weight.dtype
+        ctx.grad_into = grad_into
         ctx.set_materialize_grads(False)
         return s, y
 
@@ -119,24 +145,30 @@ class FusedAddRMSNorm(torch.autograd.Function):
         s, w, rstd = ctx.saved_tensors
         if dy is None:  # only the sum is used: the norm contributes nothing
             dx = ds.to(s.dtype)
-            return dx, dx, torch.zeros(w.shape, dtype=ctx.weight_dtype, device=w.device), None
+            return (dx, dx, torch.zeros(w.shape, dtype=ctx.weight_dtype, device=w.device), None,
+                    None)
         dy = _rows_view(dy)
         rows = rstd.numel()
         dx = torch.empty(s.shape, dtype=s.dtype, device=s.device)
-        dw = torch.empty(w.shape, dtype=w.dtype, device=w.device)
         ws = torch.empty(_lib.rmsnorm_workspace(rows, s.shape[-1]), dtype=torch.float32,
                          device=s.device)
+        g = _grad_target(w, ctx.weight_dtype) if ctx.grad_into else None
+        dw = g if g is not None else torch.empty(w.shape, dtype=w.dtype, device=w.device)
         if ds is None:  # only the normalised output is used (e.g. after the last add)
-            _lib.rmsnorm_bwd(s, w, rstd, dy, dx, dw, ws)
+            _lib.rmsnorm_bwd(s, w, rstd, dy, dx, dw, ws, accumulate=g is not None)
         else:
             ds = _rows_view(ds.to(s.dtype))
-            _lib.rmsnorm_add_bwd(s, w, rstd, dy, ds, dx, dw, ws)
-        return dx, dx, dw.to(ctx.weight_dtype), None
+            _lib.rmsnorm_add_bwd(s, w, rstd, dy, ds, dx, dw, ws, accumulate=g is not None)
+        if g is not None:
+            return dx, dx, None, None, None
+        return dx, dx, dw.to(ctx.weight_dtype), None, None
 
 
-def add_rms_norm(x: torch.Tensor, res: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6):
-    """``s = x + res; return s, RMSNorm(s)`` in one kernel (and one backward)."""
-    return FusedAddRMSNorm.apply(x, res, weight, eps)
+def add_rms_norm(x: torch.Tensor, res: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6,
+                 grad_into: bool = False):
+    """``s = x + res; return s, RMSNorm(s)`` in one kernel (and one backward).
+    `grad_into` as for FusedRMSNorm."""
+    return FusedAddRMSNorm.apply(x, res, weight, eps, grad_into)
 
 
 class RMSNorm(nn.Module):

@@ -320,6 +320,28 @@ mi_status mi_rmsnorm_add_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, i
                              int64_t workspace_elems, void* stream);
 
 /*
+ * mi_rmsnorm_bwd and mi_rmsnorm_add_bwd with dweight accumulated instead of
+ * written: dweight[j] = round_w(dweight[j] + round_w(sum over rows)), the
+ * gradient the norm's backward returns followed by autograd's accumulation of
+ * it into an existing weight gradient (AccumulateGrad, for the weight of
+ * core/normalization.py:8-11 whose .grad is the optimizer's flat buffer view,
+ * core/optimizer.py:39-70), bitwise as the two steps round, without the
+ * separate [hidden] gradient and the extra launch.  Other arguments and
+ * conditions as those two.
+ */
+mi_status mi_rmsnorm_bwd_acc(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
+                             const void* x, int64_t x_row_stride, const void* weight,
+                             const float* rstd, const void* dy, int64_t dy_row_stride, void* dx,
+                             int64_t dx_row_stride, void* dweight, float* workspace,
+                             int64_t workspace_elems, void* stream);
+mi_status mi_rmsnorm_add_bwd_acc(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows,
+                                 int64_t hidden, const void* sum, int64_t sum_row_stride,
+                                 const void* weight, const float* rstd, const void* dy,
+                                 int64_t dy_row_stride, const void* dsum, int64_t dsum_row_stride,
+                                 void* dx, int64_t dx_row_stride, void* dweight, float* workspace,
+                                 int64_t workspace_elems, void* stream);
+
+/*
  * SwiGLU on the fused gate_up projection: rows of 2*inter elements, gate in
  * columns [0, inter), up in [inter, 2*inter).  Replaces
  * `gate, up = gate_up.chunk(2, dim=-1); x = F.silu(gate) * up`,

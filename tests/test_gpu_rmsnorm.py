@@ -284,3 +284,56 @@ def test_add_norm_in_place_and_model_stack(gpu):
     assert torch.equal(l1, l2) and torch.equal(g1, g2)
     for a, b in zip(p1, p2):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("xd,wd", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                   (torch.float32, torch.float32), (torch.bfloat16, torch.float32)])
+@pytest.mark.parametrize("rows,H", [(37, 768), (21, 7)])
+def test_weight_gradient_accumulated_in_place(gpu, xd, wd, rows, H):
+    """mi_rmsnorm_bwd_acc / mi_rmsnorm_add_bwd_acc against the non-accumulating
+    entry points followed by the add autograd's accumulation performs
+    (g + dw in w's dtype): dweight and dx bit for bit, on the vector path (H =
+    768) and the scalar one (H = 7); and the opt-in autograd path
+    (grad_into=True) against the default one on an existing .grad."""
+    from gpt_from_scratch_amd import _lib
+    from gpt_from_scratch_amd.normalization import add_rms_norm, rms_norm
+
+    x = seeded((rows, H), 600 + H, std=1.5, dtype=xd).to(gpu)
+    w = (1.0 + 0.1 * seeded((H,), 601 + H, dtype=torch.float32)).to(wd).to(gpu)
+    yd = torch.float32 if wd == torch.float32 else xd
+    dy = seeded((rows, H), 602 + H, dtype=yd).to(gpu)
+    ds = seeded((rows, H), 603 + H, std=0.5, dtype=xd).to(gpu)
+    g0 = seeded((H,), 604 + H, std=0.3, dtype=wd).to(gpu)
+    rstd = torch.empty(rows, dtype=torch.float32, device=gpu)
+    _lib.rmsnorm_fwd(x, w, EPS, torch.empty(rows, H, dtype=yd, device=gpu), rstd)
+    ws = torch.empty(_lib.rmsnorm_workspace(rows, H), dtype=torch.float32, device=gpu)
+    for add in (False, True):
+        dx_a, dx_b = torch.empty_like(x), torch.empty_like(x)
+        dw = torch.empty_like(w)
+        acc = g0.clone()
+        if add:
+            _lib.rmsnorm_add_bwd(x, w, rstd, dy, ds, dx_a, dw, ws)
+            _lib.rmsnorm_add_bwd(x, w, rstd, dy, ds, dx_b, acc, ws, accumulate=True)
+        else:
+            _lib.rmsnorm_bwd(x, w, rstd, dy, dx_a, dw, ws)
+            _lib.rmsnorm_bwd(x, w, rstd, dy, dx_b, acc, ws, accumulate=True)
+        torch.cuda.synchronize()
+        assert torch.equal(dx_a, dx_b), add
+        assert torch.equal(acc, g0 + dw), (add, float((acc.float() - (g0 + dw).float()).abs().max()))
+
+    # autograd: the kernel adds into .grad and hands autograd none
+    for add in (False, True):
+        grads = []
+        for into in (False, True):
+            wp = torch.nn.Parameter(w.clone())
+            wp.grad = g0.clone()
+            xi = x.clone().requires_grad_()
+            if add:
+                s, y = add_rms_norm(xi, ds.clone(), wp, EPS, grad_into=into)
+                torch.autograd.backward([s, y], [ds, dy])
+            else:
+                rms_norm(xi, wp, EPS, grad_into=into).backward(dy)
+            grads.append((xi.grad, wp.grad))
+        torch.cuda.synchronize()
+        (xa, wa), (xb, wb) = grads
+        assert torch.equal(xa, xb) and torch.equal(wa, wb), add
