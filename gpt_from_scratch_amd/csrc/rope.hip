@@ -192,10 +192,12 @@ hipError_t rope_launch(const RopeArgs& a, bool vec, hipStream_t st) {
   if (vec) {
     // one lane per (s, b, h, 16-byte chunk), all tensors
     const uint64_t total = (uint64_t)a.S * a.B * a.H * C;
-    // four items per lane (C2: 768 workgroups, every load of the launch in
-    // flight at once): 9.3 us from HBM against 10.7 us for the grid-stride loop
-    // over 2048 workgroups; two items 10.6, six 10.2, eight 12.2 us
-    constexpr int U = 4;
+    // three items per lane (C2: 1024 workgroups, four per CU, every load of
+    // the launch in flight at once): 9.04-9.09 us from HBM against 9.17-9.18
+    // for four items (768 workgroups) and 9.9-10.1 for five, interleaved on one
+    // box; earlier, 10.7 us for a grid-stride loop over 2048 workgroups, two
+    // items 10.6, six 10.2, eight 12.2
+    constexpr int U = 3;
     const dim3 grid((uint32_t)((total + ROPE_T * U - 1) / (ROPE_T * U))), block(ROPE_T);
     if (a.ntensors == 2)
       hipLaunchKernelGGL((rope_vec_kernel<XDT, TDT, 2, U>), grid, block, 0, st, a, dv, (uint32_t)total);
