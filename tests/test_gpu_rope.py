@@ -50,6 +50,21 @@ def test_bf16_model_layout_qk(gpu):
     assert torch.equal(kr, apply_rope(k, cos, sin))
 
 
+@pytest.mark.parametrize("B,H,S,D", [(1, 5, 37, 64), (3, 7, 19, 128), (1, 1, 1, 64)])
+def test_vector_path_ragged_grid(gpu, B, H, S, D):
+    """Vector-path sizes whose 16-byte items do not fill the last workgroup (each
+    lane takes several items, 256 lanes per workgroup): every element is written
+    and matches the oracle; the last workgroup's missing items touch nothing."""
+    from gpt_from_scratch_amd import apply_rope_qk
+    q, k, _, cos, sin, _ = rope_inputs(B, H, S, D, 40 + S, 1.0, torch.bfloat16, gpu)
+    items = 2 * S * B * H * D // 8
+    assert items % (256 * 2) and items % (256 * 3) and items % (256 * 4)
+    qr, kr = apply_rope_qk(q, k, cos, sin)
+    for x, y in ((q, qr), (k, kr)):
+        ref = rope_apply(x.cpu(), cos.cpu(), sin.cpu(), dtype=torch.float32)
+        assert _bf16_ulp_ok(y, ref)
+
+
 def test_qk_backward_is_inverse_rotation(gpu):
     from gpt_from_scratch_amd import apply_rope_qk
     q, k, v, cos, sin, _ = rope_inputs(2, 4, 128, 64, 3, 1.0, torch.bfloat16, gpu)
