@@ -295,30 +295,37 @@ __device__ __forceinline__ void store_block_rows_rope_t(const f32x16 (&acc)[D / 
       *(u32x2*)(lds + l32 * D + ((c ^ (l32 & 7)) << 3) + 4 * g) = w;
     }
   // the angles after the accumulators are staged (and dead): loading them
-  // earlier would hold both at once
+  // earlier would hold both at once.  Groups of PCH store instructions load
+  // their angles together (all eight at D = 64; four at a time at D = 128,
+  // whose dK/dV kernel sits at its register limit).
   __builtin_amdgcn_sched_barrier(0);
-  typename Tab4<TDT>::type cs[32 / RPI], sn[32 / RPI];
+  constexpr int NP = 32 / RPI;
+  constexpr int PCH = D == 128 ? 4 : NP;
 #pragma unroll
-  for (int p = 0; p < 32 / RPI; ++p) {
-    const int r = p * RPI + lane / CPR;
-    const int c = lane % CPR;
-    cs[p] = Tab4<TDT>::load(t.cos, t.cs_s, pos0 + r, 4 * c);
-    sn[p] = Tab4<TDT>::load(t.sin, t.ss_s, pos0 + r, 4 * c);
-  }
+  for (int p0 = 0; p0 < NP; p0 += PCH) {
+    typename Tab4<TDT>::type cs[PCH], sn[PCH];
 #pragma unroll
-  for (int p = 0; p < 32 / RPI; ++p) {
-    const int r = p * RPI + lane / CPR;
-    const int c = lane % CPR;
-    const u32x4 v = *(const u32x4*)(lds + r * D + ((c ^ (r & 7)) << 3));
-    u32x4 o;
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      float re, ro;
-      rope_rotate(E::to_f32((uint16_t)(v[k] & 0xffffu)), E::to_f32((uint16_t)(v[k] >> 16)),
-                  Tab4<TDT>::get(cs[p], k), Tab4<TDT>::get(sn[p], k), true, re, ro);
-      o[k] = E::pack2(re, ro);
+    for (int i = 0; i < PCH; ++i) {
+      const int r = (p0 + i) * RPI + lane / CPR;
+      const int c = lane % CPR;
+      cs[i] = Tab4<TDT>::load(t.cos, t.cs_s, pos0 + r, 4 * c);
+      sn[i] = Tab4<TDT>::load(t.sin, t.ss_s, pos0 + r, 4 * c);
     }
-    *(u32x4*)(grow + (int64_t)r * ss + 8 * c) = o;
+#pragma unroll
+    for (int i = 0; i < PCH; ++i) {
+      const int r = (p0 + i) * RPI + lane / CPR;
+      const int c = lane % CPR;
+      const u32x4 v = *(const u32x4*)(lds + r * D + ((c ^ (r & 7)) << 3));
+      u32x4 o;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        float re, ro;
+        rope_rotate(E::to_f32((uint16_t)(v[k] & 0xffffu)), E::to_f32((uint16_t)(v[k] >> 16)),
+                    Tab4<TDT>::get(cs[i], k), Tab4<TDT>::get(sn[i], k), true, re, ro);
+        o[k] = E::pack2(re, ro);
+      }
+      *(u32x4*)(grow + (int64_t)r * ss + 8 * c) = o;
+    }
   }
 }
 
@@ -489,7 +496,7 @@ __device__ __forceinline__ void dma_stage(const StageSrc<D>& s, int kind, int ro
 // accumulators together need ~290 VGPRs, and holding all of them spilled
 // ~390 bytes per lane.  The region then stages the wave's dK and dV stores.
 // ---------------------------------------------------------------------------
-template <typename E, int D, bool CAUSAL>
+template <typename E, int D, bool CAUSAL, bool ROPE>
 __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
                                           const BwdBuf (&bufs)[2]) {
   using C = BwdCfg<D>;
@@ -675,7 +682,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     uint16_t* stage = wave_stage_buf(bufs, wave);
     // dV first: its accumulators are dead before dK's rotation needs registers
     store_block_rows<E, D>(dv, 1.f, stage, dv_rows, a.dv.ss);
-    if (a.rope.cos)
+    if (ROPE && a.rope.cos)
       store_block_rows_rope<E, D>(dk, a.scale, stage, dk_rows, a.dk.ss, a.rope, kw);
     else
       store_block_rows<E, D>(dk, a.scale, stage, dk_rows, a.dk.ss);
@@ -683,11 +690,12 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     // D = 128: the wave's K region (32 x D, its own) is idle after the last
     // step.  (Written straight from the accumulators instead, 8 bytes per lane
     // and row, the launch measured the same at configs 3 and 4 and 2% slower
-    // at B8 S1024.)  No fused rotation here: its code costs this kernel, at
-    // its register limit, a spilled value reloaded every step; the host runs
-    // the inverse RoPE as a separate pass at D = 128.
+    // at B8 S1024.)
     store_block_rows<E, D>(dv, 1.f, kw_lds, dv_rows, a.dv.ss);
-    store_block_rows<E, D>(dk, a.scale, kw_lds, dk_rows, a.dk.ss);
+    if (ROPE && a.rope.cos)
+      store_block_rows_rope<E, D>(dk, a.scale, kw_lds, dk_rows, a.dk.ss, a.rope, kw);
+    else
+      store_block_rows<E, D>(dk, a.scale, kw_lds, dk_rows, a.dk.ss);
   }
 }
 
@@ -697,7 +705,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
 // per-lane scalars and dS^T feeds dQ^T = K^T dS^T directly (K^T read
 // transposed from the K tile).
 // ---------------------------------------------------------------------------
-template <typename E, int D, bool CAUSAL>
+template <typename E, int D, bool CAUSAL, bool ROPE>
 __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
                                         const BwdBuf (&bufs)[2]) {
   using C = BwdCfg<D>;
@@ -829,7 +837,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   const int h = it.bh % a.H;
   uint16_t* const dq_rows =
       (uint16_t*)a.dq.ptr + b * a.dq.sb + h * a.dq.sh + (int64_t)qw * a.dq.ss;
-  if (D == 64 && a.rope.cos)
+  if (ROPE && a.rope.cos)
     store_block_rows_rope<E, D>(acc, a.scale, wave_stage_buf(bufs, wave), dq_rows, a.dq.ss,
                                 a.rope, qw);
   else
@@ -839,7 +847,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
 // One item per workgroup.  One LDS array per buffer and tensor, so that the
 // compiler can see that a direct load into one buffer never aliases the
 // reads of the other.
-template <typename E, int D, bool CAUSAL>
+template <typename E, int D, bool CAUSAL, bool ROPE>
 __device__ __forceinline__ void run_item(const AttnArgs& a, const BwdItem it) {
   using C = BwdCfg<D>;
   __shared__ __attribute__((aligned(16))) uint16_t A0[C::ELEMS];
@@ -850,22 +858,25 @@ __device__ __forceinline__ void run_item(const AttnArgs& a, const BwdItem it) {
   __shared__ __attribute__((aligned(16))) float SB[2 * C::TILE];
   const BwdBuf bufs[2] = {{A0, A1, SA}, {B0, B1, SB}};
   if (it.kind)
-    dq_item<E, D, CAUSAL>(a, it, bufs);
+    dq_item<E, D, CAUSAL, ROPE>(a, it, bufs);
   else
-    dkdv_item<E, D, CAUSAL>(a, it, bufs);
+    dkdv_item<E, D, CAUSAL, ROPE>(a, it, bufs);
 }
 
-template <typename E, int D, bool CAUSAL>
+// ROPE (every kernel below): the kernel carries the rotating stores, and dQ
+// and dK leave inverse-rotated by the tables in a.rope when a.rope.cos is set;
+// without it the kernel has no rotation code.
+template <typename E, int D, bool CAUSAL, bool ROPE>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(AttnArgs a) {
   // key tile 0 sees the most query tiles: dispatched first
   const int BH = a.B * a.H;
-  run_item<E, D, CAUSAL>(a, BwdItem{0, (int)(blockIdx.x / BH), (int)(blockIdx.x % BH)});
+  run_item<E, D, CAUSAL, ROPE>(a, BwdItem{0, (int)(blockIdx.x / BH), (int)(blockIdx.x % BH)});
 }
 
-template <typename E, int D, bool CAUSAL>
+template <typename E, int D, bool CAUSAL, bool ROPE>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a, int n_qtiles) {
   const int BH = a.B * a.H;
-  run_item<E, D, CAUSAL>(
+  run_item<E, D, CAUSAL, ROPE>(
       a, BwdItem{1, n_qtiles - 1 - (int)(blockIdx.x / BH), (int)(blockIdx.x % BH)});
 }
 
@@ -874,42 +885,65 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a, int n_q
 // n_tiles-1-r/2, the tiles that see the most of the sequence under causal
 // masking), so the short tails of both kinds overlap the long heads of the
 // other and the launch keeps the whole chip busy.
-template <typename E, int D, bool CAUSAL>
+template <typename E, int D, bool CAUSAL, bool ROPE>
 __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(AttnArgs a, int n_tiles) {
   const int BH = a.B * a.H;
   const int rank = blockIdx.x / BH;
   const int kind = rank & 1;
-  run_item<E, D, CAUSAL>(
+  run_item<E, D, CAUSAL, ROPE>(
       a, BwdItem{kind, kind ? n_tiles - 1 - (rank >> 1) : (rank >> 1), (int)(blockIdx.x % BH)});
 }
 
-template <typename E, int D>
-hipError_t launch_dkdv_d(const AttnArgs& a, hipStream_t st) {
+template <typename E, int D, bool ROPE>
+hipError_t launch_dkdv_dr(const AttnArgs& a, hipStream_t st) {
   const int BH = a.B * a.H;
   const int nkt = (a.S + BwdCfg<D>::OWN - 1) / BwdCfg<D>::OWN;
   if (a.causal)
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, true>), dim3(nkt * BH), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, true, ROPE>), dim3(nkt * BH), dim3(256), 0, st,
+                       a);
   else
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, false>), dim3(nkt * BH), dim3(256), 0, st, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, false, ROPE>), dim3(nkt * BH), dim3(256), 0,
+                       st, a);
   return hipGetLastError();
+}
+
+template <typename E, int D, bool ROPE>
+hipError_t launch_dq_dr(const AttnArgs& a, hipStream_t st) {
+  const int BH = a.B * a.H;
+  const int nqt = (a.S + BwdCfg<D>::OWN - 1) / BwdCfg<D>::OWN;
+  if (a.causal)
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<E, D, true, ROPE>), dim3(nqt * BH), dim3(256), 0, st,
+                       a, nqt);
+  else
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<E, D, false, ROPE>), dim3(nqt * BH), dim3(256), 0, st,
+                       a, nqt);
+  return hipGetLastError();
+}
+
+// The separate launches rotate only at D = 128 (the D = 64 rotation runs in
+// the combined launch).
+template <typename E, int D>
+hipError_t launch_dkdv_d(const AttnArgs& a, hipStream_t st) {
+  if constexpr (D == 128)
+    if (a.rope.cos) return launch_dkdv_dr<E, D, true>(a, st);
+  return launch_dkdv_dr<E, D, false>(a, st);
 }
 
 template <typename E, int D>
 hipError_t launch_dq_d(const AttnArgs& a, hipStream_t st) {
-  const int BH = a.B * a.H;
-  const int nqt = (a.S + BwdCfg<D>::OWN - 1) / BwdCfg<D>::OWN;
-  if (a.causal)
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<E, D, true>), dim3(nqt * BH), dim3(256), 0, st, a, nqt);
-  else
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<E, D, false>), dim3(nqt * BH), dim3(256), 0, st, a, nqt);
-  return hipGetLastError();
+  if constexpr (D == 128)
+    if (a.rope.cos) return launch_dq_dr<E, D, true>(a, st);
+  return launch_dq_dr<E, D, false>(a, st);
 }
 
+// (One instantiation with the rotation applied at run time: compiled without
+// the rotating stores, the causal kernel's registers spilled 12 bytes.)
 template <typename E, int D, bool CAUSAL>
 hipError_t launch_both_dc(const AttnArgs& a, hipStream_t st) {
   const int BH = a.B * a.H;
   const int n = (a.S + BwdCfg<D>::OWN - 1) / BwdCfg<D>::OWN;
-  hipLaunchKernelGGL((attn_bwd_kernel<E, D, CAUSAL>), dim3(2 * n * BH), dim3(256), 0, st, a, n);
+  hipLaunchKernelGGL((attn_bwd_kernel<E, D, CAUSAL, true>), dim3(2 * n * BH), dim3(256), 0, st,
+                     a, n);
   return hipGetLastError();
 }
 

@@ -233,6 +233,29 @@ static mi_status rope_common(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B,
                              const int64_t cos_strides[2], const void* sin_tab,
                              const int64_t sin_strides[2], void* stream);
 
+// Whether the gradients run on the matrix-core kernels: bf16/f16 at their
+// head dims and sequence multiple, every row 16-byte aligned.
+static bool bwd_mfma_path(mi_dtype dtype, int D, int S, const void* q, const int64_t* qs,
+                          const void* k, const int64_t* ks, const void* v, const int64_t* vs,
+                          const void* dout, const int64_t* dos, const void* dq,
+                          const int64_t* dqs, const void* dk, const int64_t* dks, const void* dv,
+                          const int64_t* dvs) {
+  const int esz = elem_size(dtype);
+  return mi::mfma_supports(dtype, D, S) && aligned16(q, qs, esz) && aligned16(k, ks, esz) &&
+         aligned16(v, vs, esz) && aligned16(dout, dos, esz) && aligned16(dq, dqs, esz) &&
+         aligned16(dk, dks, esz) && aligned16(dv, dvs, esz);
+}
+
+// Whether the matrix-core kernels can rotate dQ and dK as they store them:
+// their stores read four 16-bit angles per table with one vector load, so the
+// tables must be 16-bit, with contiguous angles and every row start aligned to
+// four of them.  Otherwise the host runs the inverse RoPE as a separate pass.
+static bool rope_fusable(const mi::RopeTab& r) {
+  const int tsz = elem_size((mi_dtype)r.tdt);
+  return r.tdt != MI_F32 && r.cs_i == 1 && r.ss_i == 1 && r.cs_s % 4 == 0 && r.ss_s % 4 == 0 &&
+         ((uintptr_t)r.cos) % (4 * tsz) == 0 && ((uintptr_t)r.sin) % (4 * tsz) == 0;
+}
+
 // `rope` != nullptr: dQ and dK leave inverse-rotated (mi_attn_bwd_rope).
 static mi_status grads_impl(mi_dtype dtype, int B, int H, int S, int D, int causal, float scale,
                             const void* q, const int64_t q_strides[4], const void* k,
@@ -250,24 +273,14 @@ static mi_status grads_impl(mi_dtype dtype, int B, int H, int S, int D, int caus
   if ((st = check_attn_tensor("dq", dq, dq_strides)) != MI_OK) return st;
   if ((st = check_attn_tensor("dk", dk, dk_strides)) != MI_OK) return st;
   if ((st = check_attn_tensor("dv", dv, dv_strides)) != MI_OK) return st;
-  const int esz = elem_size(dtype);
-  if (mi::mfma_supports(dtype, D, S) && aligned16(q, q_strides, esz) &&
-      aligned16(k, k_strides, esz) && aligned16(v, v_strides, esz) &&
-      aligned16(dout, dout_strides, esz) && aligned16(dq, dq_strides, esz) &&
-      aligned16(dk, dk_strides, esz) && aligned16(dv, dv_strides, esz)) {
+  if (bwd_mfma_path(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout, dout_strides,
+                    dq, dq_strides, dk, dk_strides, dv, dv_strides)) {
     mi::AttnArgs a = grad_args(B, H, S, D, causal, scale, q, q_strides, k, k_strides, v,
                                v_strides, dout, dout_strides, lse, ws);
     a.dq = targ(dq, dq_strides);
     a.dk = targ(dk, dk_strides);
     a.dv = targ(dv, dv_strides);
-    // The D = 64 kernels' stores rotate with one vector load of four 16-bit
-    // angles per table: rows of contiguous angles, every row start aligned to
-    // four of them.
-    const int tsz = rope ? elem_size((mi_dtype)rope->tdt) : 0;
-    const bool fuse_rope =
-        rope && D == 64 && rope->tdt != MI_F32 && rope->cs_i == 1 && rope->ss_i == 1 && rope->cs_s % 4 == 0 &&
-        rope->ss_s % 4 == 0 && ((uintptr_t)rope->cos) % (4 * tsz) == 0 &&
-        ((uintptr_t)rope->sin) % (4 * tsz) == 0;
+    const bool fuse_rope = rope && rope_fusable(*rope);
     if (fuse_rope) a.rope = *rope;
     if ((st = launched(mi::launch_attn_bwd_mfma(dtype, a, (hipStream_t)stream),
                        "attn_bwd_mfma")) != MI_OK || !rope || fuse_rope)
@@ -328,6 +341,14 @@ mi_status mi_attn_bwd_rope(mi_dtype dtype, int B, int H, int S, int D, int causa
   rope.ss_s = sin_strides[0];
   rope.ss_i = sin_strides[1];
   rope.tdt = tab_dtype;
+  // The separate inverse-RoPE pass (taken when the kernels cannot rotate as
+  // they store) has its own launch limit: refuse before anything is enqueued.
+  const bool fused = bwd_mfma_path(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
+                                   dout_strides, dq, dq_strides, dk, dk_strides, dv,
+                                   dv_strides) &&
+                     rope_fusable(rope);
+  if (!fused && (uint64_t)2 * S * B * H * (D / 2) >= (1ull << 31))
+    return fail(MI_ERR_UNSUPPORTED, "tensor too large for one launch");
   if ((st = mi_attn_bwd_preprocess(dtype, B, H, S, D, o, o_strides, dout, dout_strides, lse, ws,
                                    stream)) != MI_OK)
     return st;

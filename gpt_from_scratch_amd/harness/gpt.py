@@ -61,7 +61,14 @@ class _LinearGradInto(torch.autograd.Function):
     ``w.grad.addmm_(gy^T, x)``, beta = 1 in the GEMM's epilogue, instead of a
     separate gradient tensor that autograd then adds into the buffer with one
     more pass over it.  Without a usable ``w.grad`` (none yet, another dtype or
-    layout, or a double backward) the gradient is returned as F.linear's is."""
+    layout, or a double backward) the gradient is returned as F.linear's is.
+
+    The fused form rounds once, round(g + acc), where autograd's add rounds the
+    gradient first, round(round(g) + acc).  The two agree bit for bit only when
+    ``w.grad`` starts zeroed and the weight receives exactly one gradient per
+    backward, as in this harness (the optimizer zeroes its flat buffer each step
+    and every projection weight is used once).  With micro-batch accumulation or
+    a weight used twice in one graph the results would differ in the last bit."""
 
     @staticmethod
     def forward(ctx, x, w):

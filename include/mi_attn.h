@@ -398,12 +398,14 @@ mi_status mi_adamw_step(mi_dtype grad_dtype, mi_dtype param_dtype, int64_t n, co
 /*
  * mi_attn_bwd without the workspace argument, for callers that cannot
  * allocate device memory: code under HIP graph capture, tight serving loops,
- * harnesses that forbid hipMalloc.  It has no counterpart in the reference
- * (whose backward allocates D itself, core/myFlashAttn.py:323).
+ * harnesses that forbid hipMalloc.  It has no counterpart in the reference.
  * The workspace lives in a library-owned static device array of
  * 2 * MI_ATTN_NOALLOC_MAX_ROWS floats (8 MiB) on each GPU the library runs on,
  * held until the process ends; its address is looked up once per device on
- * the first call there.  B*H*S must not exceed MI_ATTN_NOALLOC_MAX_ROWS
+ * the first call there (hipGetSymbolAddress, with that device made current
+ * for the lookup).  Make that first call on each device outside stream
+ * capture; later calls only enqueue kernels and may be captured into a HIP
+ * graph and replayed.  B*H*S must not exceed MI_ATTN_NOALLOC_MAX_ROWS
  * (MI_ERR_INVALID_ARGUMENT otherwise, before anything is enqueued).  The call
  * allocates nothing.  Every call on one GPU shares that array: calls that
  * overlap on one GPU (other streams, other threads) race and must be

@@ -285,3 +285,9 @@ def test_new_entry_points_reject_bad_arguments():
     assert b"cos/sin" in lib.mi_last_error()
     odd = [2, 1, 1, 64, 63, 1, 0.125] + args[7:]
     assert lib.mi_attn_bwd_rope(*odd, 2, fake, t2, fake, t2, None) != 0
+    # fp32 tables are rotated by a separate inverse-RoPE pass after the gradient
+    # kernels; a shape past that pass's launch limit (2^31 angle pairs) is
+    # refused before the preprocess or the gradients are enqueued
+    big = [2, 1, 512, 65536, 64, 1, 0.125] + args[7:]
+    assert lib.mi_attn_bwd_rope(*big, 0, fake, t2, fake, t2, None) == 2
+    assert b"too large" in lib.mi_last_error()

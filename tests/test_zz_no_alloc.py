@@ -49,3 +49,29 @@ def test_noalloc_refuses_more_rows_than_its_array(gpu):
                                  None, arr(), None, arr(), None, arr(), None, arr(), None, arr(),
                                  None, None, arr(), None, arr(), None, arr(), stream)
     assert st == 1 and b"MI_ATTN_NOALLOC_MAX_ROWS" in lib.mi_last_error()
+
+
+def test_noalloc_backward_replays_under_graph_capture(gpu):
+    """After one call outside capture (the per-device address lookup), the call
+    is captured into a graph; every replay, with eager work between replays,
+    reproduces mi_attn_bwd bit for bit."""
+    from gpt_from_scratch_amd import _lib
+    B, H, S, D = 2, 4, 512, 64
+    q, k, v, o, do, lse = _inputs(gpu, B, H, S, D, 900)
+    scale = 1.0 / math.sqrt(D)
+    want = [torch.empty_like(q) for _ in range(3)]
+    _lib.attn_bwd(q, k, v, o, do, lse, _lib.bwd_workspace(lse), *want, True, scale)
+    got = [torch.empty_like(q) for _ in range(3)]
+    _lib.attn_bwd_noalloc(q, k, v, o, do, lse, *got, True, scale)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        _lib.attn_bwd_noalloc(q, k, v, o, do, lse, *got, True, scale)
+    for replay in range(3):
+        for t in got:
+            t.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for name, g, w in zip(("dq", "dk", "dv"), got, want):
+            assert torch.equal(g, w), (name, replay)
