@@ -27,8 +27,14 @@
 //     run a masked body that also skips tiles a wave cannot see;
 //   * the running max is only moved (and O, l rescaled) when a new score
 //     exceeds it by more than 2^8 in exp2 units; otherwise probabilities are
-//     taken against the stale max, which keeps them <= 256 and the result
-//     exact (O and l share the same reference point);
+//     taken against the stale max, which keeps the result exact (O and l share
+//     the same reference point).  At D = 64 a step does not even compute its
+//     tile's max: it takes the probabilities against the stale max and checks
+//     their sum, and only a sum past a bound (a probability possibly above
+//     2^8, or the first tile, which has no reference yet) recomputes the tile's
+//     scores and takes the exact step;
+//   * at D = 64, l sums the probabilities as rounded for P V (v_dot2 over the
+//     packed pairs), so O / l normalises exactly the weights P V applied;
 //   * the grid is linearised heaviest-first: the Q tiles nearest the end of the
 //     sequence (which see the most keys under causal masking) are dispatched
 //     first, and all tiles of one head land on the same XCD (workgroups go
@@ -85,7 +91,17 @@ __device__ __forceinline__ int swz_k(int r) { return D == 64 ? ((r & 7) ^ ((r >>
 template <int D>
 __device__ __forceinline__ int swz_v(int r) { return D == 64 ? ((r & 3) << 1) : ((r & 3) << 2); }
 
-constexpr float kRescaleSlack = 8.f;  // log2 units: probabilities stay <= 2^8
+constexpr float kRescaleSlack = 8.f;  // log2 units: exact-max probabilities stay <= 2^8
+
+// Largest probability sum of one lane and tile taken without the tile's max
+// (D = 64): 2^64 for bf16 P (fp32 O and l have room for it at any length),
+// 2^14 for fp16 P (whose largest finite value is 65504).  A sum past it means
+// a probability above 2^8, i.e. a max more than kRescaleSlack above the
+// reference, so the exact step that follows moves the reference.
+template <typename E>
+__device__ __forceinline__ constexpr float kProbLimit() {
+  return std::is_same<E, BF16>::value ? 0x1p64f : 0x1p14f;
+}
 
 template <typename E, int D, bool CAUSAL>
 __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_kernel(AttnArgs a, int n_qtiles, int n_cu) {
@@ -194,16 +210,43 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
       }
     }
   };
-  // Softmax of S^T in place, probabilities packed into pb; key tile starts at kv0.
-  auto softmax = [&](f32x16(&s)[2], u32x4(&pb)[2][2], int kv0, bool masked) __attribute__((always_inline)) {
-    if (masked) {
-      const int rel = qrow - kv0 - 4 * g;  // visible iff (kv - kv0 - 4g) <= rel
+  // Triangle mask of a diagonal tile (key tile starting at kv0).
+  auto mask = [&](f32x16(&s)[2], int kv0) __attribute__((always_inline)) {
+    const int rel = qrow - kv0 - 4 * g;  // visible iff (kv - kv0 - 4g) <= rel
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          if (32 * kb + 8 * (r >> 2) + (r & 3) > rel) s[kb][r] = -INFINITY;
+      for (int r = 0; r < 16; ++r)
+        if (32 * kb + 8 * (r >> 2) + (r & 3) > rel) s[kb][r] = -INFINITY;
+  };
+  // Probabilities against the reference mref, in place, packed into pb; returns
+  // their sum.  D = 64 sums the packed (rounded) values, the ones P V
+  // multiplies, with one v_dot2 per pair; D = 128 (where that measured ~1%
+  // slower) sums the fp32 values.
+  auto probs = [&](f32x16(&s)[2], u32x4(&pb)[2][2], float mref) __attribute__((always_inline)) {
+    float ps[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        s[kb][r] = fast_exp2(__builtin_fmaf(s[kb][r], c, -mref));
+        if constexpr (D != 64) ps[r & 3] += s[kb][r];
+      }
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          pb[kb][hh][w] = E::pack2(s[kb][8 * hh + 2 * w], s[kb][8 * hh + 2 * w + 1]);
+          if constexpr (D == 64) ps[w] = E::sum2(pb[kb][hh][w], ps[w]);
+        }
     }
+    return (ps[0] + ps[1]) + (ps[2] + ps[3]);
+  };
+  // Exact reference: the running max moved to this tile's max (O and l
+  // rescaled) when that exceeds it by more than kRescaleSlack; otherwise the
+  // probabilities stay against the stale max, <= 2^8, and exact (O and l share
+  // the reference point).
+  auto to_max = [&](f32x16(&s)[2]) __attribute__((always_inline)) {
     // NaN-propagating maximum: v_maximum3_f32 chains without input
     // canonicalisation (2 scores per instruction).
     float mx = vmax(s[0][0], s[0][1]);
@@ -213,28 +256,11 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
     if (__any(mx > m_run + kRescaleSlack)) {
       const float m_new = fmaxf(m_run, mx);
       const float alpha = fast_exp2(m_run - m_new);
-      m_run = m_new;
       l_run *= alpha;
 #pragma unroll
       for (int db = 0; db < C::DB; ++db) acc[db] *= alpha;
+      m_run = m_new;
     }
-    const float mref = m_run;
-    float psum = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(__builtin_fmaf(s[kb][r], c, -mref));
-        s[kb][r] = p;
-        psum += p;
-      }
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-        for (int w = 0; w < 4; ++w)
-          pb[kb][hh][w] = E::pack2(s[kb][8 * hh + 2 * w], s[kb][8 * hh + 2 * w + 1]);
-    }
-    l_run += psum;
   };
   // O^T += V^T P^T.
   auto pv = [&](const uint16_t* vt, const u32x4(&pb)[2][2]) __attribute__((always_inline)) {
@@ -266,10 +292,32 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
     }
     const int kv0 = j * C::BKV;
     if (wave_valid && (!MASKED || !CAUSAL || kv0 <= qw + 31)) {
+      const bool msk = MASKED && CAUSAL && kv0 + C::BKV - 1 > qw;
       f32x16 s[2];
       qk(kt, s);
+      if (msk) mask(s, kv0);
       u32x4 pb[2][2];
-      softmax(s, pb, kv0, MASKED && CAUSAL && kv0 + C::BKV - 1 > qw);
+      // D = 64: probabilities against the running reference m_run without
+      // this tile's max, exact as long as their sum stays within kProbLimit
+      // (O and l share the reference).  The first tile (no reference yet) and
+      // a tile whose sum says a probability may have passed the limit
+      // recompute S from the staged K tile and take the exact step.  D = 128
+      // takes the exact step every time (the skip's extra code spills there).
+      float psum = 0.f;
+      bool exact = D != 64 || j == 0;
+      if (!exact) {
+        psum = probs(s, pb, m_run);
+        if (__any(!(psum <= kProbLimit<E>()))) {
+          exact = true;
+          qk(kt, s);
+          if (msk) mask(s, kv0);
+        }
+      }
+      if (exact) {
+        to_max(s);
+        psum = probs(s, pb, m_run);
+      }
+      l_run += psum;
       pv(vt, pb);
     }
     __syncthreads();
