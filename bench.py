@@ -689,6 +689,60 @@ def main():
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                 "algorithmic_flop_per_launch": kflops[dom], "traffic": read_traffic(dom)}
 
+    # The same step with its operands out of the Infinity Cache: NC buffer sets
+    # (RoPE'd q/k, the qkv tensor V is a view of, dO, O, LSE, workspace, dQ,
+    # dK, dV; ~113 MB each, 452 MB together against the 256 MB cache) used in
+    # turn, so each step reads from HBM what the last NC - 1 steps evicted, as
+    # a layer of the train step does.  Step time over that rotation, and each
+    # kernel's average over back-to-back launches rotating the same way.
+    NC = 4
+    cold_sets = []
+    for _ in range(NC):
+        qkv_c = torch.randn(S, B, 3, H, D, generator=g).to(torch.bfloat16).to(dev)
+        do_c = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16).to(dev)
+        qc, kc, vc = qkv_c.unbind(2)
+        qrc, krc = apply_rope_qk(qc, kc, cos, sin)
+        Qc, Kc, Vc = qrc.permute(1, 2, 0, 3), krc.permute(1, 2, 0, 3), vc.permute(1, 2, 0, 3)
+        Oc = torch.empty_like(O)
+        LSEc, WSc = torch.empty_like(LSE), torch.empty_like(DELTA)
+        dQc, dKc, dVc = (torch.empty_like(dQ) for _ in range(3))
+        keep = (qkv_c, do_c, qrc, krc, Oc, LSEc, WSc, dQc, dKc, dVc)
+        fa = hdr + (1, scale, P(Qc), ST(Qc), P(Kc), ST(Kc), P(Vc), ST(Vc), P(Oc), ST(Oc),
+                    P(LSEc), sp)
+        pa = hdr + (P(Oc), ST(Oc), P(do_c), ST(do_c), P(LSEc), P(WSc), sp)
+        ga = hdr + (1, scale, P(Qc), ST(Qc), P(Kc), ST(Kc), P(Vc), ST(Vc), P(do_c), ST(do_c),
+                    P(LSEc), P(WSc), P(dQc), ST(dQc), P(dKc), ST(dKc), P(dVc), ST(dVc), sp)
+        cold_sets.append((keep, fa, pa, ga))
+    set_bytes = sum(t.numel() * t.element_size() for t in cold_sets[0][0])
+    for i in range(4 * NC):
+        for (name, fn, _), a in zip(calls, cold_sets[i % NC][1:]):
+            if fn(*a) != 0:
+                raise RuntimeError(f"{name} (HBM-cold pass): {lib.mi_last_error().decode()}")
+    n_cold = max(args.steps, 10 * NC) // NC * NC
+    torch.cuda.synchronize()
+    REGIONS.resume()
+    t_start.record(stream)
+    for i in range(n_cold):
+        for (name, fn, _), a in zip(calls, cold_sets[i % NC][1:]):
+            fn(*a)
+    t_end.record(stream)
+    torch.cuda.synchronize()
+    REGIONS.pause()
+    cold_step_us = t_start.elapsed_time(t_end) / n_cold * 1e3
+    cold_kernels = {}
+    for j, (name, fn, _) in enumerate(calls):
+        us = _time_rotating(stream, fn, [cs[1 + j] for cs in cold_sets], 25 * NC, name + " (cold)")
+        ent = {"avg_us": round(us, 3)}
+        if name in kflops:
+            ent["tflops"] = round(kflops[name] / (us * 1e-6) / 1e12, 2)
+        cold_kernels[name] = ent
+    cold_tflops = flops["total"] / (cold_step_us * 1e-6) / 1e12
+    hbm_cold = {"sets": NC, "set_bytes": set_bytes, "steps": n_cold,
+                "step_us": round(cold_step_us, 2), "tflops": round(cold_tflops, 2),
+                "frac": round(cold_tflops / PEAK_BF16_TFLOPS, 4), "kernels": cold_kernels}
+    del cold_sets
+    _progress(f"config 2 HBM-cold pass: {cold_step_us:.1f} us per step")
+
     # RoPE (q and k in one launch, the model's strided layout) — HBM-bound.
     # Called through the C ABI with a pre-built argument list, like the
     # attention calls, so that the timed loop is not bound by Python.
@@ -725,6 +779,14 @@ def main():
                           ST(rk), sp))
     rope_cold_us = _time_rotating(stream, lib.mi_rope_qk, cold_args, 8 * NQ, "rope_qk")
     rope_cold_gbps = rope_bytes / (rope_cold_us * 1e-6) / 1e9
+    # The streaming ceiling of that launch, in the same run: mi_copy_qk moves
+    # the same q/k views into the same outputs with the same items, grid and
+    # accesses, without the rotation (and the 131 KB of tables).
+    copy_bytes = 4 * B * S * H * D * 2
+    copy_args = [(a[0], S, B, H, D, a[7], a[8], a[9], a[10], a[15], a[16], a[17], a[18], sp)
+                 for a in cold_args]
+    copy_cold_us = _time_rotating(stream, lib.mi_copy_qk, copy_args, 8 * NQ, "copy_qk")
+    copy_cold_gbps = copy_bytes / (copy_cold_us * 1e-6) / 1e9
     del qkvs
 
     _progress("config 2 per-kernel and RoPE passes done")
@@ -766,6 +828,7 @@ def main():
         "algorithmic_gflop_per_step": flops["total"] / 1e9,
         "kernels": kernels,
         "roofline": roofline,
+        "config2_hbm_cold": hbm_cold,
         # RoPE's roofline line is measured from HBM (inputs cycled through 12 qkv
         # copies, 453 MB, more than the 256 MB Infinity Cache); the
         # cache-resident rate (one q/k pair re-read) is reported beside it
@@ -773,6 +836,12 @@ def main():
                  "achieved": round(rope_cold_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
                  "frac": round(rope_cold_gbps / PEAK_HBM_GBPS, 4), "algorithmic_bytes": rope_bytes,
                  "traffic": read_traffic("rope_qk"), "inputs": "12 rotating qkv copies (HBM)",
+                 "copy_yardstick": {"kernel": "mi_copy_qk (the same launch without the rotation)",
+                                    "avg_us": round(copy_cold_us, 3),
+                                    "achieved": round(copy_cold_gbps, 1),
+                                    "frac": round(copy_cold_gbps / PEAK_HBM_GBPS, 4),
+                                    "bytes": copy_bytes},
+                 "frac_of_copy": round(rope_cold_gbps / copy_cold_gbps, 4),
                  "cache_resident": {"avg_us": round(rope_us, 3), "achieved": round(rope_gbps, 1),
                                     "frac": round(rope_gbps / PEAK_HBM_GBPS, 4),
                                     "inputs": "one q/k pair re-read (Infinity Cache)"}},

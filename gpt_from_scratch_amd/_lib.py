@@ -28,7 +28,7 @@ EXPORTED = ("mi_version", "mi_status_str", "mi_last_error", "mi_attn_fwd", "mi_a
             "mi_rmsnorm_bwd_workspace", "mi_rmsnorm_bwd", "mi_swiglu_fwd", "mi_swiglu_bwd",
             "mi_adamw_workspace", "mi_grad_sumsq", "mi_adamw_step", "mi_attn_bwd_noalloc",
             "mi_rmsnorm_add_fwd", "mi_rmsnorm_add_bwd", "mi_attn_bwd_rope",
-            "mi_rmsnorm_bwd_acc", "mi_rmsnorm_add_bwd_acc")
+            "mi_rmsnorm_bwd_acc", "mi_rmsnorm_add_bwd_acc", "mi_copy_qk")
 
 # B*H*S limit of mi_attn_bwd_noalloc (its static workspace array), include/mi_attn.h
 NOALLOC_MAX_ROWS = 1 << 20
@@ -82,6 +82,8 @@ def _declare(lib):
     lib.mi_rope_qk.restype = i
     lib.mi_rope_qk.argtypes = [i, i, i, i, i, i, i, p, i64p, p, i64p, p, i64p, p, i64p,
                                p, i64p, p, i64p, p]
+    lib.mi_copy_qk.restype = i
+    lib.mi_copy_qk.argtypes = [i, i, i, i, i, p, i64p, p, i64p, p, i64p, p, i64p, p]
     i64 = ctypes.c_int64
     lib.mi_xent_fwd.restype = i
     lib.mi_xent_fwd.argtypes = [i, i64, i64, p, i64, p, p, p, p]

@@ -131,7 +131,7 @@ mi::AttnArgs grad_args(int B, int H, int S, int D, int causal, float scale, cons
 
 extern "C" {
 
-int mi_version(void) { return (2 << 16) | 3; }
+int mi_version(void) { return (2 << 16) | 4; }
 
 const char* mi_status_str(mi_status s) {
   switch (s) {
@@ -502,6 +502,43 @@ mi_status mi_rope_qk(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, 
   const int64_t* ost[2] = {q_out_strides, k_out_strides};
   return rope_common(x_dtype, tab_dtype, S, B, H, D, inverse, 2, ins, ist, outs, ost, cos_tab,
                      cos_strides, sin_tab, sin_strides, stream);
+}
+
+mi_status mi_copy_qk(mi_dtype dtype, int S, int B, int H, int D, const void* q,
+                     const int64_t q_strides[4], const void* k, const int64_t k_strides[4],
+                     void* q_out, const int64_t q_out_strides[4], void* k_out,
+                     const int64_t k_out_strides[4], void* stream) {
+  if (!dtype_ok(dtype)) return fail(MI_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
+  if (S <= 0 || B <= 0 || H <= 0 || D <= 0)
+    return fail(MI_ERR_INVALID_ARGUMENT, "sizes must be positive (S=%d B=%d H=%d D=%d)", S, B, H, D);
+  const int esz = elem_size(dtype);
+  if ((D * esz) % 16) return fail(MI_ERR_UNSUPPORTED, "D * element size must be a multiple of 16");
+  if ((uint64_t)S * B * H * (D * esz / 16) >= (1ull << 31))
+    return fail(MI_ERR_UNSUPPORTED, "tensor too large for one launch");
+  const void* ins[2] = {q, k};
+  const int64_t* ist[2] = {q_strides, k_strides};
+  void* outs[2] = {q_out, k_out};
+  const int64_t* ost[2] = {q_out_strides, k_out_strides};
+  mi::RopeArgs a = {};
+  a.ntensors = 2;
+  a.S = S; a.B = B; a.H = H; a.D = D;
+  for (int t = 0; t < 2; ++t) {
+    if (!ins[t] || !outs[t] || !ist[t] || !ost[t])
+      return fail(MI_ERR_INVALID_ARGUMENT, "copy tensor %d: null pointer", t);
+    if (ist[t][3] != 1 || ost[t][3] != 1)
+      return fail(MI_ERR_UNSUPPORTED, "copy tensor %d: dim stride must be 1", t);
+    if (((uintptr_t)ins[t]) % 16 || ((uintptr_t)outs[t]) % 16)
+      return fail(MI_ERR_UNSUPPORTED, "copy tensor %d: base not 16-byte aligned", t);
+    for (int i = 0; i < 3; ++i)
+      if (ist[t][i] < 0 || ost[t][i] < 0 || (ist[t][i] * esz) % 16 || (ost[t][i] * esz) % 16)
+        return fail(MI_ERR_UNSUPPORTED, "copy tensor %d: strides must be 16-byte multiples", t);
+    mi::RopeTensor& T = a.t[t];
+    T.in = ins[t];
+    T.out = outs[t];
+    T.is_s = ist[t][0]; T.is_b = ist[t][1]; T.is_h = ist[t][2]; T.is_d = 1;
+    T.os_s = ost[t][0]; T.os_b = ost[t][1]; T.os_h = ost[t][2]; T.os_d = 1;
+  }
+  return launched(mi::launch_copy_qk(dtype, a, (hipStream_t)stream), "copy_qk");
 }
 
 static mi_status xent_common(mi_dtype dtype, int64_t rows, int64_t vocab, const void* logits,

@@ -71,6 +71,9 @@ struct RopeArgs {
 
 hipError_t launch_rope(int x_dtype, int tab_dtype, const RopeArgs& a, bool vector_ok,
                        hipStream_t st);
+// mi_copy_qk: two tensors copied with the RoPE vector path's launch (its
+// layout requirements checked by the caller).
+hipError_t launch_copy_qk(int x_dtype, const RopeArgs& a, hipStream_t st);
 
 // Softmax cross entropy over the vocabulary (model_ops.hip).  One row per
 // token; logits / grad rows are `row_stride` / `grad_row_stride` elements apart.

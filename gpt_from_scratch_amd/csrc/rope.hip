@@ -151,6 +151,44 @@ __global__ __launch_bounds__(ROPE_T) void rope_vec_kernel(RopeArgs a, RopeDivs d
   }
 }
 
+// mi_copy_qk: the vector path's items, grid and accesses without the rotation
+// (and without the tables): each lane copies the same 16 bytes of q and of k
+// for U items, all loads before the first store.
+template <int U>
+__global__ __launch_bounds__(ROPE_T) void copy_qk_vec_kernel(RopeArgs a, RopeDivs dv,
+                                                             uint32_t total) {
+  const uint32_t first = blockIdx.x * (ROPE_T * U) + threadIdx.x;
+  const int64_t ebytes = 16 / (a.D / (int)dv.C.d);  // bytes per element (D/C per 16-byte chunk)
+  u32x4 x[U][2];
+  int64_t out_off[U][2];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const uint32_t item = first + ROPE_T * u;
+    if (item >= total) continue;
+    uint32_t r = fdiv(item, dv.C);
+    const uint32_t cidx = item - r * dv.C.d;
+    const uint32_t r2 = fdiv(r, dv.H);
+    const uint32_t h = r - r2 * dv.H.d;
+    const uint32_t s = fdiv(r2, dv.B);
+    const uint32_t b = r2 - s * dv.B.d;
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      const RopeTensor& T = a.t[t];
+      // byte offsets (the strides count elements)
+      const int64_t in_off = (s * T.is_s + b * T.is_b + h * T.is_h) * ebytes + (int64_t)cidx * 16;
+      out_off[u][t] = (s * T.os_s + b * T.os_b + h * T.os_h) * ebytes + (int64_t)cidx * 16;
+      x[u][t] = __builtin_nontemporal_load((const u32x4*)((const char*)T.in + in_off));
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    if (first + ROPE_T * u >= total) continue;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      __builtin_nontemporal_store(x[u][t], (u32x4*)((char*)a.t[t].out + out_off[u][t]));
+  }
+}
+
 // Scalar path: one pair per lane, any strides.
 template <int XDT, int TDT>
 __global__ __launch_bounds__(256) void rope_pair_kernel(RopeArgs a, RopeDivs dv, uint32_t total) {
@@ -219,6 +257,21 @@ hipError_t rope_x(int tab_dtype, const RopeArgs& a, bool vec, hipStream_t st) {
 }
 
 }  // namespace
+
+hipError_t launch_copy_qk(int x_dtype, const RopeArgs& a, hipStream_t st) {
+  const int vecn = (x_dtype == 0) ? 4 : 8;
+  const int C = a.D / vecn;
+  RopeDivs dv;
+  dv.C = make_fastdiv(C);
+  dv.H = make_fastdiv(a.H);
+  dv.B = make_fastdiv(a.B);
+  dv.S = make_fastdiv(a.S);
+  const uint64_t total = (uint64_t)a.S * a.B * a.H * C;
+  constexpr int U = 3;  // as the RoPE vector path
+  const dim3 grid((uint32_t)((total + ROPE_T * U - 1) / (ROPE_T * U))), block(ROPE_T);
+  hipLaunchKernelGGL((copy_qk_vec_kernel<U>), grid, block, 0, st, a, dv, (uint32_t)total);
+  return hipGetLastError();
+}
 
 hipError_t launch_rope(int x_dtype, int tab_dtype, const RopeArgs& a, bool vector_ok,
                        hipStream_t st) {

@@ -107,10 +107,12 @@ mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal,
  * tables (interleaved pairs, the rotation of mi_rope with inverse = 1,
  * evaluated on dQ and dK rounded to `dtype` first, so the result equals
  * mi_attn_bwd followed by mi_rope_qk(inverse = 1) on dq, dk in place, bit for
- * bit).  On the matrix-core path at D = 64 with 16-bit tables whose angles
- * are contiguous and whose row starts are 4-angle aligned (the model's), the
- * rotation is applied as the kernels store dQ and dK, saving the separate read
- * and write of both; otherwise the two run one after the other.  cos / sin:
+ * bit).  On the matrix-core path (D = 64 or 128) with 16-bit tables whose
+ * angles are contiguous and whose row starts are 4-angle aligned (the
+ * model's), the rotation is applied as the kernels store dQ and dK, saving the
+ * separate read and write of both; otherwise the two run one after the other
+ * (a shape past the separate pass's launch limit, 2^31 angle pairs, is then
+ * refused with MI_ERR_UNSUPPORTED before anything is enqueued).  cos / sin:
  * [>= S rows, D/2 angles], strides in elements, dtype tab_dtype.  Replaces the attention block's backward pair,
  * FlashAttn.backward (core/myFlashAttn.py:288-441) then TritonRoPE.backward
  * on dq and dk (core/rope_triton.py:50-72), as driven by the autograd of
@@ -223,6 +225,22 @@ mi_status mi_rope_qk(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, 
                      const void* k, const int64_t k_strides[4],
                      const void* cos_tab, const int64_t cos_strides[2],
                      const void* sin_tab, const int64_t sin_strides[2],
+                     void* q_out, const int64_t q_out_strides[4],
+                     void* k_out, const int64_t k_out_strides[4],
+                     void* stream);
+
+/*
+ * Copy of two [S, B, H, D] tensors (q and k views, any 16-byte aligned row
+ * strides) into outputs of any 16-byte aligned row strides: the relayout that
+ * FlashAttn.forward's .contiguous() calls perform (core/myFlashAttn.py:206-208),
+ * run with mi_rope_qk's launch (the same items, grid and memory accesses,
+ * without the rotation and the tables), so it is also the streaming ceiling
+ * of that launch.  Requires unit dim strides, D a multiple of 16 bytes and
+ * 16-byte aligned bases and row strides (MI_ERR_UNSUPPORTED otherwise).
+ */
+mi_status mi_copy_qk(mi_dtype dtype, int S, int B, int H, int D,
+                     const void* q, const int64_t q_strides[4],
+                     const void* k, const int64_t k_strides[4],
                      void* q_out, const int64_t q_out_strides[4],
                      void* k_out, const int64_t k_out_strides[4],
                      void* stream);

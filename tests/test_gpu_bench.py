@@ -43,6 +43,15 @@ def test_bench_prints_one_contract_line(gpu, capsys, monkeypatch):
     assert rf["bound"] in ("hbm", "mfma") and rf["peak"] == 2500.0
     assert 0 < rf["frac"] <= 1 and rf["frac"] == pytest.approx(rf["achieved"] / rf["peak"], rel=1e-3)
 
+    # the HBM-cold pass of the same step, and RoPE beside its same-launch copy
+    hc = d["config2_hbm_cold"]
+    assert hc["sets"] * hc["set_bytes"] > 256 * 2 ** 20  # more than the Infinity Cache
+    assert hc["step_us"] > 0 and set(hc["kernels"]) == {"attn_fwd", "attn_bwd_preprocess", "attn_bwd"}
+    assert hc["tflops"] == pytest.approx(gflop / (hc["step_us"] * 1e-3), rel=1e-2)
+    cy = d["rope"]["copy_yardstick"]
+    assert cy["avg_us"] > 0 and 0 < cy["frac"] <= 1
+    assert d["rope"]["frac_of_copy"] == pytest.approx(d["rope"]["frac"] / cy["frac"], rel=1e-2)
+
     cb = d["cpu_baseline"]
     for k in ("value", "unit", "cores", "kind", "sample"):
         assert k in cb, k

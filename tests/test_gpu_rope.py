@@ -182,3 +182,32 @@ def test_in_place(gpu, dtype, D):
         _lib.rope(yq, cos, sin, yq, inverse)
         assert torch.equal(yq, want_q)
         assert torch.equal(y[:, :, 1:], qkv[:, :, 1:])  # nothing else touched
+
+
+@pytest.mark.parametrize("dtype,B,H,S,D", [(torch.bfloat16, 8, 12, 1024, 64),
+                                           (torch.bfloat16, 1, 5, 37, 64),
+                                           (torch.float32, 3, 7, 19, 128)])
+def test_copy_qk_is_the_relayout(gpu, dtype, B, H, S, D):
+    """mi_copy_qk (RoPE's launch without the rotation) writes exactly the dense
+    copies of the strided q/k views, ragged last workgroup included, and leaves
+    the bytes around its outputs alone; layouts it cannot stream are refused."""
+    import ctypes
+    from gpt_from_scratch_amd import _lib
+    lib = _lib.lib()
+    q, k, _, _, _, _ = rope_inputs(B, H, S, D, 60 + S, 1.0, dtype, gpu)
+    pad = torch.full((2, S * B * H * D + 64), 7.0, dtype=dtype, device=gpu)
+    outq = pad[0, :S * B * H * D].view(S, B, H, D)
+    outk = pad[1, :S * B * H * D].view(S, B, H, D)
+    st = lambda t: _lib._strides(t, 4)
+    dt = _lib.dtype_code(q)
+    r = lib.mi_copy_qk(dt, S, B, H, D, _lib._ptr(q), st(q), _lib._ptr(k), st(k),
+                       _lib._ptr(outq), st(outq), _lib._ptr(outk), st(outk), _lib._stream(q))
+    assert r == 0, lib.mi_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(outq, q) and torch.equal(outk, k)
+    assert bool((pad[:, S * B * H * D:] == 7.0).all())
+    # a row that is not a multiple of 16 bytes cannot take the 16-byte path
+    bad = torch.zeros(S, B, H, 4, dtype=torch.bfloat16, device=gpu)
+    r = lib.mi_copy_qk(2, S, B, H, 4, _lib._ptr(bad), st(bad), _lib._ptr(bad), st(bad),
+                       _lib._ptr(bad), st(bad), _lib._ptr(bad), st(bad), _lib._stream(bad))
+    assert r == 2 and b"16" in lib.mi_last_error()
