@@ -10,9 +10,13 @@
 #include <cmath>
 #include <initializer_list>
 #include <utility>
+#include <dlfcn.h>
+#include <limits.h>
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
+#include <unistd.h>
 
 #include <string>
 
@@ -38,6 +42,41 @@ mi_status ok() {
   g_last_error.clear();
   return MI_OK;
 }
+
+// One build of this library per process.  Two builds loaded side by side
+// register kernels of the same names with the HIP runtime, and a process that
+// held four builds at once saw every build's outputs change from call to call
+// (cause not traced; each build alone is bitwise deterministic).  The first
+// copy loaded records "<pid>:<path>" in MI_ATTN_LIBRARY (the pid keeps a child
+// process from inheriting the claim); a copy from another path that finds its
+// own pid there refuses every entry point that launches work.
+char g_first_copy[PATH_MAX + 32];  // set when another copy claimed the process first
+
+__attribute__((constructor)) void claim_process() {
+  Dl_info info;
+  char self[PATH_MAX];
+  if (!dladdr((void*)&claim_process, &info) || !info.dli_fname || !realpath(info.dli_fname, self))
+    return;
+  char mine[PATH_MAX + 32];
+  snprintf(mine, sizeof(mine), "%ld:%s", (long)getpid(), self);
+  const char* prev = getenv("MI_ATTN_LIBRARY");
+  char pid[32];
+  const int np = snprintf(pid, sizeof(pid), "%ld:", (long)getpid());
+  if (prev && strncmp(prev, pid, np) == 0) {
+    if (strcmp(prev, mine) != 0) snprintf(g_first_copy, sizeof(g_first_copy), "%s", prev + np);
+    return;
+  }
+  setenv("MI_ATTN_LIBRARY", mine, 1);
+}
+
+#define MI_SOLE_COPY()                                                                      \
+  do {                                                                                      \
+    if (g_first_copy[0])                                                                    \
+      return fail(MI_ERR_UNSUPPORTED,                                                       \
+                  "another build of libmi_attn (%s) is loaded in this process; one build "  \
+                  "per process",                                                            \
+                  g_first_copy);                                                            \
+  } while (0)
 
 int elem_size(int dt) { return dt == MI_F32 ? 4 : 2; }
 
@@ -149,6 +188,7 @@ mi_status mi_attn_fwd(mi_dtype dtype, int B, int H, int S, int D, int causal, fl
                       const void* q, const int64_t q_strides[4], const void* k,
                       const int64_t k_strides[4], const void* v, const int64_t v_strides[4],
                       void* o, const int64_t o_strides[4], float* lse, void* stream) {
+  MI_SOLE_COPY();
   mi_status st;
   if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
   if ((st = check_attn_tensor("q", q, q_strides)) != MI_OK) return st;
@@ -195,6 +235,7 @@ mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal, fl
                       const int64_t dout_strides[4], const float* lse, float* ws, void* dq,
                       const int64_t dq_strides[4], void* dk, const int64_t dk_strides[4],
                       void* dv, const int64_t dv_strides[4], void* stream) {
+  MI_SOLE_COPY();
   // Validate everything up front so that nothing is enqueued on a bad call.
   mi_status st;
   if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
@@ -221,6 +262,7 @@ mi_status mi_attn_bwd_grads(mi_dtype dtype, int B, int H, int S, int D, int caus
                             void* dq, const int64_t dq_strides[4], void* dk,
                             const int64_t dk_strides[4], void* dv, const int64_t dv_strides[4],
                             void* stream) {
+  MI_SOLE_COPY();
   return grads_impl(dtype, B, H, S, D, causal, scale, q, q_strides, k, k_strides, v, v_strides,
                     dout, dout_strides, lse, ws, dq, dq_strides, dk, dk_strides, dv, dv_strides,
                     nullptr, stream);
@@ -318,6 +360,7 @@ mi_status mi_attn_bwd_rope(mi_dtype dtype, int B, int H, int S, int D, int causa
                            void* dv, const int64_t dv_strides[4], mi_dtype tab_dtype,
                            const void* cos_tab, const int64_t cos_strides[2],
                            const void* sin_tab, const int64_t sin_strides[2], void* stream) {
+  MI_SOLE_COPY();
   mi_status st;
   if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
   if ((st = check_attn_tensor("o", o, o_strides)) != MI_OK) return st;
@@ -361,6 +404,7 @@ mi_status mi_attn_bwd_preprocess(mi_dtype dtype, int B, int H, int S, int D, con
                                  const int64_t o_strides[4], const void* dout,
                                  const int64_t dout_strides[4], const float* lse, float* ws,
                                  void* stream) {
+  MI_SOLE_COPY();
   mi_status st;
   if ((st = check_shape(dtype, B, H, S, D, 1.f)) != MI_OK) return st;
   if ((st = check_attn_tensor("o", o, o_strides)) != MI_OK) return st;
@@ -382,6 +426,7 @@ mi_status mi_attn_bwd_dkdv(mi_dtype dtype, int B, int H, int S, int D, int causa
                            const void* dout, const int64_t dout_strides[4], const float* lse,
                            const float* ws, void* dk, const int64_t dk_strides[4], void* dv,
                            const int64_t dv_strides[4], void* stream) {
+  MI_SOLE_COPY();
   mi_status st;
   if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
   if ((st = check_grad_inputs(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
@@ -409,6 +454,7 @@ mi_status mi_attn_bwd_dq(mi_dtype dtype, int B, int H, int S, int D, int causal,
                          const void* dout, const int64_t dout_strides[4], const float* lse,
                          const float* ws, void* dq, const int64_t dq_strides[4],
                          void* stream) {
+  MI_SOLE_COPY();
   mi_status st;
   if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
   if ((st = check_grad_inputs(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
@@ -482,6 +528,7 @@ mi_status mi_rope(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, int
                   const void* x, const int64_t x_strides[4], const void* cos_tab,
                   const int64_t cos_strides[2], const void* sin_tab, const int64_t sin_strides[2],
                   void* out, const int64_t out_strides[4], void* stream) {
+  MI_SOLE_COPY();
   const void* ins[1] = {x};
   const int64_t* ist[1] = {x_strides};
   void* outs[1] = {out};
@@ -496,6 +543,7 @@ mi_status mi_rope_qk(mi_dtype x_dtype, mi_dtype tab_dtype, int S, int B, int H, 
                      const void* sin_tab, const int64_t sin_strides[2], void* q_out,
                      const int64_t q_out_strides[4], void* k_out, const int64_t k_out_strides[4],
                      void* stream) {
+  MI_SOLE_COPY();
   const void* ins[2] = {q, k};
   const int64_t* ist[2] = {q_strides, k_strides};
   void* outs[2] = {q_out, k_out};
@@ -508,6 +556,7 @@ mi_status mi_copy_qk(mi_dtype dtype, int S, int B, int H, int D, const void* q,
                      const int64_t q_strides[4], const void* k, const int64_t k_strides[4],
                      void* q_out, const int64_t q_out_strides[4], void* k_out,
                      const int64_t k_out_strides[4], void* stream) {
+  MI_SOLE_COPY();
   if (!dtype_ok(dtype)) return fail(MI_ERR_INVALID_ARGUMENT, "unknown dtype %d", dtype);
   if (S <= 0 || B <= 0 || H <= 0 || D <= 0)
     return fail(MI_ERR_INVALID_ARGUMENT, "sizes must be positive (S=%d B=%d H=%d D=%d)", S, B, H, D);
@@ -566,6 +615,7 @@ static mi_status xent_common(mi_dtype dtype, int64_t rows, int64_t vocab, const 
 mi_status mi_xent_fwd(mi_dtype dtype, int64_t rows, int64_t vocab, const void* logits,
                       int64_t row_stride, const int64_t* target, void* loss, float* lse,
                       void* stream) {
+  MI_SOLE_COPY();
   mi::XentArgs a;
   if (mi_status st = xent_common(dtype, rows, vocab, logits, row_stride, target, a)) return st;
   if (!loss || !lse) return fail(MI_ERR_INVALID_ARGUMENT, "loss / lse: null pointer");
@@ -580,6 +630,7 @@ mi_status mi_xent_bwd(mi_dtype dtype, int64_t rows, int64_t vocab, const void* l
                       int64_t row_stride, const int64_t* target, const float* lse,
                       const void* grad_loss, void* grad_logits, int64_t grad_row_stride,
                       void* stream) {
+  MI_SOLE_COPY();
   mi::XentArgs a;
   if (mi_status st = xent_common(dtype, rows, vocab, logits, row_stride, target, a)) return st;
   if (!lse || !grad_loss || !grad_logits)
@@ -697,6 +748,7 @@ static mi_status rms_fwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64
 mi_status mi_rmsnorm_fwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64_t hidden,
                          float eps, const void* x, int64_t x_row_stride, const void* weight,
                          void* y, int64_t y_row_stride, float* rstd, void* stream) {
+  MI_SOLE_COPY();
   return rms_fwd(x_dtype, w_dtype, rows, hidden, eps, x, x_row_stride, nullptr, 0, weight,
                  nullptr, 0, y, y_row_stride, rstd, stream);
 }
@@ -706,6 +758,7 @@ mi_status mi_rmsnorm_add_fwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, i
                              int64_t res_row_stride, const void* weight, void* sum,
                              int64_t sum_row_stride, void* y, int64_t y_row_stride, float* rstd,
                              void* stream) {
+  MI_SOLE_COPY();
   if (!res || !sum) return fail(MI_ERR_INVALID_ARGUMENT, "residual / sum: null pointer");
   return rms_fwd(x_dtype, w_dtype, rows, hidden, eps, x, x_row_stride, res, res_row_stride,
                  weight, sum, sum_row_stride, y, y_row_stride, rstd, stream);
@@ -766,6 +819,7 @@ mi_status mi_rmsnorm_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64
                          const float* rstd, const void* dy, int64_t dy_row_stride, void* dx,
                          int64_t dx_row_stride, void* dweight, float* workspace,
                          int64_t workspace_elems, void* stream) {
+  MI_SOLE_COPY();
   return rms_bwd(x_dtype, w_dtype, rows, hidden, x, x_row_stride, weight, rstd, dy,
                  dy_row_stride, nullptr, 0, dx, dx_row_stride, dweight, workspace,
                  workspace_elems, stream);
@@ -777,6 +831,7 @@ mi_status mi_rmsnorm_add_bwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, i
                              const void* dsum, int64_t dsum_row_stride, void* dx,
                              int64_t dx_row_stride, void* dweight, float* workspace,
                              int64_t workspace_elems, void* stream) {
+  MI_SOLE_COPY();
   if (!dsum) return fail(MI_ERR_INVALID_ARGUMENT, "dsum: null pointer");
   return rms_bwd(x_dtype, w_dtype, rows, hidden, sum, sum_row_stride, weight, rstd, dy,
                  dy_row_stride, dsum, dsum_row_stride, dx, dx_row_stride, dweight, workspace,
@@ -788,6 +843,7 @@ mi_status mi_rmsnorm_bwd_acc(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, i
                              const float* rstd, const void* dy, int64_t dy_row_stride, void* dx,
                              int64_t dx_row_stride, void* dweight, float* workspace,
                              int64_t workspace_elems, void* stream) {
+  MI_SOLE_COPY();
   return rms_bwd(x_dtype, w_dtype, rows, hidden, x, x_row_stride, weight, rstd, dy,
                  dy_row_stride, nullptr, 0, dx, dx_row_stride, dweight, workspace,
                  workspace_elems, stream, true);
@@ -799,6 +855,7 @@ mi_status mi_rmsnorm_add_bwd_acc(mi_dtype x_dtype, mi_dtype w_dtype, int64_t row
                                  int64_t dy_row_stride, const void* dsum, int64_t dsum_row_stride,
                                  void* dx, int64_t dx_row_stride, void* dweight, float* workspace,
                                  int64_t workspace_elems, void* stream) {
+  MI_SOLE_COPY();
   if (!dsum) return fail(MI_ERR_INVALID_ARGUMENT, "dsum: null pointer");
   return rms_bwd(x_dtype, w_dtype, rows, hidden, sum, sum_row_stride, weight, rstd, dy,
                  dy_row_stride, dsum, dsum_row_stride, dx, dx_row_stride, dweight, workspace,
@@ -839,6 +896,7 @@ static bool swiglu_vec_ok(int dtype, int64_t inter, std::initializer_list<const 
 mi_status mi_swiglu_fwd(mi_dtype dtype, int64_t rows, int64_t inter, const void* gate_up,
                         int64_t gate_up_row_stride, void* out, int64_t out_row_stride,
                         void* stream) {
+  MI_SOLE_COPY();
   if (mi_status st = swiglu_common(dtype, rows, inter, gate_up, gate_up_row_stride, out,
                                    out_row_stride, inter))
     return st;
@@ -852,6 +910,7 @@ mi_status mi_swiglu_fwd(mi_dtype dtype, int64_t rows, int64_t inter, const void*
 mi_status mi_swiglu_bwd(mi_dtype dtype, int64_t rows, int64_t inter, const void* gate_up,
                         int64_t gate_up_row_stride, const void* dout, int64_t dout_row_stride,
                         void* dgate_up, int64_t dgate_up_row_stride, void* stream) {
+  MI_SOLE_COPY();
   if (mi_status st = swiglu_common(dtype, rows, inter, gate_up, gate_up_row_stride, dgate_up,
                                    dgate_up_row_stride, 2 * inter))
     return st;
@@ -873,6 +932,7 @@ int64_t mi_adamw_workspace(void) { return 1 + mi::adam_parts(); }
 
 mi_status mi_grad_sumsq(mi_dtype grad_dtype, int64_t n, const void* grad, float* workspace,
                         int64_t workspace_elems, void* stream) {
+  MI_SOLE_COPY();
   if (!dtype_ok(grad_dtype)) return fail(MI_ERR_INVALID_ARGUMENT, "unknown dtype %d", grad_dtype);
   if (n <= 0) return fail(MI_ERR_INVALID_ARGUMENT, "n must be positive (got %lld)", (long long)n);
   if (!grad || !workspace) return fail(MI_ERR_INVALID_ARGUMENT, "grad / workspace: null pointer");
@@ -892,6 +952,7 @@ mi_status mi_adamw_step(mi_dtype grad_dtype, mi_dtype param_dtype, int64_t n, co
                         float weight_decay_factor, float lerp_weight, float beta2,
                         float one_minus_beta2, float step_size, float bias_correction2_sqrt,
                         float eps, float clip, const float* grad_sumsq, void* stream) {
+  MI_SOLE_COPY();
   if (!dtype_ok(grad_dtype) || !dtype_ok(param_dtype))
     return fail(MI_ERR_INVALID_ARGUMENT, "unknown dtype (grad %d, param %d)", grad_dtype,
                 param_dtype);
@@ -974,6 +1035,7 @@ extern "C" mi_status mi_attn_bwd_noalloc(
     const int64_t v_strides[4], const void* o, const int64_t o_strides[4], const void* dout,
     const int64_t dout_strides[4], const float* lse, void* dq, const int64_t dq_strides[4],
     void* dk, const int64_t dk_strides[4], void* dv, const int64_t dv_strides[4], void* stream) {
+  MI_SOLE_COPY();
   mi_status st;
   if ((st = check_shape(dtype, B, H, S, D, scale)) != MI_OK) return st;
   const int64_t rows = (int64_t)B * H * S;

@@ -291,3 +291,32 @@ def test_new_entry_points_reject_bad_arguments():
     big = [2, 1, 512, 65536, 64, 1, 0.125] + args[7:]
     assert lib.mi_attn_bwd_rope(*big, 0, fake, t2, fake, t2, None) == 2
     assert b"too large" in lib.mi_last_error()
+
+
+def test_second_build_in_one_process_is_refused(tmp_path):
+    """A process holds one build of the library: a second copy loaded from
+    another path refuses every launching entry point (the first keeps working),
+    and a child process makes its own claim."""
+    import shutil
+    import subprocess
+    import sys
+    dup = tmp_path / "libmi_attn_copy.so"
+    shutil.copy(_lib.LIB_PATH, dup)
+    code = f"""
+import ctypes, torch
+def load(path):
+    lib = ctypes.CDLL(path)
+    lib.mi_last_error.restype = ctypes.c_char_p
+    return lib
+a, b = load({_lib.LIB_PATH!r}), load({str(dup)!r})
+st = (ctypes.c_int64 * 4)(0, 0, 64, 1)
+f = ctypes.c_void_p(16)
+args = (1, 1, 64, 64, 1, ctypes.c_float(0.125), f, st, f, st, f, st, f, st, f, None)
+assert a.mi_attn_fwd(7, *args) == 1 and b"dtype" in a.mi_last_error()
+assert b.mi_attn_fwd(7, *args) == 2, b.mi_last_error()
+assert b"another build" in b.mi_last_error()
+assert {os.path.realpath(_lib.LIB_PATH)!r}.encode() in b.mi_last_error()
+print("ok")
+"""
+    r = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=300)
+    assert r.returncode == 0 and r.stdout.strip().endswith("ok"), r.stderr[-2000:]

@@ -77,17 +77,60 @@ def _oracle_block(qkv, cos, sin, H, g, causal):
     return o.detach(), x.grad
 
 
+def _slot_budget(qkv, cos, sin, H, g, o, want_slot, causal):
+    """Element-wise bound on |got - want| for the q and k slots of the qkv
+    gradient ([S, B, 2, H, D]).
+
+    The slot is the inverse rotation R^-1 of the attention gradient dQ (dK),
+    rounded once more.  The reference rounds dQ to bf16 before its inverse-RoPE
+    kernel (myFlashAttn.py:349-351 into rope_triton.py:50-72) and so does the
+    oracle chain; this build rounds dQ the same way, rotates it in fp32 and
+    rounds the result.  So, per element:
+      * the attention gradient may sit gpu_ref.grad_rounding_budget from the
+        fp32 one (evaluated on the rotated, rounded q and k the kernels see),
+        and the oracle's own rounding of it adds one bf16 ulp (u = 2^-8) of it;
+      * R^-1 rotates each interleaved pair (2i, 2i+1) by one angle: it keeps a
+        pair's error vector's length, so an element's error is at most the
+        norm of its pair's two bounds;
+      * the final rounding adds u |want| (and a 1e-4 floor covers the fp32
+        rotation arithmetic).
+    """
+    from gpu_ref import grad_rounding_budget
+    from oracle import rope_apply
+    S, B, _ = qkv.shape
+    D = qkv.shape[-1] // (3 * H)
+    u = 2.0 ** -8
+    q, k, v = qkv.view(S, B, 3, H, D).unbind(2)
+    c, s = cos.float(), sin.float()
+    qr = rope_apply(q, c, s, dtype=torch.float32).to(qkv.dtype)
+    kr = rope_apply(k, c, s, dtype=torch.float32).to(qkv.dtype)
+    to_bhsd = lambda t: t.permute(1, 2, 0, 3)
+    o4 = to_bhsd(o.detach().view(S, B, H, D))
+    do4 = to_bhsd(g.view(S, B, H, D))
+    slots = []
+    for name, i in (("dq", 0), ("dk", 1)):
+        budgets = []
+        for b in range(B):
+            want_b, bud_b = grad_rounding_budget(to_bhsd(qr)[b:b + 1], to_bhsd(kr)[b:b + 1],
+                                                 to_bhsd(v)[b:b + 1], do4[b:b + 1],
+                                                 o4[b:b + 1], causal)
+            budgets.append(bud_b[name] + u * want_b[name].abs())
+        e = torch.cat(budgets).permute(2, 0, 1, 3)           # [S, B, H, D]
+        pair = e.reshape(S, B, H, D // 2, 2).norm(dim=-1, keepdim=True).expand(S, B, H, D // 2, 2)
+        slots.append(pair.reshape(S, B, H, D).cpu() + u * want_slot[:, :, i].abs() + 1e-4)
+    return slots
+
+
 @pytest.mark.parametrize("S,B,H,D,std", [(1024, 8, 12, 64, 1.0), (2048, 1, 4, 128, 0.5)])
 def test_block_against_oracle(gpu, S, B, H, D, std):
     """The fused block (RoPE into a [S, B, 2, H, D] buffer, attention on strided
     views, O stored as [S, B, H*D], dQ/dK/dV into one [S, B, 3, H, D] gradient
     with the inverse rotation in place) against the oracle's autograd of the
     unfused reference chain: config 2's shape and a D = 128 shape.  Output and
-    each slot of the qkv gradient (the q and k slots carry the in-place inverse
-    rotation) within the bf16 bounds (max-abs 2e-2, mean-rel 1e-2); the q and k
-    slots are rounded once more than an attention gradient (the inverse
-    rotation's output), so their elements may also move by that rounding,
-    2^-8 |ref|."""
+    the v slot within the bf16 bounds (max-abs 2e-2, mean-rel 1e-2); the q and
+    k slots (the inverse rotation's output, rounded once more than an
+    attention gradient) element by element within the rounding budget
+    _slot_budget derives, and within mean-rel 1e-2."""
     from gpt_from_scratch_amd import RotaryEmbedding, attention_block
     from gpu_ref import assert_close_bf16
     qkv = seeded((S, B, 3 * H * D), 190 + D, std).to(gpu)
@@ -102,8 +145,11 @@ def test_block_against_oracle(gpu, S, B, H, D, std):
     got = x.grad.cpu().view(S, B, 3, H, D)
     want = rgrad.view(S, B, 3, H, D)
     assert_close_bf16("dv", got[:, :, 2], want[:, :, 2])
+    budgets = _slot_budget(qkv, cos, sin, H, g, o, want, True)
     for i, name in ((0, "dq"), (1, "dk")):
         err = (got[:, :, i].float() - want[:, :, i]).abs()
-        bound = 2e-2 + 2.0 ** -8 * want[:, :, i].abs()
-        assert bool((err <= bound).all()), (name, float(err.max()), float((err - bound).max()))
+        worst = float((err / budgets[i]).max())
+        print(f"S{S} D{D} {name} slot: worst error {worst:.3f} of the budget, "
+              f"max-abs {float(err.max()):.3e}")
+        assert worst <= 1.0, (name, worst)
         assert float(err.mean() / want[:, :, i].abs().mean()) <= 1e-2, name
