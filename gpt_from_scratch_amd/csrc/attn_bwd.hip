@@ -884,14 +884,19 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a, int n_q
 // two kinds alternating (rank r: kind r & 1; key tile r/2, or query tile
 // n_tiles-1-r/2, the tiles that see the most of the sequence under causal
 // masking), so the short tails of both kinds overlap the long heads of the
-// other and the launch keeps the whole chip busy.
+// other and the launch keeps the whole chip busy.  only_kind 0 or 1 runs the
+// items of that kind alone (rank r: tile r of it, heaviest first): the D = 64
+// separate launches use this kernel, whose compiled item bodies have no
+// scratch (standalone instantiations of the dK/dV item spilled 8-28 bytes).
 template <typename E, int D, bool CAUSAL, bool ROPE>
-__global__ __launch_bounds__(256, 2) void attn_bwd_kernel(AttnArgs a, int n_tiles) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_kernel(AttnArgs a, int n_tiles,
+                                                          int only_kind) {
   const int BH = a.B * a.H;
   const int rank = blockIdx.x / BH;
-  const int kind = rank & 1;
+  const int kind = only_kind < 0 ? rank & 1 : only_kind;
+  const int r = only_kind < 0 ? rank >> 1 : rank;
   run_item<E, D, CAUSAL, ROPE>(
-      a, BwdItem{kind, kind ? n_tiles - 1 - (rank >> 1) : (rank >> 1), (int)(blockIdx.x % BH)});
+      a, BwdItem{kind, kind ? n_tiles - 1 - r : r, (int)(blockIdx.x % BH)});
 }
 
 template <typename E, int D, bool ROPE>
@@ -920,36 +925,45 @@ hipError_t launch_dq_dr(const AttnArgs& a, hipStream_t st) {
   return hipGetLastError();
 }
 
-// The separate launches rotate only at D = 128 (the D = 64 rotation runs in
-// the combined launch).
-template <typename E, int D>
-hipError_t launch_dkdv_d(const AttnArgs& a, hipStream_t st) {
-  if constexpr (D == 128)
-    if (a.rope.cos) return launch_dkdv_dr<E, D, true>(a, st);
-  return launch_dkdv_dr<E, D, false>(a, st);
-}
-
-template <typename E, int D>
-hipError_t launch_dq_d(const AttnArgs& a, hipStream_t st) {
-  if constexpr (D == 128)
-    if (a.rope.cos) return launch_dq_dr<E, D, true>(a, st);
-  return launch_dq_dr<E, D, false>(a, st);
-}
-
 // (One instantiation with the rotation applied at run time: compiled without
 // the rotating stores, the causal kernel's registers spilled 12 bytes.)
+// only_kind: -1 both kinds interleaved, else that kind alone.
 template <typename E, int D, bool CAUSAL>
-hipError_t launch_both_dc(const AttnArgs& a, hipStream_t st) {
+hipError_t launch_both_dc(const AttnArgs& a, int only_kind, hipStream_t st) {
   const int BH = a.B * a.H;
   const int n = (a.S + BwdCfg<D>::OWN - 1) / BwdCfg<D>::OWN;
-  hipLaunchKernelGGL((attn_bwd_kernel<E, D, CAUSAL, true>), dim3(2 * n * BH), dim3(256), 0, st,
-                     a, n);
+  hipLaunchKernelGGL((attn_bwd_kernel<E, D, CAUSAL, true>), dim3((only_kind < 0 ? 2 : 1) * n * BH),
+                     dim3(256), 0, st, a, n, only_kind);
   return hipGetLastError();
 }
 
 template <typename E, int D>
-hipError_t launch_both_d(const AttnArgs& a, hipStream_t st) {
-  return a.causal ? launch_both_dc<E, D, true>(a, st) : launch_both_dc<E, D, false>(a, st);
+hipError_t launch_both_d(const AttnArgs& a, hipStream_t st, int only_kind = -1) {
+  return a.causal ? launch_both_dc<E, D, true>(a, only_kind, st)
+                  : launch_both_dc<E, D, false>(a, only_kind, st);
+}
+
+// The separate launches: at D = 64 the combined kernel restricted to one kind
+// (it rotates only when a.rope.cos is set, which these entry points leave
+// unset); at D = 128 the kernels of one kind, rotating when a.rope.cos is set.
+template <typename E, int D>
+hipError_t launch_dkdv_d(const AttnArgs& a, hipStream_t st) {
+  if constexpr (D == 64) {
+    return launch_both_d<E, D>(a, st, 0);
+  } else {
+    if (a.rope.cos) return launch_dkdv_dr<E, D, true>(a, st);
+    return launch_dkdv_dr<E, D, false>(a, st);
+  }
+}
+
+template <typename E, int D>
+hipError_t launch_dq_d(const AttnArgs& a, hipStream_t st) {
+  if constexpr (D == 64) {
+    return launch_both_d<E, D>(a, st, 1);
+  } else {
+    if (a.rope.cos) return launch_dq_dr<E, D, true>(a, st);
+    return launch_dq_dr<E, D, false>(a, st);
+  }
 }
 
 template <typename E>

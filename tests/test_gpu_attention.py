@@ -344,6 +344,47 @@ def test_backward_deterministic_writes_every_output_keeps_inputs(gpu, B, H, S, D
     assert all(torch.equal(a, b) for a, b in zip(before, (Q, K, V, dO, M, Dl)))
 
 
+@pytest.mark.parametrize("causal", [1, 0])
+@pytest.mark.parametrize("B,H,S,D", [(2, 3, 576, 64), (1, 2, 512, 128)])
+def test_separate_dkdv_dq_equal_combined(gpu, B, H, S, D, causal):
+    """mi_attn_bwd_dkdv then mi_attn_bwd_dq (the reference's `_attn_bwd_LoopQ`
+    and `_attn_bwd_LoopKV` launches, core/myFlashAttn.py:349-439) on NaN-filled
+    outputs give the same bits as mi_attn_bwd_grads, which runs both kinds of
+    work item in one launch at D = 64: the items accumulate in the same order
+    whichever launch runs them.  S = 576 leaves the last 128-row item half
+    empty; each entry point writes only its own outputs."""
+    import ctypes
+    from gpt_from_scratch_amd import _lib
+    lib = _lib.lib()
+    g = torch.Generator(device=gpu).manual_seed(11)
+    Q, K, V, dO = (torch.randn(B, H, S, D, generator=g, device=gpu).to(torch.bfloat16)
+                   for _ in range(4))
+    O = torch.empty_like(Q)
+    M = torch.empty(B, H, S, device=gpu)
+    Dl = torch.empty(2, B, H, S, device=gpu)
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    ST = lambda t: (ctypes.c_int64 * 4)(*t.stride())
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    sc = 1 / math.sqrt(D)
+    ins = (P(Q), ST(Q), P(K), ST(K), P(V), ST(V))
+    assert lib.mi_attn_fwd(2, B, H, S, D, causal, sc, *ins, P(O), ST(O), P(M), sp) == 0
+    assert lib.mi_attn_bwd_preprocess(2, B, H, S, D, P(O), ST(O), P(dO), ST(dO), P(M), P(Dl),
+                                      sp) == 0
+    gin = (2, B, H, S, D, causal, sc) + ins + (P(dO), ST(dO), P(M), P(Dl))
+    want = [torch.full_like(Q, float("nan")) for _ in range(3)]
+    assert lib.mi_attn_bwd_grads(*gin, P(want[0]), ST(want[0]), P(want[1]), ST(want[1]),
+                                 P(want[2]), ST(want[2]), sp) == 0
+    dQ, dK, dV = (torch.full_like(Q, float("nan")) for _ in range(3))
+    assert lib.mi_attn_bwd_dkdv(*gin, P(dK), ST(dK), P(dV), ST(dV), sp) == 0
+    torch.cuda.synchronize()
+    assert bool(torch.isnan(dQ).all())
+    assert lib.mi_attn_bwd_dq(*gin, P(dQ), ST(dQ), sp) == 0
+    torch.cuda.synchronize()
+    for got, ref in zip((dQ, dK, dV), want):
+        assert not bool(torch.isnan(got).any())
+        assert torch.equal(got, ref)
+
+
 @pytest.mark.parametrize("causal", [True, False])
 @pytest.mark.parametrize("S,D", [(1024, 64), (512, 128)])
 def test_running_max_moves_every_tile(gpu, S, D, causal):

@@ -2,11 +2,11 @@
 
 The matrix-core attention kernels, RoPE and the model operators must not use
 scratch memory (register spills or run-time-indexed private arrays), and the hot
-attention kernels must keep the occupancy their tiling assumes.  The one
-documented exceptions are the separate D = 64 dK/dV launch behind
-mi_attn_bwd_dkdv (the default path runs the combined dK/dV + dQ launch), the
-causal D = 128 dK/dV launch with the rotating stores (4 bytes, outside its
-step loops) and the exact-fp32 VALU kernels at D = 128."""
+attention kernels must keep the occupancy their tiling assumes.  The
+documented exceptions are the causal D = 128 dK/dV launch with the rotating
+stores (one spilled register) and the exact-fp32 VALU kernels at D = 128.  At
+D = 64 every backward launch, the separate dK/dV and dQ ones included, runs the
+combined kernel, which has no scratch."""
 import os
 import re
 import shutil
@@ -19,13 +19,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "gpt_from_scratch_amd", "csrc")
 HIPCC = "/opt/rocm/bin/hipcc"
 SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "attn_valu.hip", "rope.hip", "model_ops.hip")
-# the separate D = 64 dK/dV launch (mi_attn_bwd_dkdv only): 8 / 28 bytes per lane;
 # the causal D = 128 dK/dV launch with the rotating stores (mi_attn_bwd_rope):
-# one 4-byte LDS offset, reloaded only in the steps outside the unrolled step
-# loops; the exact-fp32 / ragged-length VALU kernels at D = 128, where one
-# lane's rows alone fill the register file
-ALLOWED_SCRATCH = re.compile(r"attn_bwd_dkdv_kernel<mi::(BF16|F16), 64, (true|false), false>"
-                             r"|attn_bwd_dkdv_kernel<mi::(BF16|F16), 128, true, true>"
+# 8 bytes per lane, one register reloaded once per step; the exact-fp32 /
+# ragged-length VALU kernels at D = 128, where one lane's rows alone fill the
+# register file
+ALLOWED_SCRATCH = re.compile(r"attn_bwd_dkdv_kernel<mi::(BF16|F16), 128, true, true>"
                              r"|attn_(fwd|bwd_dq|bwd_dkdv)_valu_kernel<\d, 128, (true|false)>")
 
 
