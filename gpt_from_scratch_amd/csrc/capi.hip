@@ -741,6 +741,15 @@ static mi_status rms_fwd(mi_dtype x_dtype, mi_dtype w_dtype, int64_t rows, int64
   if (add)
     vec = vec && rms_vec_ok(hidden, {{res, res_row_stride}, {sum, sum_row_stride}},
                             {{res, elem_size(x_dtype)}, {sum, elem_size(x_dtype)}});
+  // 16-byte accesses: bf16 x, every row of every operand 8-element aligned
+  if (vec && x_dtype == MI_BF16 && hidden % 8 == 0) {
+    bool v16 = x_row_stride % 8 == 0 && y_row_stride % 8 == 0 && ((uintptr_t)x) % 16 == 0 &&
+               ((uintptr_t)y) % 16 == 0 && ((uintptr_t)weight) % 16 == 0;
+    if (add)
+      v16 = v16 && res_row_stride % 8 == 0 && sum_row_stride % 8 == 0 &&
+            ((uintptr_t)res) % 16 == 0 && ((uintptr_t)sum) % 16 == 0;
+    a.vec16 = v16;
+  }
   return launched(mi::launch_rmsnorm_fwd(x_dtype, w_dtype, a, vec, (hipStream_t)stream),
                   add ? "rmsnorm_add_fwd" : "rmsnorm_fwd");
 }

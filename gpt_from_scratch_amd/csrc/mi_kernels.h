@@ -109,6 +109,7 @@ struct RmsArgs {
   float* partial;  // [parts, hidden] fp32 workspace of the backward
   int parts;
   int dw_acc = 0;  // backward: dw += round_w(reduction) instead of dw = ...
+  int vec16 = 0;   // forward: 16-byte accesses (bf16 x, H % 8 == 0, 16-byte aligned rows)
   // Residual add fused in front (all null otherwise).  Forward: x is the
   // residual stream, res the branch output; sum = round_x(x + res) is written
   // and normalised.  Backward: x is that sum and dsum the gradient reaching

@@ -448,6 +448,49 @@ __device__ __forceinline__ void st4(void* row, int64_t i, const float (&v)[4]) {
   }
 }
 
+// 8 consecutive elements: one 16-byte access for 16-bit types, two for fp32.
+template <int DT, bool NT = false>
+__device__ __forceinline__ void ld8(const void* row, int64_t i, float (&v)[8]) {
+  if constexpr (DT == 0) {
+    float h[2][4];
+    ld4<0, NT>(row, i, h[0]);
+    ld4<0, NT>(row, i + 4, h[1]);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = h[e >> 2][e & 3];
+  } else {
+    const u32x4* p = (const u32x4*)((const uint16_t*)row + i);
+    const u32x4 q = NT ? __builtin_nontemporal_load(p) : *p;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      if constexpr (DT == 2) {
+        v[2 * e] = __uint_as_float(q[e] << 16);
+        v[2 * e + 1] = __uint_as_float(q[e] & 0xffff0000u);
+      } else {
+        v[2 * e] = f16_to_f32((uint16_t)(q[e] & 0xffffu));
+        v[2 * e + 1] = f16_to_f32((uint16_t)(q[e] >> 16));
+      }
+    }
+  }
+}
+
+template <int DT, bool NT = false>
+__device__ __forceinline__ void st8(void* row, int64_t i, const float (&v)[8]) {
+  if constexpr (DT == 0) {
+    float h[2][4];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) h[e >> 2][e & 3] = v[e];
+    st4<0, NT>(row, i, h[0]);
+    st4<0, NT>(row, i + 4, h[1]);
+  } else {
+    u32x4 q;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      q[e] = DT == 2 ? BF16::pack2(v[2 * e], v[2 * e + 1]) : F16::pack2(v[2 * e], v[2 * e + 1]);
+    if constexpr (NT) __builtin_nontemporal_store(q, (u32x4*)((uint16_t*)row + i));
+    else *(u32x4*)((uint16_t*)row + i) = q;
+  }
+}
+
 template <int DT>
 __device__ __forceinline__ const void* row_ptr(const void* base, int64_t row, int64_t stride) {
   return (const char*)base + row * stride * (DT == 0 ? 4 : 2);
@@ -474,6 +517,22 @@ __device__ __forceinline__ float wave_sum(float v) {
                                                   false);
   v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
   return sum_halves(v);
+}
+
+// The same sum as wave_sum over 64 lanes whose lane l held p0 (l even) or p1
+// (l odd) of lane l/2 here, computed by each half-wave (lanes 0-31 and 32-63
+// separately): lane i of the 64-lane tree maps to lane i/2 of a half, so each
+// step of the tree is the step that pairs the same groups here, and every add
+// sees the operands wave_sum's add sees (the same bits in every lane).
+__device__ __forceinline__ float half_wave_sum2(float p0, float p1) {
+  float v = p0 + p1;        // wave_sum's quad_perm [1,0,3,2]
+  v = dpp_add<0xB1>(v);     // its quad_perm [2,3,0,1]
+  v = dpp_add<0x4E>(v);     // its row_half_mirror
+  v = dpp_add<0x141>(v);    // its row_mirror
+  v = dpp_add<0x140>(v);    // its permlane16 swap
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);  // its permlane32 swap
 }
 
 // y dtype: the promotion of x's dtype and w's dtype (w is x's dtype or fp32)
@@ -548,6 +607,88 @@ __global__ __launch_bounds__(256) void rmsnorm_fwd_vec_kernel(RmsArgs a) {
     }
   }
   if (lane == 0) a.rstd[row] = r;
+}
+
+// Forward with 16-byte accesses (bf16 x, H % 8 == 0, 16-byte aligned rows):
+// each half-wave takes RPH rows, C chunks of 8 elements per lane and row, and
+// issues every load of its rows before the first reduction.  At config 5's
+// [8192, 768] from HBM: 5.8 us against 7.7 for rmsnorm_fwd_vec_kernel (and 6.7
+// for torch's copy of the same bytes), with the residual add 9.0 against 10.2;
+// two rows per half-wave measured 7.3 and 10.5.  Rows past the end
+// are computed on zeros and not stored (the half-wave reduction needs every
+// lane of the half).  Lane l's 8 elements of chunk c are the 4 + 4 that lanes
+// 2l and 2l + 1 of rmsnorm_fwd_vec_kernel hold in its chunk c; summed as two
+// partials in that kernel's order and reduced by half_wave_sum2, the sum of
+// squares, and so every output, is bitwise that kernel's.
+constexpr int RMS_V16_RPH = 1;
+template <int DT, int WDT, int C, bool ADD>
+__global__ __launch_bounds__(256) void rmsnorm_fwd_v16_kernel(RmsArgs a) {
+  constexpr int YDT = RmsTypes<DT, WDT>::YDT;
+  constexpr int RPH = RMS_V16_RPH;
+  const int lane = threadIdx.x & 63, hl = lane & 31;
+  const int64_t row0 = ((int64_t)blockIdx.x * 8 + (threadIdx.x >> 5)) * RPH;
+  const int nq = (int)(a.hidden / 8);
+  float w[C][8], v[RPH][C][8], rv[ADD ? RPH : 1][ADD ? C : 1][8];
+#pragma unroll
+  for (int r = 0; r < RPH; ++r) {
+    const int64_t row = row0 + r;
+    const bool ok = row < a.rows;
+    const void* xr = row_ptr<DT>(a.x, ok ? row : 0, a.x_stride);
+    const void* rr = ADD ? row_ptr<DT>(a.res, ok ? row : 0, a.res_stride) : nullptr;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int q = c * 32 + hl;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[r][c][e] = 0.f;
+      if (ok && q < nq) {
+        ld8<DT, kRmsNtLoad>(xr, 8 * q, v[r][c]);
+        if constexpr (ADD) ld8<DT, kRmsNtLoad>(rr, 8 * q, rv[r][c]);
+      }
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < C; ++c) {
+    const int q = c * 32 + hl;
+    if (q < nq) ld8<WDT>(a.w, 8 * q, w[c]);
+  }
+#pragma unroll
+  for (int r = 0; r < RPH; ++r) {
+    const int64_t row = row0 + r;
+    const bool ok = row < a.rows;
+    float ss0 = 0.f, ss1 = 0.f;
+    void* sr = ADD ? row_ptr<DT>(a.sum, ok ? row : 0, a.sum_stride) : nullptr;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int q = c * 32 + hl;
+      if (q < nq) {
+        if constexpr (ADD) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) v[r][c][e] = round_to<DT>(v[r][c][e] + rv[r][c][e]);
+          if (ok) st8<DT, kRmsNtStore>(sr, 8 * q, v[r][c]);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          ss0 = __builtin_fmaf(v[r][c][e], v[r][c][e], ss0);
+          ss1 = __builtin_fmaf(v[r][c][4 + e], v[r][c][4 + e], ss1);
+        }
+      }
+    }
+    const float ss = half_wave_sum2(ss0, ss1);
+    const float rs = __builtin_amdgcn_rsqf(ss / (float)a.hidden + a.eps);
+    if (!ok) continue;
+    void* yr = row_ptr<YDT>(a.y, row, a.y_stride);
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      const int q = c * 32 + hl;
+      if (q < nq) {
+        float y[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = round_to<DT>(v[r][c][e] * rs) * w[c][e];
+        st8<YDT, kRmsNtStore>(yr, 8 * q, y);
+      }
+    }
+    if (hl == 0) a.rstd[row] = rs;
+  }
 }
 
 template <int DT, int WDT, bool ADD>
@@ -777,6 +918,25 @@ template <int DT, int WDT, bool ADD>
 hipError_t launch_rms_dt(bool fwd, const RmsArgs& a, bool vec, hipStream_t st) {
   const int64_t nq = a.hidden / 4;
   if (a.hidden > (fwd ? RMS_VEC_FWD_MAX : RMS_VEC_BWD_MAX)) vec = false;
+  // bf16 only: for fp16 the backend fuses some of a row's x * r products with
+  // their conversion into one v_fma_mixlo_f16 (a single rounding of the exact
+  // product), and which ones depends on the kernel's code, so the two kernels
+  // could round a rare element differently; bf16 has no such fusion
+  if constexpr (DT == 2) {
+    if (fwd && vec && a.vec16) {
+      const int64_t n8 = a.hidden / 8;
+      const dim3 grid((unsigned)((a.rows + 8 * RMS_V16_RPH - 1) / (8 * RMS_V16_RPH)));
+      if (n8 <= 32) hipLaunchKernelGGL((rmsnorm_fwd_v16_kernel<DT, WDT, 1, ADD>), grid, dim3(256), 0, st, a);
+      else if (n8 <= 64) hipLaunchKernelGGL((rmsnorm_fwd_v16_kernel<DT, WDT, 2, ADD>), grid, dim3(256), 0, st, a);
+      else if (n8 <= 96) hipLaunchKernelGGL((rmsnorm_fwd_v16_kernel<DT, WDT, 3, ADD>), grid, dim3(256), 0, st, a);
+      else if (n8 <= 128) hipLaunchKernelGGL((rmsnorm_fwd_v16_kernel<DT, WDT, 4, ADD>), grid, dim3(256), 0, st, a);
+      else if (n8 <= 192) hipLaunchKernelGGL((rmsnorm_fwd_v16_kernel<DT, WDT, 6, ADD>), grid, dim3(256), 0, st, a);
+      else if (n8 <= 256) hipLaunchKernelGGL((rmsnorm_fwd_v16_kernel<DT, WDT, 8, ADD>), grid, dim3(256), 0, st, a);
+      else if (n8 <= 384) hipLaunchKernelGGL((rmsnorm_fwd_v16_kernel<DT, WDT, 12, ADD>), grid, dim3(256), 0, st, a);
+      else hipLaunchKernelGGL((rmsnorm_fwd_v16_kernel<DT, WDT, 16, ADD>), grid, dim3(256), 0, st, a);
+      return hipGetLastError();
+    }
+  }
   if (vec) {
     // smallest instantiated chunk count covering the row
     if (nq <= 64) launch_rms_vec<DT, WDT, 1, ADD>(fwd, a, st);
@@ -880,30 +1040,6 @@ __device__ __forceinline__ void swiglu_bwd_elem(float g, float u, float dh, floa
   dg = ds * (sig * (1.f + g * (1.f - sig)));
 }
 
-// 8 elements of a 16-bit row at i (16-byte aligned) as floats; fp32 rows use
-// two 16-byte loads.
-template <int DT>
-__device__ __forceinline__ void ld8(const void* row, int64_t i, float (&v)[8]) {
-  float a[4], b[4];
-  ld4<DT>(row, i, a);
-  ld4<DT>(row, i + 4, b);
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    v[e] = a[e];
-    v[4 + e] = b[e];
-  }
-}
-template <int DT>
-__device__ __forceinline__ void st8(void* row, int64_t i, const float (&v)[8]) {
-  float a[4], b[4];
-#pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    a[e] = v[e];
-    b[e] = v[4 + e];
-  }
-  st4<DT>(row, i, a);
-  st4<DT>(row, i + 4, b);
-}
 
 // Grid: x covers the row's chunks (SW_T lanes per workgroup), y the rows with
 // a stride loop; no per-element division.
