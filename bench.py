@@ -545,6 +545,27 @@ def summarize(root):
             b2b = f"{span[k] / span_n[k] / 1e3:.3f}" if span_n[k] else "-"
             print(f"| {k} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} | {min(d) / 1e3:.3f} "
                   f"| {max(d) / 1e3:.3f} | {b2b} | {scratch[k]} |")
+        # each pass separately: maximal runs of one kernel and grid at a fixed
+        # stride in the dispatch order (1: back-to-back launches; 3: the fwd,
+        # delta, bwd steps of a timed pass), at least 5 dispatches
+        runs, open_run = [], {}
+        for idx, (start, end, k, _) in enumerate(disp):
+            r = open_run.get(k)
+            gap = idx - r["last"] if r is not None else None
+            if r is not None and gap <= 3 and (r["gap"] is None or gap == r["gap"]):
+                r["d"].append(end - start)
+                r["last"], r["gap"] = idx, gap
+            else:
+                r = {"k": k, "last": idx, "gap": None, "d": [end - start]}
+                open_run[k] = r
+                runs.append(r)
+        print("\n| pass (in trace order) | kernel [grid threads] | dispatches | avg µs | min µs | max µs |")
+        print("|---|---|---|---|---|---|")
+        for i, r in enumerate(runs):
+            d = r["d"]
+            if len(d) >= 5:
+                print(f"| {i} | {r['k']} | {len(d)} | {sum(d) / len(d) / 1e3:.3f} "
+                      f"| {min(d) / 1e3:.3f} | {max(d) / 1e3:.3f} |")
     elif stats:
         for path in stats:
             print("| kernel | calls | avg µs | min µs | max µs |")
