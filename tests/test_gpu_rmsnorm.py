@@ -286,6 +286,48 @@ def test_add_norm_in_place_and_model_stack(gpu):
         assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("xd,wd", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                   (torch.float16, torch.float16)])
+@pytest.mark.parametrize("rows,H", [(37, 768), (45, 1024), (9, 2048), (13, 64)])
+def test_forward_paths_agree_bit_for_bit(gpu, xd, wd, rows, H):
+    """The forward's 16-byte path (bf16 rows 8-element aligned: half a wave per
+    row) and its 8-byte path (rows only 4-element aligned: a wave per row) sum
+    the squares in the same order, so y, rstd and the fused add's sum agree bit
+    for bit; fp16 takes the 8-byte path at both strides.  Rows are laid out at
+    strides H (16-byte aligned), H + 8 (aligned, padded) and H + 4 (4-element
+    aligned only)."""
+    import ctypes
+    from gpt_from_scratch_amd import _lib
+    lib = _lib.lib()
+    x = seeded((rows, H), 700 + H, std=1.5, dtype=xd).to(gpu)
+    r = seeded((rows, H), 701 + H, std=0.7, dtype=xd).to(gpu)
+    w = (1.0 + 0.1 * seeded((H,), 702 + H, dtype=torch.float32)).to(wd).to(gpu)
+    yd = torch.float32 if wd == torch.float32 else xd
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    dx_, dw_ = _lib.dtype_code(x), _lib.dtype_code(w)
+    outs = {}
+    for pad in (0, 8, 4):
+        ld = H + pad
+        xb, rb = (torch.zeros(rows, ld, dtype=xd, device=gpu) for _ in range(2))
+        xb[:, :H] = x
+        rb[:, :H] = r
+        yb, y2 = (torch.zeros(rows, ld, dtype=yd, device=gpu) for _ in range(2))
+        sb = torch.zeros(rows, ld, dtype=xd, device=gpu)
+        rs, rs2 = (torch.empty(rows, device=gpu) for _ in range(2))
+        assert lib.mi_rmsnorm_fwd(dx_, dw_, rows, H, ctypes.c_float(EPS), P(xb), ld, P(w),
+                                  P(yb), ld, P(rs), sp) == 0
+        assert lib.mi_rmsnorm_add_fwd(dx_, dw_, rows, H, ctypes.c_float(EPS), P(xb), ld, P(rb),
+                                      ld, P(w), P(sb), ld, P(y2), ld, P(rs2), sp) == 0
+        torch.cuda.synchronize()
+        outs[pad] = (yb[:, :H].clone(), rs.clone(), sb[:, :H].clone(), y2[:, :H].clone(),
+                     rs2.clone())
+    for pad in (8, 4):
+        for name, a, b in zip(("y", "rstd", "sum", "add y", "add rstd"), outs[0], outs[pad]):
+            assert torch.equal(a, b), (pad, name, float((a.float() - b.float()).abs().max()))
+    _check_forward(outs[0][0], x, w, EPS)
+
+
 @pytest.mark.parametrize("xd,wd", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
                                    (torch.float32, torch.float32), (torch.bfloat16, torch.float32)])
 @pytest.mark.parametrize("rows,H", [(37, 768), (21, 7)])
