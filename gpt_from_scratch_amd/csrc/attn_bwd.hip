@@ -392,7 +392,8 @@ __device__ __forceinline__ int first_row(const BwdItem& it) {
 }
 
 // SKIP0: leave res.r[0] unloaded (the D = 128 dK/dV kind keeps K in LDS).
-template <int D, bool SKIP0 = false>
+// DP < D: rows of DP columns; the registers of columns past DP are zeros.
+template <int D, bool SKIP0 = false, int DP = D>
 __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& it,
                                               Resident<D>& res) {
   const int lane = threadIdx.x & 63;
@@ -404,14 +405,19 @@ __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& 
   const int w0 = it.tile * BwdCfg<D>::OWN + 32 * wave;  // first row of this wave (SGPR)
   if (w0 < a.S) {
     // wave base in the descriptor, lane offset (row l%32, 8 columns) in one VGPR
-    const auto r0 = tile_rsrc(head_ptr(t0, b, h) + (int64_t)w0 * t0.ss, rows_extent(32, t0.ss, D));
-    const auto r1 = tile_rsrc(head_ptr(t1, b, h) + (int64_t)w0 * t1.ss, rows_extent(32, t1.ss, D));
+    const auto r0 = tile_rsrc(head_ptr(t0, b, h) + (int64_t)w0 * t0.ss, rows_extent(32, t0.ss, DP));
+    const auto r1 = tile_rsrc(head_ptr(t1, b, h) + (int64_t)w0 * t1.ss, rows_extent(32, t1.ss, DP));
     const uint32_t o0 = (uint32_t)(((lane & 31) * t0.ss + 8 * (lane >> 5)) * 2);
     const uint32_t o1 = (uint32_t)(((lane & 31) * t1.ss + 8 * (lane >> 5)) * 2);
     // kind 0 keeps V negated (sign bits of both 16-bit halves flipped)
     const uint32_t neg = it.kind ? 0u : 0x80008000u;
 #pragma unroll
     for (int ks = 0; ks < D / 16; ++ks) {
+      if (ks >= DP / 16) {
+        res.r[0][ks] = u32x4{0, 0, 0, 0};
+        res.r[1][ks] = u32x4{0, 0, 0, 0};
+        continue;
+      }
       if (!SKIP0) res.r[0][ks] = __builtin_amdgcn_raw_buffer_load_b128(r0, o0 + 32 * ks, 0, 0);
       res.r[1][ks] = __builtin_amdgcn_raw_buffer_load_b128(r1, o1 + 32 * ks, 0, 0) ^ neg;
     }
@@ -433,7 +439,9 @@ __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& 
   }
 }
 
-template <int D, bool SW16 = false>
+// DP < D: chunks past DP (padding) take the out-of-range offset and stage as
+// zeros.
+template <int D, bool SW16 = false, int DP = D>
 __device__ __forceinline__ StageSrc<D> stage_src(const AttnArgs& a, const BwdItem& it) {
   using C = BwdCfg<D>;
   const int lane = threadIdx.x & 63;
@@ -453,9 +461,10 @@ __device__ __forceinline__ StageSrc<D> stage_src(const AttnArgs& a, const BwdIte
 #pragma unroll
   for (int m = 0; m < C::SPW; ++m) {
     const int r = (wave + 4 * m) * C::RPS + lane / C::CPR;
-    const int col = ((lane % C::CPR) ^ bwd_swz<D, SW16>(r)) << 3;
-    s.off0[m] = (uint32_t)((r * t0.ss + col) * 2);
-    s.off1[m] = (uint32_t)((r * t1.ss + col) * 2);
+    const int ch = (lane % C::CPR) ^ bwd_swz<D, SW16>(r);
+    const bool pad = DP < D && ch >= DP / 8;
+    s.off0[m] = pad ? kOobOffset : (uint32_t)((r * t0.ss + (ch << 3)) * 2);
+    s.off1[m] = pad ? kOobOffset : (uint32_t)((r * t1.ss + (ch << 3)) * 2);
   }
   s.lse = a.lse2 + (int64_t)it.bh * a.S;
   s.delta = a.delta + (int64_t)it.bh * a.S;
@@ -464,14 +473,14 @@ __device__ __forceinline__ StageSrc<D> stage_src(const AttnArgs& a, const BwdIte
 
 // Streamed tile starting at row `row0` straight into LDS buffer `dst`;
 // completion is tracked by vmcnt and the barrier that ends the step.
-template <int D>
+template <int D, int DP = D>
 __device__ __forceinline__ void dma_stage(const StageSrc<D>& s, int kind, int row0,
                                           const BwdBuf& dst) {
   using C = BwdCfg<D>;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const auto r0 = tile_rsrc(s.p0 + (int64_t)row0 * s.ss0, rows_extent(C::TILE, s.ss0, D));
-  const auto r1 = tile_rsrc(s.p1 + (int64_t)row0 * s.ss1, rows_extent(C::TILE, s.ss1, D));
+  const auto r0 = tile_rsrc(s.p0 + (int64_t)row0 * s.ss0, rows_extent(C::TILE, s.ss0, DP));
+  const auto r1 = tile_rsrc(s.p1 + (int64_t)row0 * s.ss1, rows_extent(C::TILE, s.ss1, DP));
 #pragma unroll
   for (int m = 0; m < C::SPW; ++m) {
     buffer_load_lds16(r0, s.off0[m], dst.t0 + (wave + 4 * m) * 512);
@@ -496,10 +505,12 @@ __device__ __forceinline__ void dma_stage(const StageSrc<D>& s, int kind, int ro
 // accumulators together need ~290 VGPRs, and holding all of them spilled
 // ~390 bytes per lane.  The region then stages the wave's dK and dV stores.
 // ---------------------------------------------------------------------------
-template <typename E, int D, bool CAUSAL, bool ROPE>
+template <typename E, int D, bool CAUSAL, bool ROPE, int DP>
 __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
                                           const BwdBuf (&bufs)[2]) {
   using C = BwdCfg<D>;
+  constexpr int KSP = DP / 16;         // k-steps over the valid columns
+  constexpr int DBP = (DP + 31) / 32;  // accumulator blocks holding valid columns
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
@@ -521,7 +532,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
 
   const int q_begin = first_row<D, CAUSAL>(it);
   const int nq = (S - q_begin) / C::TILE;
-  const StageSrc<D> src = stage_src<D>(a, it);
+  const StageSrc<D> src = stage_src<D, false, DP>(a, it);
 
   f32x16 dk[C::DB], dv[C::DB];
 #pragma unroll
@@ -533,7 +544,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
 
   // First tile's loads before the resident rows: one memory round trip for
   // both (the V negation waits for its rows, not for the tile).
-  dma_stage<D>(src, 0, q_begin, bufs[0]);
+  dma_stage<D, DP>(src, 0, q_begin, bufs[0]);
   if constexpr (K_IN_LDS) {
     // the wave's 32 K rows: 8 one-KB slices of 4 rows, lane i writing chunk
     // position i%16 of row 4m + i/16, i.e. fetching chunk (i%16) ^ swz(row)
@@ -549,7 +560,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     }
   }
   Resident<D> res;
-  load_resident<D, K_IN_LDS>(a, it, res);
+  load_resident<D, K_IN_LDS, DP>(a, it, res);
   const u32x4(&kf)[C::KS] = res.r[0];
   const u32x4(&vn)[C::KS] = res.r[1];  // -V
   __syncthreads();
@@ -565,7 +576,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     constexpr int P = decltype(parity)::value;
     const int q0 = q_begin + j * C::TILE;
     // (at D = 128 the last step is not peeled: a uniform branch skips its load)
-    if (!LAST && (D == 64 || j + 1 < nq)) dma_stage<D>(src, 0, q0 + C::TILE, bufs[P ^ 1]);
+    if (!LAST && (D == 64 || j + 1 < nq)) dma_stage<D, DP>(src, 0, q0 + C::TILE, bufs[P ^ 1]);
 
     if (wave_valid && (!MASKED || q0 + C::TILE - 1 >= kw)) {
       const uint16_t* Qs = bufs[P].t0;
@@ -586,7 +597,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
           for (int i = 0; i < 4; ++i) dp[4 * jj + i] = d4[i];
         }
 #pragma unroll
-        for (int ks = 0; ks < C::KS; ++ks) {
+        for (int ks = 0; ks < KSP; ++ks) {
           const u32x4 qa = *(const u32x4*)(&Qs[32 * qb * D + lo.row(ks)]);
           if constexpr (K_IN_LDS)
             s = E::mfma(qa, *(const u32x4*)(&kw_lds[lo.row(ks)]), s);
@@ -594,7 +605,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
             s = E::mfma(qa, kf[ks], s);
         }
 #pragma unroll
-        for (int ks = 0; ks < C::KS; ++ks) {
+        for (int ks = 0; ks < KSP; ++ks) {
           const u32x4 da = *(const u32x4*)(&dOs[32 * qb * D + lo.row(ks)]);
           dp = E::mfma(da, vn[ks], dp);
         }
@@ -627,7 +638,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-          for (int db = 0; db < C::DB; ++db) {
+          for (int db = 0; db < DBP; ++db) {
             const int off = (32 * qb + 16 * hh) * D;
             dv[db] = E::mfma(tr_operand2(&dOs[off + lo.tr(db)], &dOs[off + lo.tr_hi(db)]),
                              pb[qb][hh], dv[db]);
@@ -681,11 +692,11 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     // stages its rows (dK, then dV) through tile buffer w.
     uint16_t* stage = wave_stage_buf(bufs, wave);
     // dV first: its accumulators are dead before dK's rotation needs registers
-    store_block_rows<E, D>(dv, 1.f, stage, dv_rows, a.dv.ss);
+    store_block_rows<E, D, DP>(dv, 1.f, stage, dv_rows, a.dv.ss);
     if (ROPE && a.rope.cos)
       store_block_rows_rope<E, D>(dk, a.scale, stage, dk_rows, a.dk.ss, a.rope, kw);
     else
-      store_block_rows<E, D>(dk, a.scale, stage, dk_rows, a.dk.ss);
+      store_block_rows<E, D, DP>(dk, a.scale, stage, dk_rows, a.dk.ss);
   } else {
     // D = 128: the wave's K region (32 x D, its own) is idle after the last
     // step.  (Written straight from the accumulators instead, 8 bytes per lane
@@ -705,10 +716,12 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
 // per-lane scalars and dS^T feeds dQ^T = K^T dS^T directly (K^T read
 // transposed from the K tile).
 // ---------------------------------------------------------------------------
-template <typename E, int D, bool CAUSAL, bool ROPE>
+template <typename E, int D, bool CAUSAL, bool ROPE, int DP>
 __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
                                         const BwdBuf (&bufs)[2]) {
   using C = BwdCfg<D>;
+  constexpr int KSP = DP / 16;         // k-steps over the valid columns
+  constexpr int DBP = (DP + 31) / 32;  // accumulator blocks holding valid columns
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
@@ -724,7 +737,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
 
   const int kv_end = CAUSAL ? min(q0 + C::OWN, S) : S;
   const int nkv = kv_end / C::TILE;
-  const StageSrc<D> src = stage_src<D, D == 128>(a, it);
+  const StageSrc<D> src = stage_src<D, D == 128, DP>(a, it);
 
   f32x16 acc[C::DB];
 #pragma unroll
@@ -732,9 +745,9 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   const float c = a.scale_log2;
 
   // First tile's loads before the resident rows (one round trip for both).
-  dma_stage<D>(src, 1, 0, bufs[0]);
+  dma_stage<D, DP>(src, 1, 0, bufs[0]);
   Resident<D> res;
-  load_resident<D>(a, it, res);
+  load_resident<D, false, DP>(a, it, res);
   const u32x4(&qf)[C::KS] = res.r[0];
   const u32x4(&df)[C::KS] = res.r[1];
   const float lse2 = res.lse2;
@@ -755,7 +768,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
     constexpr bool LAST = decltype(last_tag)::value;
     constexpr int P = decltype(parity)::value;
     const int kv0 = j * C::TILE;
-    if (!LAST) dma_stage<D>(src, 1, kv0 + C::TILE, bufs[P ^ 1]);
+    if (!LAST) dma_stage<D, DP>(src, 1, kv0 + C::TILE, bufs[P ^ 1]);
 
     if (wave_valid && (!MASKED || kv0 <= qw + 31)) {
       const uint16_t* Ks = bufs[P].t0;
@@ -769,12 +782,12 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
         if (!live[kb]) continue;
         f32x16 s = f32x16{}, dp = ndl;
 #pragma unroll
-        for (int ks = 0; ks < C::KS; ++ks) {
+        for (int ks = 0; ks < KSP; ++ks) {
           const u32x4 ka = *(const u32x4*)(&Ks[32 * kb * D + lo.row(ks)]);
           s = E::mfma(ka, qf[ks], s);
         }
 #pragma unroll
-        for (int ks = 0; ks < C::KS; ++ks) {
+        for (int ks = 0; ks < KSP; ++ks) {
           const u32x4 va = *(const u32x4*)(&Vs[32 * kb * D + lo.row(ks)]);
           dp = E::mfma(va, df[ks], dp);
         }
@@ -797,7 +810,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
 #pragma unroll
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
-          for (int db = 0; db < C::DB; ++db) {
+          for (int db = 0; db < DBP; ++db) {
             const int off = (32 * kb + 16 * hh) * D;
             acc[db] = E::mfma(tr_operand2(&Ks[off + lo.tr(db)], &Ks[off + lo.tr_hi(db)]),
                               sb[kb][hh], acc[db]);
@@ -841,13 +854,13 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
     store_block_rows_rope<E, D>(acc, a.scale, wave_stage_buf(bufs, wave), dq_rows, a.dq.ss,
                                 a.rope, qw);
   else
-    store_block_rows<E, D>(acc, a.scale, wave_stage_buf(bufs, wave), dq_rows, a.dq.ss);
+    store_block_rows<E, D, DP>(acc, a.scale, wave_stage_buf(bufs, wave), dq_rows, a.dq.ss);
 }
 
 // One item per workgroup.  One LDS array per buffer and tensor, so that the
 // compiler can see that a direct load into one buffer never aliases the
 // reads of the other.
-template <typename E, int D, bool CAUSAL, bool ROPE>
+template <typename E, int D, bool CAUSAL, bool ROPE, int DP = D>
 __device__ __forceinline__ void run_item(const AttnArgs& a, const BwdItem it) {
   using C = BwdCfg<D>;
   __shared__ __attribute__((aligned(16))) uint16_t A0[C::ELEMS];
@@ -858,9 +871,9 @@ __device__ __forceinline__ void run_item(const AttnArgs& a, const BwdItem it) {
   __shared__ __attribute__((aligned(16))) float SB[2 * C::TILE];
   const BwdBuf bufs[2] = {{A0, A1, SA}, {B0, B1, SB}};
   if (it.kind)
-    dq_item<E, D, CAUSAL, ROPE>(a, it, bufs);
+    dq_item<E, D, CAUSAL, ROPE, DP>(a, it, bufs);
   else
-    dkdv_item<E, D, CAUSAL, ROPE>(a, it, bufs);
+    dkdv_item<E, D, CAUSAL, ROPE, DP>(a, it, bufs);
 }
 
 // ROPE (every kernel below): the kernel carries the rotating stores, and dQ
@@ -888,14 +901,19 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a, int n_q
 // items of that kind alone (rank r: tile r of it, heaviest first): the D = 64
 // separate launches use this kernel, whose compiled item bodies have no
 // scratch (standalone instantiations of the dK/dV item spilled 8-28 bytes).
-template <typename E, int D, bool CAUSAL, bool ROPE>
+// DP: head columns of the tensors.  Head dims 16 and 32 run in the D = 64
+// layout: the padding chunks of the staged tiles and resident rows load as
+// zeros, the products over the head dim stop at DP, accumulator blocks past
+// DP are not formed and only DP columns are stored (no rotating stores).
+template <typename E, int D, bool CAUSAL, bool ROPE, int DP = D>
 __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(AttnArgs a, int n_tiles,
                                                           int only_kind) {
+  static_assert(DP == D || (D == 64 && !ROPE && (DP == 16 || DP == 32)), "head dim");
   const int BH = a.B * a.H;
   const int rank = blockIdx.x / BH;
   const int kind = only_kind < 0 ? rank & 1 : only_kind;
   const int r = only_kind < 0 ? rank >> 1 : rank;
-  run_item<E, D, CAUSAL, ROPE>(
+  run_item<E, D, CAUSAL, ROPE, DP>(
       a, BwdItem{kind, kind ? n_tiles - 1 - r : r, (int)(blockIdx.x % BH)});
 }
 
@@ -928,19 +946,29 @@ hipError_t launch_dq_dr(const AttnArgs& a, hipStream_t st) {
 // (One instantiation with the rotation applied at run time: compiled without
 // the rotating stores, the causal kernel's registers spilled 12 bytes.)
 // only_kind: -1 both kinds interleaved, else that kind alone.
-template <typename E, int D, bool CAUSAL>
+// Head dims 16 and 32 (DP < D) have no rotating stores: the host runs their
+// inverse RoPE as a separate pass.
+template <typename E, int D, bool CAUSAL, int DP = D>
 hipError_t launch_both_dc(const AttnArgs& a, int only_kind, hipStream_t st) {
   const int BH = a.B * a.H;
   const int n = (a.S + BwdCfg<D>::OWN - 1) / BwdCfg<D>::OWN;
-  hipLaunchKernelGGL((attn_bwd_kernel<E, D, CAUSAL, true>), dim3((only_kind < 0 ? 2 : 1) * n * BH),
-                     dim3(256), 0, st, a, n, only_kind);
+  hipLaunchKernelGGL((attn_bwd_kernel<E, D, CAUSAL, DP == D, DP>),
+                     dim3((only_kind < 0 ? 2 : 1) * n * BH), dim3(256), 0, st, a, n, only_kind);
   return hipGetLastError();
 }
 
-template <typename E, int D>
+template <typename E, int D, int DP = D>
 hipError_t launch_both_d(const AttnArgs& a, hipStream_t st, int only_kind = -1) {
-  return a.causal ? launch_both_dc<E, D, true>(a, only_kind, st)
-                  : launch_both_dc<E, D, false>(a, only_kind, st);
+  return a.causal ? launch_both_dc<E, D, true, DP>(a, only_kind, st)
+                  : launch_both_dc<E, D, false, DP>(a, only_kind, st);
+}
+
+// Head dims 16 and 32: the combined D = 64 kernel with DP columns, restricted
+// to one kind (0 or 1) or both (-1).
+template <typename E>
+hipError_t launch_small_d(const AttnArgs& a, hipStream_t st, int only_kind) {
+  if (a.D == 16) return launch_both_d<E, 64, 16>(a, st, only_kind);
+  return launch_both_d<E, 64, 32>(a, st, only_kind);
 }
 
 // The separate launches: at D = 64 the combined kernel restricted to one kind
@@ -968,12 +996,14 @@ hipError_t launch_dq_d(const AttnArgs& a, hipStream_t st) {
 
 template <typename E>
 hipError_t launch_dkdv_e(const AttnArgs& a, hipStream_t st) {
+  if (a.D < 64) return launch_small_d<E>(a, st, 0);
   if (a.D == 64) return launch_dkdv_d<E, 64>(a, st);
   return launch_dkdv_d<E, 128>(a, st);
 }
 
 template <typename E>
 hipError_t launch_dq_e(const AttnArgs& a, hipStream_t st) {
+  if (a.D < 64) return launch_small_d<E>(a, st, 1);
   if (a.D == 64) return launch_dq_d<E, 64>(a, st);
   return launch_dq_d<E, 128>(a, st);
 }
@@ -983,6 +1013,7 @@ hipError_t launch_dq_e(const AttnArgs& a, hipStream_t st) {
 // (when the dK/dV kind still held K in registers and spilled).
 template <typename E>
 hipError_t launch_both_e(const AttnArgs& a, hipStream_t st) {
+  if (a.D < 64) return launch_small_d<E>(a, st, -1);
   if (a.D == 64) return launch_both_d<E, 64>(a, st);
   hipError_t e = launch_dkdv_d<E, 128>(a, st);
   if (e != hipSuccess) return e;

@@ -103,9 +103,16 @@ __device__ __forceinline__ constexpr float kProbLimit() {
   return std::is_same<E, BF16>::value ? 0x1p64f : 0x1p14f;
 }
 
-template <typename E, int D, bool CAUSAL>
+// DP: head columns of the tensors.  Head dims 16 and 32 run in the D = 64
+// layout: the padding chunks of the staged tiles load as zeros, the K Q^T
+// products stop at DP, O^T blocks past DP are not accumulated and only DP
+// columns are stored.
+template <typename E, int D, bool CAUSAL, int DP = D>
 __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_kernel(AttnArgs a, int n_qtiles, int n_cu) {
   using C = FwdCfg<D>;
+  static_assert(DP == D || (D == 64 && (DP == 16 || DP == 32)), "head dim");
+  constexpr int KSP = DP / 16;         // k-steps of K Q^T over the valid columns
+  constexpr int DBP = (DP + 31) / 32;  // O^T blocks holding valid columns
   // One array per buffer, so that the compiler can see that a direct load
   // into one buffer never aliases the reads of another.
   __shared__ __attribute__((aligned(16))) uint16_t K0[C::TILE];
@@ -147,8 +154,9 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
   u32x4 qf[C::KS];
 #pragma unroll
   for (int ks = 0; ks < C::KS; ++ks)
-    qf[ks] = wave_valid ? *(const u32x4*)(qp + (int64_t)qrow * a.q.ss + 16 * ks + 8 * g)
-                        : u32x4{0, 0, 0, 0};
+    qf[ks] = (wave_valid && ks < KSP)
+                 ? *(const u32x4*)(qp + (int64_t)qrow * a.q.ss + 16 * ks + 8 * g)
+                 : u32x4{0, 0, 0, 0};
 
   const int kv_end = CAUSAL ? min(q0 + C::BQ, S) : S;
   const int nkv = kv_end / C::BKV;
@@ -159,18 +167,20 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
   // Lane i of slice s writes the 16 bytes at row s*RPS + i/CPR, chunk position
   // i%CPR, so it fetches chunk (i%CPR) ^ swz(row) of that row.  One buffer
   // descriptor per tile, fixed per-lane byte offsets; completion is tracked by
-  // vmcnt and the barrier that ends each step.
+  // vmcnt and the barrier that ends each step.  Chunks past DP (padding) take
+  // the out-of-range offset and stage as zeros.
   uint32_t kdo[C::SPW], vdo[C::SPW];
 #pragma unroll
   for (int m = 0; m < C::SPW; ++m) {
     const int r = (wave + 4 * m) * C::RPS + lane / C::CPR;
     const int pos = lane % C::CPR;
-    kdo[m] = (uint32_t)((r * a.k.ss + ((pos ^ swz_k<D>(r)) << 3)) * 2);
-    vdo[m] = (uint32_t)((r * a.v.ss + ((pos ^ swz_v<D>(r)) << 3)) * 2);
+    const int kc = pos ^ swz_k<D>(r), vc = pos ^ swz_v<D>(r);
+    kdo[m] = (DP < D && kc >= DP / 8) ? kOobOffset : (uint32_t)((r * a.k.ss + (kc << 3)) * 2);
+    vdo[m] = (DP < D && vc >= DP / 8) ? kOobOffset : (uint32_t)((r * a.v.ss + (vc << 3)) * 2);
   }
   auto dma = [&](const uint16_t* base, int64_t ss, const uint32_t(&off)[C::SPW], int t,
                  uint16_t* tile) __attribute__((always_inline)) {
-    const auto rs = tile_rsrc(base + (int64_t)t * C::BKV * ss, rows_extent(C::BKV, ss, D));
+    const auto rs = tile_rsrc(base + (int64_t)t * C::BKV * ss, rows_extent(C::BKV, ss, DP));
 #pragma unroll
     for (int m = 0; m < C::SPW; ++m)
       buffer_load_lds16(rs, off[m], tile + (wave + 4 * m) * 512);
@@ -202,7 +212,7 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
   // S^T for one key tile (two 32-key blocks).
   auto qk = [&](const uint16_t* kt, f32x16(&s)[2]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int ks = 0; ks < C::KS; ++ks) {
+    for (int ks = 0; ks < KSP; ++ks) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         const u32x4 kf = *(const u32x4*)(&kt[32 * kb * D + kro[ks]]);
@@ -269,7 +279,7 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
 #pragma unroll
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
-        for (int db = 0; db < C::DB; ++db)
+        for (int db = 0; db < DBP; ++db)
           acc[db] = E::mfma(tr_operand(&vt[(32 * kb + 16 * hh) * D + vro[db]], D), pb[kb][hh],
                             acc[db]);
   };
@@ -342,7 +352,7 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
   // Every buffer is idle after the last step's barrier: wave w stages its O
   // rows through buffer w.
   uint16_t* stage = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? V0 : V1;
-  store_block_rows<E, D>(acc, 1.f / l_tot, stage, op + (int64_t)qw * a.o.ss, a.o.ss);
+  store_block_rows<E, D, DP>(acc, 1.f / l_tot, stage, op + (int64_t)qw * a.o.ss, a.o.ss);
   if (g == 0) a.lse[(int64_t)bh * S + qrow] = (m_run + fast_log2(l_tot)) * kLn2;
 }
 
@@ -366,21 +376,25 @@ int cu_count(hipStream_t st) {
   return n > 0 ? n : 0;
 }
 
-template <typename E, int D>
+template <typename E, int D, int DP = D>
 hipError_t launch_fwd_d(const AttnArgs& a, hipStream_t st) {
   const int n_qtiles = (a.S + FwdCfg<D>::BQ - 1) / FwdCfg<D>::BQ;
   int n_cu = cu_count(st);
   if (n_cu == 0) n_cu = 1 << 30;  // one round: no reversal
   dim3 grid(n_qtiles * a.B * a.H), block(FwdCfg<D>::NT);
   if (a.causal)
-    hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, true>), grid, block, 0, st, a, n_qtiles, n_cu);
+    hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, true, DP>), grid, block, 0, st, a, n_qtiles,
+                       n_cu);
   else
-    hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, false>), grid, block, 0, st, a, n_qtiles, n_cu);
+    hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, false, DP>), grid, block, 0, st, a, n_qtiles,
+                       n_cu);
   return hipGetLastError();
 }
 
 template <typename E>
 hipError_t launch_fwd_e(const AttnArgs& a, hipStream_t st) {
+  if (a.D == 16) return launch_fwd_d<E, 64, 16>(a, st);
+  if (a.D == 32) return launch_fwd_d<E, 64, 32>(a, st);
   if (a.D == 64) return launch_fwd_d<E, 64>(a, st);
   return launch_fwd_d<E, 128>(a, st);
 }
@@ -388,7 +402,8 @@ hipError_t launch_fwd_e(const AttnArgs& a, hipStream_t st) {
 }  // namespace
 
 bool mfma_supports(int dtype, int D, int S) {
-  return (dtype == 1 || dtype == 2) && (D == 64 || D == 128) && S > 0 && S % 64 == 0;
+  return (dtype == 1 || dtype == 2) && (D == 16 || D == 32 || D == 64 || D == 128) && S > 0 &&
+         S % 64 == 0;
 }
 
 hipError_t launch_attn_fwd_mfma(int dtype, const AttnArgs& a, hipStream_t st) {

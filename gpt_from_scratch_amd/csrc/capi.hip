@@ -291,10 +291,12 @@ static bool bwd_mfma_path(mi_dtype dtype, int D, int S, const void* q, const int
 // Whether the matrix-core kernels can rotate dQ and dK as they store them:
 // their stores read four 16-bit angles per table with one vector load, so the
 // tables must be 16-bit, with contiguous angles and every row start aligned to
-// four of them.  Otherwise the host runs the inverse RoPE as a separate pass.
-static bool rope_fusable(const mi::RopeTab& r) {
+// four of them; head dims 16 and 32 (run in the D = 64 layout) have no
+// rotating stores.  Otherwise the host runs the inverse RoPE as a separate
+// pass.
+static bool rope_fusable(const mi::RopeTab& r, int D) {
   const int tsz = elem_size((mi_dtype)r.tdt);
-  return r.tdt != MI_F32 && r.cs_i == 1 && r.ss_i == 1 && r.cs_s % 4 == 0 && r.ss_s % 4 == 0 &&
+  return D >= 64 && r.tdt != MI_F32 && r.cs_i == 1 && r.ss_i == 1 && r.cs_s % 4 == 0 && r.ss_s % 4 == 0 &&
          ((uintptr_t)r.cos) % (4 * tsz) == 0 && ((uintptr_t)r.sin) % (4 * tsz) == 0;
 }
 
@@ -322,7 +324,7 @@ static mi_status grads_impl(mi_dtype dtype, int B, int H, int S, int D, int caus
     a.dq = targ(dq, dq_strides);
     a.dk = targ(dk, dk_strides);
     a.dv = targ(dv, dv_strides);
-    const bool fuse_rope = rope && rope_fusable(*rope);
+    const bool fuse_rope = rope && rope_fusable(*rope, D);
     if (fuse_rope) a.rope = *rope;
     if ((st = launched(mi::launch_attn_bwd_mfma(dtype, a, (hipStream_t)stream),
                        "attn_bwd_mfma")) != MI_OK || !rope || fuse_rope)
@@ -389,7 +391,7 @@ mi_status mi_attn_bwd_rope(mi_dtype dtype, int B, int H, int S, int D, int causa
   const bool fused = bwd_mfma_path(dtype, D, S, q, q_strides, k, k_strides, v, v_strides, dout,
                                    dout_strides, dq, dq_strides, dk, dk_strides, dv,
                                    dv_strides) &&
-                     rope_fusable(rope);
+                     rope_fusable(rope, D);
   if (!fused && (uint64_t)2 * S * B * H * (D / 2) >= (1ull << 31))
     return fail(MI_ERR_UNSUPPORTED, "tensor too large for one launch");
   if ((st = mi_attn_bwd_preprocess(dtype, B, H, S, D, o, o_strides, dout, dout_strides, lse, ws,

@@ -177,6 +177,13 @@ __device__ __forceinline__ uint32_t rows_extent(int rows, int64_t ss, int cols) 
   return (uint32_t)(((int64_t)(rows - 1) * ss + cols) * 2);
 }
 
+// A byte offset past every extent above: the host admits a tensor to the
+// matrix-core kernels only when 256 of its rows span less than 2^31 bytes,
+// so a load at this offset returns zeros (writes zeros to LDS) and touches
+// no memory.  Head dims below 64 staged in the D = 64 layout fetch their
+// padding chunks with it.
+constexpr uint32_t kOobOffset = 0x80000000u;
+
 // ---------------------------------------------------------------------------
 // Division by a run-time invariant (Granlund-Montgomery): n / d for n < 2^31.
 // ---------------------------------------------------------------------------
@@ -271,9 +278,12 @@ __device__ __forceinline__ u32x4 tr_operand(const uint16_t* p, int ld) {
 // stores 16 contiguous bytes and one instruction covers 64/(D/8) whole rows.
 // `grow` points at row 0 of the block, `ss` is the row stride in elements.
 // Row r of the staging keeps 16-byte chunk c at position c ^ (r & 7).
-template <typename E, int D>
+// DP < D (head dims 16 and 32 run in the D = 64 layout): only the first DP
+// columns are stored; the accumulators of the others are never read.
+template <typename E, int D, int DP = D>
 __device__ __forceinline__ void store_block_rows(const f32x16 (&acc)[D / 32], float sc,
                                                  uint16_t* lds, uint16_t* grow, int64_t ss) {
+  static_assert(DP % 16 == 0 && DP <= D, "stored columns");
   constexpr int CPR = D / 8;     // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;  // rows per store instruction
   const int lane = threadIdx.x & 63;
@@ -284,6 +294,7 @@ __device__ __forceinline__ void store_block_rows(const f32x16 (&acc)[D / 32], fl
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
       const int c = 4 * db + jj;
+      if (c >= DP / 8) continue;
       u32x2 w;
       w[0] = E::pack2(acc[db][4 * jj + 0] * sc, acc[db][4 * jj + 1] * sc);
       w[1] = E::pack2(acc[db][4 * jj + 2] * sc, acc[db][4 * jj + 3] * sc);
@@ -293,6 +304,7 @@ __device__ __forceinline__ void store_block_rows(const f32x16 (&acc)[D / 32], fl
   for (int p = 0; p < 32 / RPI; ++p) {
     const int r = p * RPI + lane / CPR;
     const int c = lane % CPR;
+    if (DP < D && c >= DP / 8) continue;
     const u32x4 v = *(const u32x4*)(lds + r * D + ((c ^ (r & 7)) << 3));
     *(u32x4*)(grow + (int64_t)r * ss + 8 * c) = v;
   }

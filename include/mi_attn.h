@@ -20,8 +20,10 @@
  *   - rope tensors are logically [S, B, H, D] (the layout the model hands to
  *     RoPE); the cos/sin tables are [S, D/2] with two element strides.
  *   - dtypes: MI_F32, MI_F16, MI_BF16.  Attention runs on bf16/f16 MFMA when
- *     D is 64 or 128 and S % 64 == 0; every other supported case runs on an
- *     exact-fp32 VALU kernel.  Arithmetic is fp32 in all kernels.
+ *     D is 16, 32, 64 or 128, S % 64 == 0 and every row is 16-byte aligned
+ *     (D = 16 and 32 in the D = 64 kernels' layout, the padding staged as
+ *     zeros); every other supported case runs on an exact-fp32 VALU kernel.
+ *     Arithmetic is fp32 in all kernels.
  *
  * Errors: a non-zero mi_status; mi_last_error() gives a message for the
  * calling thread.  Arguments are validated before anything is launched.
@@ -107,7 +109,7 @@ mi_status mi_attn_bwd(mi_dtype dtype, int B, int H, int S, int D, int causal,
  * tables (interleaved pairs, the rotation of mi_rope with inverse = 1,
  * evaluated on dQ and dK rounded to `dtype` first, so the result equals
  * mi_attn_bwd followed by mi_rope_qk(inverse = 1) on dq, dk in place, bit for
- * bit).  On the matrix-core path (D = 64 or 128) with 16-bit tables whose
+ * bit).  On the matrix-core path at D = 64 or 128 with 16-bit tables whose
  * angles are contiguous and whose row starts are 4-angle aligned (the
  * model's), the rotation is applied as the kernels store dQ and dK, saving the
  * separate read and write of both; otherwise the two run one after the other

@@ -197,6 +197,97 @@ def test_ragged_sequence_lengths(gpu, S, D):
     _config_check(gpu, 2, 2, S, D, seed=7 + S, std=1.0)
 
 
+@pytest.mark.parametrize("causal", [True, False])
+@pytest.mark.parametrize("S,D,dtype", [(64, 16, torch.bfloat16), (1024, 16, torch.bfloat16),
+                                       (192, 32, torch.bfloat16), (1024, 32, torch.bfloat16),
+                                       (320, 32, torch.float16), (512, 16, torch.float16)])
+def test_small_head_dims(gpu, S, D, dtype, causal):
+    """Head dims 16 and 32 (the reference's kernels take any power-of-two head
+    dim on the matrix units, core/myFlashAttn.py:447-457) on the matrix-core
+    kernels in the D = 64 layout: RoPE'd q, k through the model's strided views,
+    fwd+bwd within the bf16 bounds of the fp32 oracle, and two heads against the
+    float64 CPU oracle."""
+    from gpt_from_scratch_amd import apply_rope_qk
+    B, H = 2, 3
+    _config_check(gpu, B, H, S, D, seed=900 + S + D, std=1.0, causal=causal, dtype=dtype)
+    q, k, v, cos, sin, do = rope_inputs(B, H, S, D, 900 + S + D, 1.0, dtype, gpu)
+    qr, kr = apply_rope_qk(q, k, cos, sin)
+    qb, kb, vb = qr.permute(1, 2, 0, 3), kr.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3)
+    o, dq, dk, dv = _run(qb, kb, vb, do, causal)
+    for b, h in ((0, 0), (B - 1, H - 1)):
+        args = [t[b, h].cpu().double() for t in (qb, kb, vb, do)]
+        ro, _ = attention_forward(*args[:3], causal)
+        rdq, rdk, rdv, _ = attention_backward(*args, causal)
+        for name, got, want in (("o", o, ro), ("dq", dq, rdq), ("dk", dk, rdk), ("dv", dv, rdv)):
+            err = float((got[b, h].cpu().double() - want).abs().max())
+            assert err < 2e-2, (name, b, h, err)
+
+
+@pytest.mark.parametrize("D", [16, 32])
+def test_small_head_dims_read_and_write_only_their_columns(gpu, D):
+    """Head dims 16 and 32 run in the D = 64 layout, so the kernels must neither
+    read nor write the 64 - D columns that follow each row.  Q, K, V, dO, O and
+    the gradients are the first D columns of 64-wide rows whose remaining
+    columns hold NaN: a padding chunk fetched from memory instead of staged as
+    zeros would turn the outputs into NaN, and a store past D would overwrite
+    the NaN.  The results equal those on dense inputs bit for bit, and the same
+    call on rows whose stride is not a multiple of 16 bytes (the exact-fp32
+    VALU kernels) gives different bits within the bf16 bounds: the two
+    shapes ran different kernels."""
+    import ctypes
+    from gpt_from_scratch_amd import _lib
+    lib = _lib.lib()
+    B, H, S = 2, 3, 320
+    g = torch.Generator(device=gpu).manual_seed(5 + D)
+    dense = [torch.randn(B, H, S, D, generator=g, device=gpu).to(torch.bfloat16)
+             for _ in range(4)]
+
+    def wide(width, src=None):
+        w = torch.full((B, H, S, width), float("nan"), dtype=torch.bfloat16, device=gpu)
+        if src is not None:
+            w[..., :D] = src
+        return w
+
+    P = lambda t: ctypes.c_void_p(t.data_ptr())
+    ST = lambda t: (ctypes.c_int64 * 4)(*t.stride())
+    sp = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    sc = 1 / math.sqrt(D)
+
+    def run(width):
+        if width == D:
+            ins = [t.clone() for t in dense]
+            outs = [torch.full_like(dense[0], float("nan")) for _ in range(4)]
+            views = ins, outs
+        else:
+            ins = [wide(width, t) for t in dense]
+            outs = [wide(width) for _ in range(4)]
+            views = [t[..., :D] for t in ins], [t[..., :D] for t in outs]
+        (Q, K, V, dO), (O, dQ, dK, dV) = views
+        M = torch.empty(B, H, S, device=gpu)
+        ws = torch.empty(2, B, H, S, device=gpu)
+        x = (P(Q), ST(Q), P(K), ST(K), P(V), ST(V))
+        assert lib.mi_attn_fwd(2, B, H, S, D, 1, sc, *x, P(O), ST(O), P(M), sp) == 0
+        assert lib.mi_attn_bwd(2, B, H, S, D, 1, sc, *x, P(O), ST(O), P(dO), ST(dO), P(M),
+                               P(ws), P(dQ), ST(dQ), P(dK), ST(dK), P(dV), ST(dV), sp) == 0
+        torch.cuda.synchronize()
+        if width != D:
+            for t in outs:
+                assert bool(torch.isnan(t[..., D:]).all())
+        return [t.clone() for t in (O, dQ, dK, dV)]
+
+    base = run(D)
+    for t in base:
+        assert not bool(torch.isnan(t).any())
+    for got, want in zip(run(64), base):
+        assert torch.equal(got, want)
+    exact = run(D + 1)  # row stride of D + 1 elements: not 16-byte aligned
+    ref = reference(*dense, True)
+    for name, mf, vl in zip(("o", "dq", "dk", "dv"), base, exact):
+        assert not torch.equal(mf, vl), name
+        assert_close_bf16(name, mf, ref[name])
+        assert_close_bf16(name, vl, ref[name])
+
+
 def test_noncausal(gpu):
     _config_check(gpu, 2, 4, 512, 64, seed=11, std=1.0, causal=False)
     _config_check(gpu, 1, 2, 256, 128, seed=12, std=0.5, causal=False)
@@ -345,12 +436,13 @@ def test_backward_deterministic_writes_every_output_keeps_inputs(gpu, B, H, S, D
 
 
 @pytest.mark.parametrize("causal", [1, 0])
-@pytest.mark.parametrize("B,H,S,D", [(2, 3, 576, 64), (1, 2, 512, 128)])
+@pytest.mark.parametrize("B,H,S,D", [(2, 3, 576, 64), (1, 2, 512, 128), (2, 3, 576, 32),
+                                     (1, 2, 512, 16)])
 def test_separate_dkdv_dq_equal_combined(gpu, B, H, S, D, causal):
     """mi_attn_bwd_dkdv then mi_attn_bwd_dq (the reference's `_attn_bwd_LoopQ`
     and `_attn_bwd_LoopKV` launches, core/myFlashAttn.py:349-439) on NaN-filled
     outputs give the same bits as mi_attn_bwd_grads, which runs both kinds of
-    work item in one launch at D = 64: the items accumulate in the same order
+    work item in one launch at D <= 64: the items accumulate in the same order
     whichever launch runs them.  S = 576 leaves the last 128-row item half
     empty; each entry point writes only its own outputs."""
     import ctypes
@@ -386,7 +478,7 @@ def test_separate_dkdv_dq_equal_combined(gpu, B, H, S, D, causal):
 
 
 @pytest.mark.parametrize("causal", [True, False])
-@pytest.mark.parametrize("S,D", [(1024, 64), (512, 128)])
+@pytest.mark.parametrize("S,D", [(1024, 64), (512, 128), (1024, 32), (512, 16)])
 def test_running_max_moves_every_tile(gpu, S, D, causal):
     """Scores that grow along the key axis (gpu_ref.rescale_stress_inputs): every
     query's maximum sits at its last visible key and rises by more than the
@@ -419,11 +511,13 @@ def test_running_max_moves_every_tile(gpu, S, D, causal):
                                              (torch.bfloat16, 64, torch.bfloat16, 1),
                                              (torch.bfloat16, 128, torch.float32, 0),
                                              (torch.float16, 64, torch.float16, 0),
+                                             (torch.bfloat16, 32, torch.bfloat16, 0),
                                              (torch.float32, 64, torch.float32, 0)])
 def test_bwd_rope_equals_bwd_then_inverse_rope(gpu, dtype, D, tab, pad):
     """mi_attn_bwd_rope (the inverse rotation fused into the dQ / dK stores on
-    the matrix-core path at D = 64 with aligned 16-bit tables; D = 128, fp32
-    tables, rows not 4-angle aligned (pad) and fp32 take a separate pass)
+    the matrix-core path at D = 64 and 128 with aligned 16-bit tables; fp32
+    tables, rows not 4-angle aligned (pad), D = 32 and fp32 take a separate
+    pass)
     against mi_attn_bwd followed by mi_rope_qk(inverse) on dq, dk in place: dQ,
     dK and dV bit for bit, with q, k, v, dO as the model's strided views and the
     gradients written into the slots of one [S, B, 3, H, D] buffer."""
