@@ -156,6 +156,26 @@ __device__ __forceinline__ float sum_halves(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// v plus the value of the lane that DPP control CTRL selects (quad_perm,
+// row_half_mirror, row_mirror, ...), in every lane.
+template <int CTRL>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF,
+                                                        false));
+}
+
+// Sum over each aligned group of N (2, 4 or 8) lanes by xor butterflies
+// (quad_perm [1,0,3,2], quad_perm [2,3,0,1], row_half_mirror): IEEE addition
+// commutes, so every lane of a group gets the same bits.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(N == 2 || N == 4 || N == 8, "group size");
+  v = dpp_add<0xB1>(v);
+  if constexpr (N >= 4) v = dpp_add<0x4E>(v);
+  if constexpr (N >= 8) v = dpp_add<0x141>(v);
+  return v;
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 __device__ __forceinline__ float fast_log2(float x) { return __builtin_amdgcn_logf(x); }
 

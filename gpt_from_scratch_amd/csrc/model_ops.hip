@@ -503,11 +503,6 @@ __device__ __forceinline__ void* row_ptr(void* base, int64_t row, int64_t stride
 // Sum over the 64 lanes, the same bits in every lane: DPP butterflies within
 // each row of 16 lanes (xor 1, xor 2, mirror within 8, mirror within 16), then
 // the row pairs (lane ^ 16) and the halves (lane ^ 32) by permlane swaps.
-template <int CTRL>
-__device__ __forceinline__ float dpp_add(float v) {
-  return v + __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF,
-                                                        false));
-}
 __device__ __forceinline__ float wave_sum(float v) {
   v = dpp_add<0xB1>(v);   // quad_perm [1,0,3,2]
   v = dpp_add<0x4E>(v);   // quad_perm [2,3,0,1]

@@ -1,10 +1,10 @@
 """Compiler resource report of the gfx950 kernels (CPU only: hipcc cross-compiles).
 
-The matrix-core attention kernels, RoPE and the model operators must not use
-scratch memory (register spills or run-time-indexed private arrays), and the hot
-attention kernels must keep the occupancy their tiling assumes.  The
-documented exceptions are the causal D = 128 dK/dV launch with the rotating
-stores (one spilled register) and the exact-fp32 VALU kernels at D = 128.  At
+The attention kernels (matrix-core and exact-fp32), RoPE and the model
+operators must not use scratch memory (register spills or run-time-indexed
+private arrays), and the hot attention kernels must keep the occupancy their
+tiling assumes.  The documented exception is the causal D = 128 dK/dV launch
+with the rotating stores (one spilled register).  At
 D = 64 every backward launch, the separate dK/dV and dQ ones included, runs the
 combined kernel, which has no scratch."""
 import os
@@ -20,11 +20,8 @@ CSRC = os.path.join(ROOT, "gpt_from_scratch_amd", "csrc")
 HIPCC = "/opt/rocm/bin/hipcc"
 SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "attn_valu.hip", "rope.hip", "model_ops.hip")
 # the causal D = 128 dK/dV launch with the rotating stores (mi_attn_bwd_rope):
-# 8 bytes per lane, one register reloaded once per step; the exact-fp32 /
-# ragged-length VALU kernels at D = 128, where one lane's rows alone fill the
-# register file
-ALLOWED_SCRATCH = re.compile(r"attn_bwd_dkdv_kernel<mi::(BF16|F16), 128, true, true>"
-                             r"|attn_(fwd|bwd_dq|bwd_dkdv)_valu_kernel<\d, 128, (true|false)>")
+# 8 bytes per lane, one register reloaded once per step
+ALLOWED_SCRATCH = re.compile(r"attn_bwd_dkdv_kernel<mi::(BF16|F16), 128, true, true>")
 
 
 def _hipflags():
