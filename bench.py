@@ -41,6 +41,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "causal attn fwd+bwd TFLOP/s & % bf16 MFMA peak, B8 H12 S1024 D64"
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_FP32_TFLOPS = 157.3    # MI355X fp32
 PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
 
 
@@ -57,7 +58,7 @@ def parse_args():
     ap.add_argument("--no-gpt", action="store_true",
                     help="skip the config-5 GPT train-step measurement")
     ap.add_argument("--no-d128", action="store_true",
-                    help="skip the D = 128 attention measurements (configs 3 and 4)")
+                    help="skip the measurements of configs 1, 3 and 4 (fp32 D = 64, bf16 D = 128)")
     ap.add_argument("--no-model-ops", action="store_true",
                     help="skip the config-5 model-operator kernel measurements")
     ap.add_argument("--summarize", metavar="DIR",
@@ -324,29 +325,33 @@ def model_ops_bench(dev, lib):
     return out
 
 
-def attn_config_bench(dev, lib, B, H, S, D, seed, std, steps):
+def attn_config_bench(dev, lib, B, H, S, D, seed, std, steps, dtype=None):
     """Per-kernel times and the fwd+bwd step of one attention configuration in
     the model's layout (q/k RoPE'd out of a fused qkv, v a view of it), through
     the C ABI like the config-2 step: the forward, the delta preprocess and the
     gradient launch(es) each timed over `steps` back-to-back launches, and the
-    whole step over `steps` steps with events only at its ends."""
+    whole step over `steps` steps with events only at its ends.  dtype: bf16
+    (default; fractions of the bf16 matrix peak) or fp32 (the exact-fp32
+    kernels; fractions of the fp32 peak)."""
     import torch
+    dtype = torch.bfloat16 if dtype is None else dtype
+    peak = PEAK_BF16_TFLOPS if dtype == torch.bfloat16 else PEAK_FP32_TFLOPS
     from gpt_from_scratch_amd import _lib
     from gpt_from_scratch_amd.rope import apply_rope_qk
     from gpt_from_scratch_amd.position_embeddings import RotaryEmbedding
 
     g = torch.Generator().manual_seed(seed)
-    qkv = (torch.randn(S, B, 3, H, D, generator=g) * std).to(torch.bfloat16).to(dev)
-    do = torch.randn(B, H, S, D, generator=g).to(torch.bfloat16).to(dev)
+    qkv = (torch.randn(S, B, 3, H, D, generator=g) * std).to(dtype).to(dev)
+    do = torch.randn(B, H, S, D, generator=g).to(dtype).to(dev)
     rot = RotaryEmbedding(D, max_position_embeddings=S, device="cpu")
-    cos, sin = (t.to(torch.bfloat16).to(dev) for t in (rot.cos_cached, rot.sin_cached))
+    cos, sin = (t.to(dtype).to(dev) for t in (rot.cos_cached, rot.sin_cached))
     q, k, v = qkv.unbind(2)
     qr, kr = apply_rope_qk(q, k, cos, sin)
     Q, K, V = qr.permute(1, 2, 0, 3), kr.permute(1, 2, 0, 3), v.permute(1, 2, 0, 3)
-    O = torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev)
+    O = torch.empty(B, H, S, D, dtype=dtype, device=dev)
     LSE = torch.empty(B, H, S, dtype=torch.float32, device=dev)
     DELTA = torch.empty((2,) + tuple(LSE.shape), dtype=torch.float32, device=dev)  # workspace
-    dQ, dK, dV = (torch.empty(B, H, S, D, dtype=torch.bfloat16, device=dev) for _ in range(3))
+    dQ, dK, dV = (torch.empty(B, H, S, D, dtype=dtype, device=dev) for _ in range(3))
     stream = torch.cuda.current_stream(dev)
     sp = ctypes.c_void_p(stream.cuda_stream)
     P = lambda t: ctypes.c_void_p(t.data_ptr())
@@ -372,15 +377,16 @@ def attn_config_bench(dev, lib, B, H, S, D, seed, std, steps):
     e1.record(stream)
     torch.cuda.synchronize()
     step_us = e0.elapsed_time(e1) / steps * 1e3
-    out = {"shape": f"B{B} H{H} S{S} D{D} bf16 causal", "step_us": round(step_us, 2),
+    dname = "bf16" if dtype == torch.bfloat16 else "fp32"
+    out = {"shape": f"B{B} H{H} S{S} D{D} {dname} causal", "step_us": round(step_us, 2),
            "tflops": round(fl["total"] / (step_us * 1e-6) / 1e12, 1),
-           "frac": round(fl["total"] / (step_us * 1e-6) / 1e12 / PEAK_BF16_TFLOPS, 4)}
+           "frac": round(fl["total"] / (step_us * 1e-6) / 1e12 / peak, 4), "peak_tflops": peak}
     for name, work in (("attn_fwd", fl["fwd"]), ("attn_bwd_preprocess", None),
                        ("attn_bwd", fl["bwd"])):
         ent = {"avg_us": round(per[name], 2)}
         if work:
             tf = work / (per[name] * 1e-6) / 1e12
-            ent.update(tflops=round(tf, 1), frac=round(tf / PEAK_BF16_TFLOPS, 4))
+            ent.update(tflops=round(tf, 1), frac=round(tf / peak, 4))
         out[name] = ent
     return out
 
@@ -868,6 +874,10 @@ def main():
                                     "inputs": "one q/k pair re-read (Infinity Cache)"}},
     }
     if not args.no_d128:
+        # config 1 (fp32, the exact-fp32 kernels): a parity case, measured beside the headline
+        out["attn_c1_fp32"] = attn_config_bench(dev, lib, 1, 12, 256, 64, 1, 1.0, args.steps,
+                                                dtype=torch.float32)
+        _progress("config 1 done")
         # configs 3 and 4 (D = 128): parity cases, measured beside the headline
         out["attn_d128"] = {
             "config3": attn_config_bench(dev, lib, 2, 16, 4096, 128, 3, 0.5, args.steps),
