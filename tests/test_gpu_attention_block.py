@@ -15,7 +15,8 @@ pytestmark = pytest.mark.gpu
 
 
 @pytest.mark.parametrize("S,B,H,D,causal", [(256, 2, 4, 64, True), (128, 2, 2, 128, True),
-                                            (192, 1, 3, 64, False), (100, 2, 2, 64, True)])
+                                            (192, 1, 3, 64, False), (100, 2, 2, 64, True),
+                                            (256, 2, 6, 32, True), (128, 1, 8, 16, False)])
 def test_block_matches_composition(gpu, S, B, H, D, causal):
     from gpt_from_scratch_amd import (RotaryEmbedding, apply_flash_attn, apply_rope_qk,
                                       attention_block)
@@ -121,12 +122,13 @@ def _slot_budget(qkv, cos, sin, H, g, o, want_slot, causal):
     return slots
 
 
-@pytest.mark.parametrize("S,B,H,D,std", [(1024, 8, 12, 64, 1.0), (2048, 1, 4, 128, 0.5)])
+@pytest.mark.parametrize("S,B,H,D,std", [(1024, 8, 12, 64, 1.0), (2048, 1, 4, 128, 0.5),
+                                         (512, 2, 8, 32, 1.0)])
 def test_block_against_oracle(gpu, S, B, H, D, std):
     """The fused block (RoPE into a [S, B, 2, H, D] buffer, attention on strided
     views, O stored as [S, B, H*D], dQ/dK/dV into one [S, B, 3, H, D] gradient
     with the inverse rotation in place) against the oracle's autograd of the
-    unfused reference chain: config 2's shape and a D = 128 shape.  Output and
+    unfused reference chain: config 2's shape, a D = 128 and a D = 32 shape.  Output and
     the v slot within the bf16 bounds (max-abs 2e-2, mean-rel 1e-2); the q and
     k slots (the inverse rotation's output, rounded once more than an
     attention gradient) element by element within the rounding budget
