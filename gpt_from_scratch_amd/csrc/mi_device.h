@@ -79,15 +79,6 @@ struct F16 {
   }
 };
 
-// Generic element access used by the fp32 VALU kernels and RoPE.
-template <typename T> struct Elem;
-template <> struct Elem<float> {
-  static __device__ __forceinline__ float load(const float* p) { return *p; }
-  static __device__ __forceinline__ void store(float* p, float v) { *p = v; }
-};
-struct bf16_tag {};
-struct f16_tag {};
-
 __device__ __forceinline__ float bf16_to_f32(uint16_t x) { return BF16::to_f32(x); }
 __device__ __forceinline__ float f16_to_f32(uint16_t x) { return F16::to_f32(x); }
 __device__ __forceinline__ uint16_t f32_to_bf16(float x) {
@@ -134,10 +125,6 @@ template <> struct Store<2> {
 // ---------------------------------------------------------------------------
 // Wave-level helpers.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float xor_shfl(float v, int mask) {
-  return __shfl_xor(v, mask, 64);
-}
-
 // IEEE 754-2019 maximum (NaN-propagating); lowers to v_maximum3_f32 chains.
 __device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
 
@@ -254,9 +241,6 @@ __device__ __forceinline__ void transpose4x2(uint32_t r0, uint32_t r1, uint32_t 
 // 32x32 accumulator (registers 8h .. 8h+7 hold rows 16h + 4*(l/32) + {0..3}
 // and 16h + 8 + 4*(l/32) + {0..3}).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int tr_lane_offset(int lane, int ld) {
-  return (4 * (lane >> 5) + ((lane & 15) >> 2)) * ld + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-}
 
 // 16 bytes per lane from a buffer straight into LDS (no VGPRs): lane i's data
 // lands at lds + 16*i bytes; `lds` must be wave-uniform.  Completion is
@@ -282,7 +266,8 @@ __device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t* p) {
 }
 
 // A operand for rows [m0, m0+32) of T^T and k rows [k0, k0+16) of T, where
-// `p` = tile + k0*ld + m0 + tr_lane_offset(lane, ld).
+// `p` = tile + k0*ld + m0 + tr_row(l)*ld + tr_col(l) (the window offsets
+// above; the kernels fold their LDS swizzle into them).
 __device__ __forceinline__ u32x4 tr_operand(const uint16_t* p, int ld) {
   const u32x2 lo = ds_read_tr16(p);
   const u32x2 hi = ds_read_tr16(p + 8 * ld);
