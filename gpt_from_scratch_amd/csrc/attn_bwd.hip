@@ -275,10 +275,13 @@ struct Tab4 {
 // values the separate inverse RoPE pass over the stored gradient would write.
 // Tables: 16-bit, contiguous angles, rows 4-angle aligned (checked by the
 // host).
-template <typename E, int D, int TDT>
+// TAIL: rows at or past nrows (sequence tails) are not stored, and read the
+// angles of row nrows - 1.
+template <typename E, int D, int TDT, bool TAIL>
 __device__ __forceinline__ void store_block_rows_rope_t(const f32x16 (&acc)[D / 32], float sc,
                                                         uint16_t* lds, uint16_t* grow,
-                                                        int64_t ss, const RopeTab& t, int pos0) {
+                                                        int64_t ss, const RopeTab& t, int pos0,
+                                                        int nrows) {
   constexpr int CPR = D / 8;
   constexpr int RPI = 64 / CPR;
   const int lane = threadIdx.x & 63;
@@ -306,7 +309,8 @@ __device__ __forceinline__ void store_block_rows_rope_t(const f32x16 (&acc)[D / 
     typename Tab4<TDT>::type cs[PCH], sn[PCH];
 #pragma unroll
     for (int i = 0; i < PCH; ++i) {
-      const int r = (p0 + i) * RPI + lane / CPR;
+      const int r0 = (p0 + i) * RPI + lane / CPR;
+      const int r = TAIL ? min(r0, nrows - 1) : r0;
       const int c = lane % CPR;
       cs[i] = Tab4<TDT>::load(t.cos, t.cs_s, pos0 + r, 4 * c);
       sn[i] = Tab4<TDT>::load(t.sin, t.ss_s, pos0 + r, 4 * c);
@@ -324,20 +328,21 @@ __device__ __forceinline__ void store_block_rows_rope_t(const f32x16 (&acc)[D / 
                     Tab4<TDT>::get(cs[i], k), Tab4<TDT>::get(sn[i], k), true, re, ro);
         o[k] = E::pack2(re, ro);
       }
-      *(u32x4*)(grow + (int64_t)r * ss + 8 * c) = o;
+      if (!TAIL || r < nrows) *(u32x4*)(grow + (int64_t)r * ss + 8 * c) = o;
     }
   }
 }
 
-template <typename E, int D>
+template <typename E, int D, bool TAIL = false>
 __device__ __forceinline__ void store_block_rows_rope(const f32x16 (&acc)[D / 32], float sc,
                                                       uint16_t* lds, uint16_t* grow, int64_t ss,
-                                                      const RopeTab& t, int pos0) {
+                                                      const RopeTab& t, int pos0,
+                                                      int nrows = 32) {
   // 16-bit tables only (the host runs fp32 tables as a separate pass)
   if (t.tdt == 2)
-    store_block_rows_rope_t<E, D, 2>(acc, sc, lds, grow, ss, t, pos0);
+    store_block_rows_rope_t<E, D, 2, TAIL>(acc, sc, lds, grow, ss, t, pos0, nrows);
   else
-    store_block_rows_rope_t<E, D, 1>(acc, sc, lds, grow, ss, t, pos0);
+    store_block_rows_rope_t<E, D, 1, TAIL>(acc, sc, lds, grow, ss, t, pos0, nrows);
 }
 
 struct BwdItem {
@@ -393,7 +398,9 @@ __device__ __forceinline__ int first_row(const BwdItem& it) {
 
 // SKIP0: leave res.r[0] unloaded (the D = 128 dK/dV kind keeps K in LDS).
 // DP < D: rows of DP columns; the registers of columns past DP are zeros.
-template <int D, bool SKIP0 = false, int DP = D>
+// RAG: the descriptors end at row S (rows past it load as zeros, lse and
+// delta as 0).
+template <int D, bool SKIP0 = false, int DP = D, bool RAG = false>
 __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& it,
                                               Resident<D>& res) {
   const int lane = threadIdx.x & 63;
@@ -405,8 +412,9 @@ __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& 
   const int w0 = it.tile * BwdCfg<D>::OWN + 32 * wave;  // first row of this wave (SGPR)
   if (w0 < a.S) {
     // wave base in the descriptor, lane offset (row l%32, 8 columns) in one VGPR
-    const auto r0 = tile_rsrc(head_ptr(t0, b, h) + (int64_t)w0 * t0.ss, rows_extent(32, t0.ss, DP));
-    const auto r1 = tile_rsrc(head_ptr(t1, b, h) + (int64_t)w0 * t1.ss, rows_extent(32, t1.ss, DP));
+    const int nr = RAG ? min(32, a.S - w0) : 32;
+    const auto r0 = tile_rsrc(head_ptr(t0, b, h) + (int64_t)w0 * t0.ss, rows_extent(nr, t0.ss, DP));
+    const auto r1 = tile_rsrc(head_ptr(t1, b, h) + (int64_t)w0 * t1.ss, rows_extent(nr, t1.ss, DP));
     const uint32_t o0 = (uint32_t)(((lane & 31) * t0.ss + 8 * (lane >> 5)) * 2);
     const uint32_t o1 = (uint32_t)(((lane & 31) * t1.ss + 8 * (lane >> 5)) * 2);
     // kind 0 keeps V negated (sign bits of both 16-bit halves flipped)
@@ -424,9 +432,9 @@ __device__ __forceinline__ void load_resident(const AttnArgs& a, const BwdItem& 
     if (it.kind) {
       const int64_t o = (int64_t)it.bh * a.S + w0;
       res.lse2 = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                     tile_rsrc(a.lse2 + o, 32 * 4), (lane & 31) * 4, 0, 0));
+                     tile_rsrc(a.lse2 + o, nr * 4), (lane & 31) * 4, 0, 0));
       res.dl = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                   tile_rsrc(a.delta + o, 32 * 4), (lane & 31) * 4, 0, 0));
+                   tile_rsrc(a.delta + o, nr * 4), (lane & 31) * 4, 0, 0));
     }
   } else {
 #pragma unroll
@@ -473,14 +481,17 @@ __device__ __forceinline__ StageSrc<D> stage_src(const AttnArgs& a, const BwdIte
 
 // Streamed tile starting at row `row0` straight into LDS buffer `dst`;
 // completion is tracked by vmcnt and the barrier that ends the step.
-template <int D, int DP = D>
+// RAG: the descriptors end at row S (rows past it stage as zeros, their lse
+// and delta as 0).
+template <int D, int DP = D, bool RAG = false>
 __device__ __forceinline__ void dma_stage(const StageSrc<D>& s, int kind, int row0,
-                                          const BwdBuf& dst) {
+                                          const BwdBuf& dst, int S = 0) {
   using C = BwdCfg<D>;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const auto r0 = tile_rsrc(s.p0 + (int64_t)row0 * s.ss0, rows_extent(C::TILE, s.ss0, DP));
-  const auto r1 = tile_rsrc(s.p1 + (int64_t)row0 * s.ss1, rows_extent(C::TILE, s.ss1, DP));
+  const int nr = RAG ? min(C::TILE, S - row0) : C::TILE;
+  const auto r0 = tile_rsrc(s.p0 + (int64_t)row0 * s.ss0, rows_extent(nr, s.ss0, DP));
+  const auto r1 = tile_rsrc(s.p1 + (int64_t)row0 * s.ss1, rows_extent(nr, s.ss1, DP));
 #pragma unroll
   for (int m = 0; m < C::SPW; ++m) {
     buffer_load_lds16(r0, s.off0[m], dst.t0 + (wave + 4 * m) * 512);
@@ -489,7 +500,7 @@ __device__ __forceinline__ void dma_stage(const StageSrc<D>& s, int kind, int ro
   if (kind == 0 && wave >= 2 && lane < C::TILE) {
     // waves 2 and 3: lse and delta of the tile's query rows (4 bytes per lane)
     const float* src = (wave == 2 ? s.lse : s.delta) + row0;
-    buffer_load_lds4(tile_rsrc(src, C::TILE * 4), lane * 4, dst.sl + (wave - 2) * C::TILE);
+    buffer_load_lds4(tile_rsrc(src, nr * 4), lane * 4, dst.sl + (wave - 2) * C::TILE);
   }
 }
 
@@ -505,7 +516,7 @@ __device__ __forceinline__ void dma_stage(const StageSrc<D>& s, int kind, int ro
 // accumulators together need ~290 VGPRs, and holding all of them spilled
 // ~390 bytes per lane.  The region then stages the wave's dK and dV stores.
 // ---------------------------------------------------------------------------
-template <typename E, int D, bool CAUSAL, bool ROPE, int DP>
+template <typename E, int D, bool CAUSAL, bool ROPE, int DP, bool RAG>
 __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
                                           const BwdBuf (&bufs)[2]) {
   using C = BwdCfg<D>;
@@ -531,7 +542,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
   const LdsOffsets<D> lo = lds_offsets<D>(lane);
 
   const int q_begin = first_row<D, CAUSAL>(it);
-  const int nq = (S - q_begin) / C::TILE;
+  const int nq = RAG ? (S - q_begin + C::TILE - 1) / C::TILE : (S - q_begin) / C::TILE;
   const StageSrc<D> src = stage_src<D, false, DP>(a, it);
 
   f32x16 dk[C::DB], dv[C::DB];
@@ -544,13 +555,13 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
 
   // First tile's loads before the resident rows: one memory round trip for
   // both (the V negation waits for its rows, not for the tile).
-  dma_stage<D, DP>(src, 0, q_begin, bufs[0]);
+  dma_stage<D, DP, RAG>(src, 0, q_begin, bufs[0], S);
   if constexpr (K_IN_LDS) {
     // the wave's 32 K rows: 8 one-KB slices of 4 rows, lane i writing chunk
     // position i%16 of row 4m + i/16, i.e. fetching chunk (i%16) ^ swz(row)
     if (wave_valid) {
       const auto rk = tile_rsrc(head_ptr(a.k, b, h) + (int64_t)kw * a.k.ss,
-                                rows_extent(32, a.k.ss, D));
+                                rows_extent(RAG ? min(32, S - kw) : 32, a.k.ss, D));
 #pragma unroll
       for (int m = 0; m < 32 * D * 2 / 1024; ++m) {
         const int r = m * C::RPS + lane / C::CPR;
@@ -560,7 +571,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     }
   }
   Resident<D> res;
-  load_resident<D, K_IN_LDS, DP>(a, it, res);
+  load_resident<D, K_IN_LDS, DP, RAG>(a, it, res);
   const u32x4(&kf)[C::KS] = res.r[0];
   const u32x4(&vn)[C::KS] = res.r[1];  // -V
   __syncthreads();
@@ -576,7 +587,8 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     constexpr int P = decltype(parity)::value;
     const int q0 = q_begin + j * C::TILE;
     // (at D = 128 the last step is not peeled: a uniform branch skips its load)
-    if (!LAST && (D == 64 || j + 1 < nq)) dma_stage<D, DP>(src, 0, q0 + C::TILE, bufs[P ^ 1]);
+    if (!LAST && (D == 64 || j + 1 < nq))
+      dma_stage<D, DP, RAG>(src, 0, q0 + C::TILE, bufs[P ^ 1], S);
 
     if (wave_valid && (!MASKED || q0 + C::TILE - 1 >= kw)) {
       const uint16_t* Qs = bufs[P].t0;
@@ -663,7 +675,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     }
     if (j < j_end) step(j++, masked_tag, std::false_type{}, P0{});
   };
-  // nq >= 1: the matrix-core path needs S % 64 == 0.
+  // nq >= 1 (S > q_begin)
   if constexpr (D == 128) {
     // Peeled last steps (four more copies of the step) raised the register
     // pressure of the whole item past 256 and spilled; here the loop runs to
@@ -685,6 +697,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
   }
 
   if (!wave_valid) return;
+  const int nrows = RAG ? min(32, S - kw) : 32;  // keys of this wave below S
   uint16_t* const dk_rows = (uint16_t*)a.dk.ptr + b * a.dk.sb + h * a.dk.sh + (int64_t)kw * a.dk.ss;
   uint16_t* const dv_rows = (uint16_t*)a.dv.ptr + b * a.dv.sb + h * a.dv.sh + (int64_t)kw * a.dv.ss;
   if constexpr (D == 64) {
@@ -692,21 +705,21 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     // stages its rows (dK, then dV) through tile buffer w.
     uint16_t* stage = wave_stage_buf(bufs, wave);
     // dV first: its accumulators are dead before dK's rotation needs registers
-    store_block_rows<E, D, DP>(dv, 1.f, stage, dv_rows, a.dv.ss);
+    store_block_rows<E, D, DP>(dv, 1.f, stage, dv_rows, a.dv.ss, nrows);
     if (ROPE && a.rope.cos)
-      store_block_rows_rope<E, D>(dk, a.scale, stage, dk_rows, a.dk.ss, a.rope, kw);
+      store_block_rows_rope<E, D, RAG>(dk, a.scale, stage, dk_rows, a.dk.ss, a.rope, kw, nrows);
     else
-      store_block_rows<E, D, DP>(dk, a.scale, stage, dk_rows, a.dk.ss);
+      store_block_rows<E, D, DP>(dk, a.scale, stage, dk_rows, a.dk.ss, nrows);
   } else {
     // D = 128: the wave's K region (32 x D, its own) is idle after the last
     // step.  (Written straight from the accumulators instead, 8 bytes per lane
     // and row, the launch measured the same at configs 3 and 4 and 2% slower
     // at B8 S1024.)
-    store_block_rows<E, D>(dv, 1.f, kw_lds, dv_rows, a.dv.ss);
+    store_block_rows<E, D>(dv, 1.f, kw_lds, dv_rows, a.dv.ss, nrows);
     if (ROPE && a.rope.cos)
-      store_block_rows_rope<E, D>(dk, a.scale, kw_lds, dk_rows, a.dk.ss, a.rope, kw);
+      store_block_rows_rope<E, D, RAG>(dk, a.scale, kw_lds, dk_rows, a.dk.ss, a.rope, kw, nrows);
     else
-      store_block_rows<E, D>(dk, a.scale, kw_lds, dk_rows, a.dk.ss);
+      store_block_rows<E, D>(dk, a.scale, kw_lds, dk_rows, a.dk.ss, nrows);
   }
 }
 
@@ -716,7 +729,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
 // per-lane scalars and dS^T feeds dQ^T = K^T dS^T directly (K^T read
 // transposed from the K tile).
 // ---------------------------------------------------------------------------
-template <typename E, int D, bool CAUSAL, bool ROPE, int DP>
+template <typename E, int D, bool CAUSAL, bool ROPE, int DP, bool RAG>
 __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
                                         const BwdBuf (&bufs)[2]) {
   using C = BwdCfg<D>;
@@ -736,7 +749,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   const LdsOffsets<D, D == 128> lo = lds_offsets<D, D == 128>(lane);
 
   const int kv_end = CAUSAL ? min(q0 + C::OWN, S) : S;
-  const int nkv = kv_end / C::TILE;
+  const int nkv = RAG ? (kv_end + C::TILE - 1) / C::TILE : kv_end / C::TILE;
   const StageSrc<D> src = stage_src<D, D == 128, DP>(a, it);
 
   f32x16 acc[C::DB];
@@ -745,9 +758,9 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   const float c = a.scale_log2;
 
   // First tile's loads before the resident rows (one round trip for both).
-  dma_stage<D, DP>(src, 1, 0, bufs[0]);
+  dma_stage<D, DP, RAG>(src, 1, 0, bufs[0], S);
   Resident<D> res;
-  load_resident<D, false, DP>(a, it, res);
+  load_resident<D, false, DP, RAG>(a, it, res);
   const u32x4(&qf)[C::KS] = res.r[0];
   const u32x4(&df)[C::KS] = res.r[1];
   const float lse2 = res.lse2;
@@ -768,7 +781,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
     constexpr bool LAST = decltype(last_tag)::value;
     constexpr int P = decltype(parity)::value;
     const int kv0 = j * C::TILE;
-    if (!LAST) dma_stage<D, DP>(src, 1, kv0 + C::TILE, bufs[P ^ 1]);
+    if (!LAST) dma_stage<D, DP, RAG>(src, 1, kv0 + C::TILE, bufs[P ^ 1], S);
 
     if (wave_valid && (!MASKED || kv0 <= qw + 31)) {
       const uint16_t* Ks = bufs[P].t0;
@@ -796,6 +809,10 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
         for (int r = 0; r < 16; ++r) {
           float p = fast_exp2(__builtin_fmaf(s[r], c, -lse2));
           if (MASKED && diag && 8 * (r >> 2) + (r & 3) > l32 - 4 * g) p = 0.f;
+          // RAG, non-causal: the last tile's keys at or past S (zero rows,
+          // whose P = exp2(-lse) need not be finite) take P = 0; causal
+          // masking already covers them
+          if (RAG && !CAUSAL && LAST && 8 * (r >> 2) + (r & 3) >= S - kvb - 4 * g) p = 0.f;
           dp[r] = p * dp[r];
         }
 #pragma unroll
@@ -832,7 +849,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
     }
     if (j < j_end) step(j++, masked_tag, std::false_type{}, P0{});
   };
-  // nkv >= 1: the matrix-core path needs S % 64 == 0.
+  // nkv >= 1 (kv_end > 0)
   const int n_main = CAUSAL ? max(0, nkv - C::OWN / C::TILE) : nkv;
   run(min(n_main, nkv - 1), std::false_type{});
   if constexpr (CAUSAL) run(nkv - 1, std::true_type{});
@@ -850,17 +867,19 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   const int h = it.bh % a.H;
   uint16_t* const dq_rows =
       (uint16_t*)a.dq.ptr + b * a.dq.sb + h * a.dq.sh + (int64_t)qw * a.dq.ss;
+  const int nrows = RAG ? min(32, S - qw) : 32;  // queries of this wave below S
   if (ROPE && a.rope.cos)
-    store_block_rows_rope<E, D>(acc, a.scale, wave_stage_buf(bufs, wave), dq_rows, a.dq.ss,
-                                a.rope, qw);
+    store_block_rows_rope<E, D, RAG>(acc, a.scale, wave_stage_buf(bufs, wave), dq_rows, a.dq.ss,
+                                a.rope, qw, nrows);
   else
-    store_block_rows<E, D, DP>(acc, a.scale, wave_stage_buf(bufs, wave), dq_rows, a.dq.ss);
+    store_block_rows<E, D, DP>(acc, a.scale, wave_stage_buf(bufs, wave), dq_rows, a.dq.ss,
+                               nrows);
 }
 
 // One item per workgroup.  One LDS array per buffer and tensor, so that the
 // compiler can see that a direct load into one buffer never aliases the
 // reads of the other.
-template <typename E, int D, bool CAUSAL, bool ROPE, int DP = D>
+template <typename E, int D, bool CAUSAL, bool ROPE, int DP = D, bool RAG = false>
 __device__ __forceinline__ void run_item(const AttnArgs& a, const BwdItem it) {
   using C = BwdCfg<D>;
   __shared__ __attribute__((aligned(16))) uint16_t A0[C::ELEMS];
@@ -871,25 +890,26 @@ __device__ __forceinline__ void run_item(const AttnArgs& a, const BwdItem it) {
   __shared__ __attribute__((aligned(16))) float SB[2 * C::TILE];
   const BwdBuf bufs[2] = {{A0, A1, SA}, {B0, B1, SB}};
   if (it.kind)
-    dq_item<E, D, CAUSAL, ROPE, DP>(a, it, bufs);
+    dq_item<E, D, CAUSAL, ROPE, DP, RAG>(a, it, bufs);
   else
-    dkdv_item<E, D, CAUSAL, ROPE, DP>(a, it, bufs);
+    dkdv_item<E, D, CAUSAL, ROPE, DP, RAG>(a, it, bufs);
 }
 
 // ROPE (every kernel below): the kernel carries the rotating stores, and dQ
 // and dK leave inverse-rotated by the tables in a.rope when a.rope.cos is set;
 // without it the kernel has no rotation code.
-template <typename E, int D, bool CAUSAL, bool ROPE>
+template <typename E, int D, bool CAUSAL, bool ROPE, bool RAG = false>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dkdv_kernel(AttnArgs a) {
   // key tile 0 sees the most query tiles: dispatched first
   const int BH = a.B * a.H;
-  run_item<E, D, CAUSAL, ROPE>(a, BwdItem{0, (int)(blockIdx.x / BH), (int)(blockIdx.x % BH)});
+  run_item<E, D, CAUSAL, ROPE, D, RAG>(a, BwdItem{0, (int)(blockIdx.x / BH),
+                                                  (int)(blockIdx.x % BH)});
 }
 
-template <typename E, int D, bool CAUSAL, bool ROPE>
+template <typename E, int D, bool CAUSAL, bool ROPE, bool RAG = false>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a, int n_qtiles) {
   const int BH = a.B * a.H;
-  run_item<E, D, CAUSAL, ROPE>(
+  run_item<E, D, CAUSAL, ROPE, D, RAG>(
       a, BwdItem{1, n_qtiles - 1 - (int)(blockIdx.x / BH), (int)(blockIdx.x % BH)});
 }
 
@@ -905,41 +925,45 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(AttnArgs a, int n_q
 // layout: the padding chunks of the staged tiles and resident rows load as
 // zeros, the products over the head dim stop at DP, accumulator blocks past
 // DP are not formed and only DP columns are stored (no rotating stores).
-template <typename E, int D, bool CAUSAL, bool ROPE, int DP = D>
+// RAG: S not a multiple of 64 (rows past S load as zeros and are not
+// stored; padded query rows add exact zeros to dK and dV, padded key rows
+// exact zeros to dQ, the non-causal last tile's padded keys take P = 0).
+template <typename E, int D, bool CAUSAL, bool ROPE, int DP = D, bool RAG = false>
 __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(AttnArgs a, int n_tiles,
                                                           int only_kind) {
   static_assert(DP == D || (D == 64 && !ROPE && (DP == 16 || DP == 32)), "head dim");
+  static_assert(!RAG || DP == D, "sequence tails at head dims 64 and 128");
   const int BH = a.B * a.H;
   const int rank = blockIdx.x / BH;
   const int kind = only_kind < 0 ? rank & 1 : only_kind;
   const int r = only_kind < 0 ? rank >> 1 : rank;
-  run_item<E, D, CAUSAL, ROPE, DP>(
+  run_item<E, D, CAUSAL, ROPE, DP, RAG>(
       a, BwdItem{kind, kind ? n_tiles - 1 - r : r, (int)(blockIdx.x % BH)});
 }
 
-template <typename E, int D, bool ROPE>
+template <typename E, int D, bool ROPE, bool RAG = false>
 hipError_t launch_dkdv_dr(const AttnArgs& a, hipStream_t st) {
   const int BH = a.B * a.H;
   const int nkt = (a.S + BwdCfg<D>::OWN - 1) / BwdCfg<D>::OWN;
   if (a.causal)
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, true, ROPE>), dim3(nkt * BH), dim3(256), 0, st,
-                       a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, true, ROPE, RAG>), dim3(nkt * BH), dim3(256),
+                       0, st, a);
   else
-    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, false, ROPE>), dim3(nkt * BH), dim3(256), 0,
-                       st, a);
+    hipLaunchKernelGGL((attn_bwd_dkdv_kernel<E, D, false, ROPE, RAG>), dim3(nkt * BH), dim3(256),
+                       0, st, a);
   return hipGetLastError();
 }
 
-template <typename E, int D, bool ROPE>
+template <typename E, int D, bool ROPE, bool RAG = false>
 hipError_t launch_dq_dr(const AttnArgs& a, hipStream_t st) {
   const int BH = a.B * a.H;
   const int nqt = (a.S + BwdCfg<D>::OWN - 1) / BwdCfg<D>::OWN;
   if (a.causal)
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<E, D, true, ROPE>), dim3(nqt * BH), dim3(256), 0, st,
-                       a, nqt);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<E, D, true, ROPE, RAG>), dim3(nqt * BH), dim3(256), 0,
+                       st, a, nqt);
   else
-    hipLaunchKernelGGL((attn_bwd_dq_kernel<E, D, false, ROPE>), dim3(nqt * BH), dim3(256), 0, st,
-                       a, nqt);
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<E, D, false, ROPE, RAG>), dim3(nqt * BH), dim3(256),
+                       0, st, a, nqt);
   return hipGetLastError();
 }
 
@@ -948,19 +972,19 @@ hipError_t launch_dq_dr(const AttnArgs& a, hipStream_t st) {
 // only_kind: -1 both kinds interleaved, else that kind alone.
 // Head dims 16 and 32 (DP < D) have no rotating stores: the host runs their
 // inverse RoPE as a separate pass.
-template <typename E, int D, bool CAUSAL, int DP = D>
+template <typename E, int D, bool CAUSAL, int DP = D, bool RAG = false>
 hipError_t launch_both_dc(const AttnArgs& a, int only_kind, hipStream_t st) {
   const int BH = a.B * a.H;
   const int n = (a.S + BwdCfg<D>::OWN - 1) / BwdCfg<D>::OWN;
-  hipLaunchKernelGGL((attn_bwd_kernel<E, D, CAUSAL, DP == D, DP>),
+  hipLaunchKernelGGL((attn_bwd_kernel<E, D, CAUSAL, DP == D, DP, RAG>),
                      dim3((only_kind < 0 ? 2 : 1) * n * BH), dim3(256), 0, st, a, n, only_kind);
   return hipGetLastError();
 }
 
-template <typename E, int D, int DP = D>
+template <typename E, int D, int DP = D, bool RAG = false>
 hipError_t launch_both_d(const AttnArgs& a, hipStream_t st, int only_kind = -1) {
-  return a.causal ? launch_both_dc<E, D, true, DP>(a, only_kind, st)
-                  : launch_both_dc<E, D, false, DP>(a, only_kind, st);
+  return a.causal ? launch_both_dc<E, D, true, DP, RAG>(a, only_kind, st)
+                  : launch_both_dc<E, D, false, DP, RAG>(a, only_kind, st);
 }
 
 // Head dims 16 and 32: the combined D = 64 kernel with DP columns, restricted
@@ -974,38 +998,42 @@ hipError_t launch_small_d(const AttnArgs& a, hipStream_t st, int only_kind) {
 // The separate launches: at D = 64 the combined kernel restricted to one kind
 // (it rotates only when a.rope.cos is set, which these entry points leave
 // unset); at D = 128 the kernels of one kind, rotating when a.rope.cos is set.
-template <typename E, int D>
+template <typename E, int D, bool RAG = false>
 hipError_t launch_dkdv_d(const AttnArgs& a, hipStream_t st) {
   if constexpr (D == 64) {
-    return launch_both_d<E, D>(a, st, 0);
+    return launch_both_d<E, D, D, RAG>(a, st, 0);
   } else {
-    if (a.rope.cos) return launch_dkdv_dr<E, D, true>(a, st);
-    return launch_dkdv_dr<E, D, false>(a, st);
+    if (a.rope.cos) return launch_dkdv_dr<E, D, true, RAG>(a, st);
+    return launch_dkdv_dr<E, D, false, RAG>(a, st);
   }
 }
 
-template <typename E, int D>
+template <typename E, int D, bool RAG = false>
 hipError_t launch_dq_d(const AttnArgs& a, hipStream_t st) {
   if constexpr (D == 64) {
-    return launch_both_d<E, D>(a, st, 1);
+    return launch_both_d<E, D, D, RAG>(a, st, 1);
   } else {
-    if (a.rope.cos) return launch_dq_dr<E, D, true>(a, st);
-    return launch_dq_dr<E, D, false>(a, st);
+    if (a.rope.cos) return launch_dq_dr<E, D, true, RAG>(a, st);
+    return launch_dq_dr<E, D, false, RAG>(a, st);
   }
 }
 
+// Sequence lengths that are not a multiple of 64 (head dims 64 and 128) run
+// the RAG instantiations.
 template <typename E>
 hipError_t launch_dkdv_e(const AttnArgs& a, hipStream_t st) {
   if (a.D < 64) return launch_small_d<E>(a, st, 0);
-  if (a.D == 64) return launch_dkdv_d<E, 64>(a, st);
-  return launch_dkdv_d<E, 128>(a, st);
+  const bool rag = a.S % 64 != 0;
+  if (a.D == 64) return rag ? launch_dkdv_d<E, 64, true>(a, st) : launch_dkdv_d<E, 64>(a, st);
+  return rag ? launch_dkdv_d<E, 128, true>(a, st) : launch_dkdv_d<E, 128>(a, st);
 }
 
 template <typename E>
 hipError_t launch_dq_e(const AttnArgs& a, hipStream_t st) {
   if (a.D < 64) return launch_small_d<E>(a, st, 1);
-  if (a.D == 64) return launch_dq_d<E, 64>(a, st);
-  return launch_dq_d<E, 128>(a, st);
+  const bool rag = a.S % 64 != 0;
+  if (a.D == 64) return rag ? launch_dq_d<E, 64, true>(a, st) : launch_dq_d<E, 64>(a, st);
+  return rag ? launch_dq_d<E, 128, true>(a, st) : launch_dq_d<E, 128>(a, st);
 }
 
 // D = 128: two launches.  Both kinds sit at the 256-register limit of two waves
@@ -1014,10 +1042,12 @@ hipError_t launch_dq_e(const AttnArgs& a, hipStream_t st) {
 template <typename E>
 hipError_t launch_both_e(const AttnArgs& a, hipStream_t st) {
   if (a.D < 64) return launch_small_d<E>(a, st, -1);
-  if (a.D == 64) return launch_both_d<E, 64>(a, st);
-  hipError_t e = launch_dkdv_d<E, 128>(a, st);
+  const bool rag = a.S % 64 != 0;
+  if (a.D == 64)
+    return rag ? launch_both_d<E, 64, 64, true>(a, st) : launch_both_d<E, 64>(a, st);
+  hipError_t e = rag ? launch_dkdv_d<E, 128, true>(a, st) : launch_dkdv_d<E, 128>(a, st);
   if (e != hipSuccess) return e;
-  return launch_dq_d<E, 128>(a, st);
+  return rag ? launch_dq_d<E, 128, true>(a, st) : launch_dq_d<E, 128>(a, st);
 }
 
 template <int DT>

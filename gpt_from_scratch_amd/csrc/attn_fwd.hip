@@ -107,10 +107,15 @@ __device__ __forceinline__ constexpr float kProbLimit() {
 // layout: the padding chunks of the staged tiles load as zeros, the K Q^T
 // products stop at DP, O^T blocks past DP are not accumulated and only DP
 // columns are stored.
-template <typename E, int D, bool CAUSAL, int DP = D>
+// RAG: S not a multiple of 64.  Rows at or past S load as zeros (the Q row
+// loads are guarded, the tile descriptors end at row S), keys at or past S
+// are masked in the last key tile, which takes the masked step, and rows at
+// or past S are not stored.
+template <typename E, int D, bool CAUSAL, int DP = D, bool RAG = false>
 __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_kernel(AttnArgs a, int n_qtiles, int n_cu) {
   using C = FwdCfg<D>;
   static_assert(DP == D || (D == 64 && (DP == 16 || DP == 32)), "head dim");
+  static_assert(!RAG || DP == D, "sequence tails at head dims 64 and 128");
   constexpr int KSP = DP / 16;         // k-steps of K Q^T over the valid columns
   constexpr int DBP = (DP + 31) / 32;  // O^T blocks holding valid columns
   // One array per buffer, so that the compiler can see that a direct load
@@ -148,19 +153,20 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
 
   const int q0 = qt * C::BQ;
   const int qw = q0 + 32 * wave;       // first query row of this wave (SGPR)
-  const bool wave_valid = qw < S;      // S % 64 == 0: 32-row blocks are all-or-nothing
+  const bool wave_valid = qw < S;      // without RAG, 32-row blocks are all-or-nothing
   const int qrow = qw + l32;
 
   u32x4 qf[C::KS];
 #pragma unroll
   for (int ks = 0; ks < C::KS; ++ks)
-    qf[ks] = (wave_valid && ks < KSP)
+    qf[ks] = (wave_valid && ks < KSP && (!RAG || qrow < S))
                  ? *(const u32x4*)(qp + (int64_t)qrow * a.q.ss + 16 * ks + 8 * g)
                  : u32x4{0, 0, 0, 0};
 
   const int kv_end = CAUSAL ? min(q0 + C::BQ, S) : S;
-  const int nkv = kv_end / C::BKV;
-  const int jdiag = CAUSAL ? q0 / C::BKV : nkv;   // first tile that may need a mask
+  const int nkv = RAG ? (kv_end + C::BKV - 1) / C::BKV : kv_end / C::BKV;
+  // first tile that may need a mask (RAG: the last one holds keys past S)
+  const int jdiag = CAUSAL ? q0 / C::BKV : (RAG ? nkv - 1 : nkv);
 
   // ---- staging: direct global -> LDS loads ----
   // A tile is 1 KB slices; wave w fills slices w, w + 4, ...
@@ -180,7 +186,8 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
   }
   auto dma = [&](const uint16_t* base, int64_t ss, const uint32_t(&off)[C::SPW], int t,
                  uint16_t* tile) __attribute__((always_inline)) {
-    const auto rs = tile_rsrc(base + (int64_t)t * C::BKV * ss, rows_extent(C::BKV, ss, DP));
+    const int rows = RAG ? min(C::BKV, S - t * C::BKV) : C::BKV;
+    const auto rs = tile_rsrc(base + (int64_t)t * C::BKV * ss, rows_extent(rows, ss, DP));
 #pragma unroll
     for (int m = 0; m < C::SPW; ++m)
       buffer_load_lds16(rs, off[m], tile + (wave + 4 * m) * 512);
@@ -228,6 +235,15 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
 #pragma unroll
       for (int r = 0; r < 16; ++r)
         if (32 * kb + 8 * (r >> 2) + (r & 3) > rel) s[kb][r] = -INFINITY;
+  };
+  // RAG: keys at or past S of the tile starting at kv0 masked.
+  auto mask_tail = [&](f32x16(&s)[2], int kv0) __attribute__((always_inline)) {
+    const int lim = S - kv0 - 4 * g;  // visible iff (kv - kv0 - 4g) < lim
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (32 * kb + 8 * (r >> 2) + (r & 3) >= lim) s[kb][r] = -INFINITY;
   };
   // Probabilities against the reference mref, in place, packed into pb; returns
   // their sum.  D = 64 sums the packed (rounded) values, the ones P V
@@ -303,9 +319,11 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
     const int kv0 = j * C::BKV;
     if (wave_valid && (!MASKED || !CAUSAL || kv0 <= qw + 31)) {
       const bool msk = MASKED && CAUSAL && kv0 + C::BKV - 1 > qw;
+      const bool tmsk = RAG && MASKED && kv0 + C::BKV > S;
       f32x16 s[2];
       qk(kt, s);
       if (msk) mask(s, kv0);
+      if (tmsk) mask_tail(s, kv0);
       u32x4 pb[2][2];
       // D = 64: probabilities against the running reference m_run without
       // this tile's max, exact as long as their sum stays within kProbLimit
@@ -321,6 +339,7 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
           exact = true;
           qk(kt, s);
           if (msk) mask(s, kv0);
+          if (tmsk) mask_tail(s, kv0);
         }
       }
       if (exact) {
@@ -352,8 +371,9 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
   // Every buffer is idle after the last step's barrier: wave w stages its O
   // rows through buffer w.
   uint16_t* stage = wave == 0 ? K0 : wave == 1 ? K1 : wave == 2 ? V0 : V1;
-  store_block_rows<E, D, DP>(acc, 1.f / l_tot, stage, op + (int64_t)qw * a.o.ss, a.o.ss);
-  if (g == 0) a.lse[(int64_t)bh * S + qrow] = (m_run + fast_log2(l_tot)) * kLn2;
+  store_block_rows<E, D, DP>(acc, 1.f / l_tot, stage, op + (int64_t)qw * a.o.ss, a.o.ss,
+                             RAG ? min(32, S - qw) : 32);
+  if (g == 0 && (!RAG || qrow < S)) a.lse[(int64_t)bh * S + qrow] = (m_run + fast_log2(l_tot)) * kLn2;
 }
 
 // Compute units of the device `st` launches on (cached per device), the size
@@ -376,18 +396,18 @@ int cu_count(hipStream_t st) {
   return n > 0 ? n : 0;
 }
 
-template <typename E, int D, int DP = D>
+template <typename E, int D, int DP = D, bool RAG = false>
 hipError_t launch_fwd_d(const AttnArgs& a, hipStream_t st) {
   const int n_qtiles = (a.S + FwdCfg<D>::BQ - 1) / FwdCfg<D>::BQ;
   int n_cu = cu_count(st);
   if (n_cu == 0) n_cu = 1 << 30;  // one round: no reversal
   dim3 grid(n_qtiles * a.B * a.H), block(FwdCfg<D>::NT);
   if (a.causal)
-    hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, true, DP>), grid, block, 0, st, a, n_qtiles,
-                       n_cu);
+    hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, true, DP, RAG>), grid, block, 0, st, a,
+                       n_qtiles, n_cu);
   else
-    hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, false, DP>), grid, block, 0, st, a, n_qtiles,
-                       n_cu);
+    hipLaunchKernelGGL((attn_fwd_mfma_kernel<E, D, false, DP, RAG>), grid, block, 0, st, a,
+                       n_qtiles, n_cu);
   return hipGetLastError();
 }
 
@@ -395,6 +415,10 @@ template <typename E>
 hipError_t launch_fwd_e(const AttnArgs& a, hipStream_t st) {
   if (a.D == 16) return launch_fwd_d<E, 64, 16>(a, st);
   if (a.D == 32) return launch_fwd_d<E, 64, 32>(a, st);
+  if (a.S % 64) {
+    if (a.D == 64) return launch_fwd_d<E, 64, 64, true>(a, st);
+    return launch_fwd_d<E, 128, 128, true>(a, st);
+  }
   if (a.D == 64) return launch_fwd_d<E, 64>(a, st);
   return launch_fwd_d<E, 128>(a, st);
 }
@@ -402,8 +426,9 @@ hipError_t launch_fwd_e(const AttnArgs& a, hipStream_t st) {
 }  // namespace
 
 bool mfma_supports(int dtype, int D, int S) {
-  return (dtype == 1 || dtype == 2) && (D == 16 || D == 32 || D == 64 || D == 128) && S > 0 &&
-         S % 64 == 0;
+  // any S at head dims 64 and 128; multiples of 64 at 16 and 32
+  return (dtype == 1 || dtype == 2) && S > 0 &&
+         (D == 64 || D == 128 || ((D == 16 || D == 32) && S % 64 == 0));
 }
 
 hipError_t launch_attn_fwd_mfma(int dtype, const AttnArgs& a, hipStream_t st) {

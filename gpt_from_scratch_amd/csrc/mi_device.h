@@ -179,9 +179,10 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* p, uint3
                                            0x00020000);
 }
 
-// Bytes spanned by `rows` rows of `cols` 16-bit elements, `ss` elements apart.
+// Bytes spanned by `rows` rows of `cols` 16-bit elements, `ss` elements apart
+// (0 for no rows).
 __device__ __forceinline__ uint32_t rows_extent(int rows, int64_t ss, int cols) {
-  return (uint32_t)(((int64_t)(rows - 1) * ss + cols) * 2);
+  return rows <= 0 ? 0u : (uint32_t)(((int64_t)(rows - 1) * ss + cols) * 2);
 }
 
 // A byte offset past every extent above: the host admits a tensor to the
@@ -284,10 +285,12 @@ __device__ __forceinline__ u32x4 tr_operand(const uint16_t* p, int ld) {
 // `grow` points at row 0 of the block, `ss` is the row stride in elements.
 // Row r of the staging keeps 16-byte chunk c at position c ^ (r & 7).
 // DP < D (head dims 16 and 32 run in the D = 64 layout): only the first DP
-// columns are stored; the accumulators of the others are never read.
+// columns are stored; the accumulators of the others are never read.  Only
+// rows below nrows are stored (sequence tails).
 template <typename E, int D, int DP = D>
 __device__ __forceinline__ void store_block_rows(const f32x16 (&acc)[D / 32], float sc,
-                                                 uint16_t* lds, uint16_t* grow, int64_t ss) {
+                                                 uint16_t* lds, uint16_t* grow, int64_t ss,
+                                                 int nrows = 32) {
   static_assert(DP % 16 == 0 && DP <= D, "stored columns");
   constexpr int CPR = D / 8;     // 16-byte chunks per row
   constexpr int RPI = 64 / CPR;  // rows per store instruction
@@ -309,7 +312,7 @@ __device__ __forceinline__ void store_block_rows(const f32x16 (&acc)[D / 32], fl
   for (int p = 0; p < 32 / RPI; ++p) {
     const int r = p * RPI + lane / CPR;
     const int c = lane % CPR;
-    if (DP < D && c >= DP / 8) continue;
+    if ((DP < D && c >= DP / 8) || r >= nrows) continue;
     const u32x4 v = *(const u32x4*)(lds + r * D + ((c ^ (r & 7)) << 3));
     *(u32x4*)(grow + (int64_t)r * ss + 8 * c) = v;
   }

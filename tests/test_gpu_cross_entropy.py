@@ -99,7 +99,7 @@ def test_reference_call_site_and_torch_fp32(gpu):
     zf = z.detach().float().requires_grad_(True)
     ref = torch.nn.functional.cross_entropy(zf.view(-1, V), t.view(-1), reduction="none")
     ref.mean().backward()
-    err = (loss.float().view(-1) - ref.detach()).abs()
+    err = (loss.detach().float().view(-1) - ref.detach()).abs()
     assert float((err / ref.detach().abs()).max()) <= 2.0 ** -8 + 1e-5
     # gradient of the mean: the upstream 1/(S*B) is itself a bf16 value here
     gs = float(torch.tensor(1.0 / (S * B), dtype=torch.bfloat16)) * (S * B)

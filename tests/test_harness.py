@@ -91,6 +91,6 @@ def test_tiny_model_trains_on_cpu_with_eager_attention():
         loss = SoftmaxCrossEntropy.apply(model(inputs), labels).mean()
         loss.backward()
         opt.step()
-        losses.append(float(loss))
+        losses.append(float(loss.detach()))
     assert abs(losses[0] - math.log(97)) < 0.5
     assert losses[-1] < losses[0]
