@@ -932,7 +932,6 @@ template <typename E, int D, bool CAUSAL, bool ROPE, int DP = D, bool RAG = fals
 __global__ __launch_bounds__(256, 2) void attn_bwd_kernel(AttnArgs a, int n_tiles,
                                                           int only_kind) {
   static_assert(DP == D || (D == 64 && !ROPE && (DP == 16 || DP == 32)), "head dim");
-  static_assert(!RAG || DP == D, "sequence tails at head dims 64 and 128");
   const int BH = a.B * a.H;
   const int rank = blockIdx.x / BH;
   const int kind = only_kind < 0 ? rank & 1 : only_kind;
@@ -991,6 +990,10 @@ hipError_t launch_both_d(const AttnArgs& a, hipStream_t st, int only_kind = -1) 
 // to one kind (0 or 1) or both (-1).
 template <typename E>
 hipError_t launch_small_d(const AttnArgs& a, hipStream_t st, int only_kind) {
+  if (a.S % 64) {
+    if (a.D == 16) return launch_both_d<E, 64, 16, true>(a, st, only_kind);
+    return launch_both_d<E, 64, 32, true>(a, st, only_kind);
+  }
   if (a.D == 16) return launch_both_d<E, 64, 16>(a, st, only_kind);
   return launch_both_d<E, 64, 32>(a, st, only_kind);
 }

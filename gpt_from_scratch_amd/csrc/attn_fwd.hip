@@ -115,7 +115,6 @@ template <typename E, int D, bool CAUSAL, int DP = D, bool RAG = false>
 __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_kernel(AttnArgs a, int n_qtiles, int n_cu) {
   using C = FwdCfg<D>;
   static_assert(DP == D || (D == 64 && (DP == 16 || DP == 32)), "head dim");
-  static_assert(!RAG || DP == D, "sequence tails at head dims 64 and 128");
   constexpr int KSP = DP / 16;         // k-steps of K Q^T over the valid columns
   constexpr int DBP = (DP + 31) / 32;  // O^T blocks holding valid columns
   // One array per buffer, so that the compiler can see that a direct load
@@ -413,12 +412,14 @@ hipError_t launch_fwd_d(const AttnArgs& a, hipStream_t st) {
 
 template <typename E>
 hipError_t launch_fwd_e(const AttnArgs& a, hipStream_t st) {
-  if (a.D == 16) return launch_fwd_d<E, 64, 16>(a, st);
-  if (a.D == 32) return launch_fwd_d<E, 64, 32>(a, st);
   if (a.S % 64) {
+    if (a.D == 16) return launch_fwd_d<E, 64, 16, true>(a, st);
+    if (a.D == 32) return launch_fwd_d<E, 64, 32, true>(a, st);
     if (a.D == 64) return launch_fwd_d<E, 64, 64, true>(a, st);
     return launch_fwd_d<E, 128, 128, true>(a, st);
   }
+  if (a.D == 16) return launch_fwd_d<E, 64, 16>(a, st);
+  if (a.D == 32) return launch_fwd_d<E, 64, 32>(a, st);
   if (a.D == 64) return launch_fwd_d<E, 64>(a, st);
   return launch_fwd_d<E, 128>(a, st);
 }
@@ -426,9 +427,7 @@ hipError_t launch_fwd_e(const AttnArgs& a, hipStream_t st) {
 }  // namespace
 
 bool mfma_supports(int dtype, int D, int S) {
-  // any S at head dims 64 and 128; multiples of 64 at 16 and 32
-  return (dtype == 1 || dtype == 2) && S > 0 &&
-         (D == 64 || D == 128 || ((D == 16 || D == 32) && S % 64 == 0));
+  return (dtype == 1 || dtype == 2) && S > 0 && (D == 16 || D == 32 || D == 64 || D == 128);
 }
 
 hipError_t launch_attn_fwd_mfma(int dtype, const AttnArgs& a, hipStream_t st) {

@@ -20,11 +20,10 @@
  *   - rope tensors are logically [S, B, H, D] (the layout the model hands to
  *     RoPE); the cos/sin tables are [S, D/2] with two element strides.
  *   - dtypes: MI_F32, MI_F16, MI_BF16.  Attention runs on bf16/f16 MFMA when
- *     every row is 16-byte aligned and D is 64 or 128 (any S; rows past S
- *     are neither read nor written) or 16 or 32 with S % 64 == 0 (in the
- *     D = 64 kernels' layout, the padding staged as zeros); every other
- *     supported case runs on an exact-fp32 VALU kernel.  Arithmetic is fp32
- *     in all kernels.
+ *     every row is 16-byte aligned, for D = 16, 32, 64 or 128 and any S (16
+ *     and 32 in the D = 64 kernels' layout, the padding staged as zeros; no
+ *     row at or past S is read or written); every other supported case runs
+ *     on an exact-fp32 VALU kernel.  Arithmetic is fp32 in all kernels.
  *
  * Errors: a non-zero mi_status; mi_last_error() gives a message for the
  * calling thread.  Arguments are validated before anything is launched.

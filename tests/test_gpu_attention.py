@@ -227,17 +227,19 @@ def _ragged_check(gpu, B, H, S, D, seed, causal=True, dtype=torch.bfloat16):
 
 
 @pytest.mark.parametrize("S,D", [(100, 64), (37, 128), (1, 64), (130, 32), (65, 64),
-                                 (1000, 64), (127, 128), (200, 128)])
+                                 (1000, 64), (127, 128), (200, 128), (77, 16), (1, 32)])
 def test_ragged_sequence_lengths(gpu, S, D):
     """Lengths the 64-row tiles do not divide: the matrix-core kernels with
-    masked tails at D = 64 and 128, the exact-fp32 kernels at D = 32."""
+    masked tails (head dims 16 and 32 in the D = 64 layout)."""
     _ragged_check(gpu, 2, 2, S, D, seed=7 + S)
 
 
 @pytest.mark.parametrize("S,D,causal,dtype", [(100, 64, False, torch.bfloat16),
                                               (300, 128, False, torch.bfloat16),
                                               (77, 64, True, torch.float16),
-                                              (190, 128, False, torch.float16)])
+                                              (190, 128, False, torch.float16),
+                                              (150, 32, False, torch.bfloat16),
+                                              (99, 16, True, torch.float16)])
 def test_ragged_noncausal_and_fp16(gpu, S, D, causal, dtype):
     """Sequence tails without the causal mask (the forward masks the last key
     tile's keys past S, the dQ items give them P = 0) and in fp16."""
@@ -245,7 +247,7 @@ def test_ragged_noncausal_and_fp16(gpu, S, D, causal, dtype):
 
 
 @pytest.mark.parametrize("S,D,causal", [(100, 64, True), (77, 64, False), (150, 128, True),
-                                        (97, 128, False)])
+                                        (97, 128, False), (90, 32, True), (70, 16, False)])
 def test_ragged_reads_and_writes_only_rows_below_S(gpu, S, D, causal):
     """Q, K, V, dO, O and the gradients are the first S rows of 64 * ceil(S/64) + 8
     rows per head whose other rows hold NaN: a row at or past S fetched instead of
@@ -541,7 +543,8 @@ def test_backward_deterministic_writes_every_output_keeps_inputs(gpu, B, H, S, D
 
 @pytest.mark.parametrize("causal", [1, 0])
 @pytest.mark.parametrize("B,H,S,D", [(2, 3, 576, 64), (1, 2, 512, 128), (2, 3, 576, 32),
-                                     (1, 2, 512, 16), (2, 3, 200, 64), (1, 2, 150, 128)])
+                                     (1, 2, 512, 16), (2, 3, 200, 64), (1, 2, 150, 128),
+                                     (2, 2, 100, 32)])
 def test_separate_dkdv_dq_equal_combined(gpu, B, H, S, D, causal):
     """mi_attn_bwd_dkdv then mi_attn_bwd_dq (the reference's `_attn_bwd_LoopQ`
     and `_attn_bwd_LoopKV` launches, core/myFlashAttn.py:349-439) on NaN-filled

@@ -4,8 +4,9 @@ The attention kernels (matrix-core and exact-fp32), RoPE and the model
 operators must not use scratch memory (register spills or run-time-indexed
 private arrays), and the hot attention kernels must keep the occupancy their
 tiling assumes.  The documented exceptions are the causal D = 128 dK/dV launch
-with the rotating stores (one spilled register) and the causal D = 64 backward
-for sequence lengths that are not a multiple of 64 (44 bytes per lane).  At
+with the rotating stores (one spilled register) and the causal combined
+backward for sequence lengths that are not a multiple of 64 (36-44 bytes per
+lane of spilled scalar registers).  At
 D = 64 every backward launch, the separate dK/dV and dQ ones included, runs the
 combined kernel, which has no scratch."""
 import os
@@ -21,10 +22,12 @@ CSRC = os.path.join(ROOT, "gpt_from_scratch_amd", "csrc")
 HIPCC = "/opt/rocm/bin/hipcc"
 SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "attn_valu.hip", "rope.hip", "model_ops.hip")
 # the causal D = 128 dK/dV launch with the rotating stores (mi_attn_bwd_rope):
-# 8 bytes per lane, one register reloaded once per step; the causal D = 64
-# backward for sequence lengths that are not a multiple of 64 (44 bytes)
+# 8 bytes per lane, one register reloaded once per step; the causal combined
+# backward (head dims 16-64) for sequence lengths that are not a multiple of
+# 64 (36-44 bytes: scalar registers spilled)
 ALLOWED_SCRATCH = re.compile(r"attn_bwd_dkdv_kernel<mi::(BF16|F16), 128, true, true(, false)?>"
-                             r"|attn_bwd_kernel<mi::(BF16|F16), 64, true, true, 64, true>")
+                             r"|attn_bwd_kernel<mi::(BF16|F16), 64, true, (true|false), "
+                             r"(16|32|64), true>")
 
 
 def _hipflags():
