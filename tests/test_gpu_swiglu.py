@@ -99,7 +99,7 @@ def test_reference_ops_at_config5_shape(gpu):
     gate, up = x.chunk(2, dim=-1)
     ref = torch.nn.functional.silu(gate) * up
     ref.backward(dh)
-    for got, want in ((h, ref.detach()), (dgu, x.grad)):
+    for got, want in ((h.detach(), ref.detach()), (dgu, x.grad)):
         eq = float((got == want).float().mean())
         assert eq >= 0.99, eq
         rel = ((got.float() - want.float()).abs() / want.float().abs().clamp_min(1e-30))
