@@ -1,7 +1,8 @@
 """mi_attn_bwd_noalloc (workspace in the library's static device array) against
 mi_attn_bwd (caller's workspace): the same kernels, so dQ, dK and dV must
 be bit-identical.  Two calls in a row, the second with a smaller input (the
-array keeps the first call's workspace); D = 16, 32, 64 and 128, causal and not; the
+array keeps the first call's workspace); D = 16, 32, 64 and 128, causal and not,
+sequence lengths with and without a partial last tile; the
 size limit is refused before anything is enqueued."""
 import math
 
@@ -24,7 +25,8 @@ def test_noalloc_backward_matches_workspace_backward(gpu):
     from gpt_from_scratch_amd import _lib
     for B, H, S, D, causal in ((2, 6, 1024, 64, True), (1, 3, 256, 128, False),
                                (1, 2, 192, 64, True), (1, 4, 320, 32, True),
-                               (2, 2, 128, 16, False)):
+                               (2, 2, 128, 16, False), (1, 3, 100, 64, True),
+                               (1, 2, 77, 128, False)):
         q, k, v, o, do, lse = _inputs(gpu, B, H, S, D, 300 + S + D)
         scale = 1.0 / math.sqrt(D)
         want = [torch.empty_like(q) for _ in range(3)]
