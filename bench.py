@@ -58,7 +58,7 @@ def parse_args():
     ap.add_argument("--no-gpt", action="store_true",
                     help="skip the config-5 GPT train-step measurement")
     ap.add_argument("--no-d128", action="store_true",
-                    help="skip the measurements of configs 1, 3 and 4 (fp32 D = 64, bf16 D = 128)")
+                    help="skip the measurements beside the headline (configs 1, 3 and 4, head dim 32, S = 1000)")
     ap.add_argument("--no-model-ops", action="store_true",
                     help="skip the config-5 model-operator kernel measurements")
     ap.add_argument("--summarize", metavar="DIR",
@@ -878,6 +878,14 @@ def main():
         out["attn_c1_fp32"] = attn_config_bench(dev, lib, 1, 12, 256, 64, 1, 1.0, args.steps,
                                                 dtype=torch.float32)
         _progress("config 1 done")
+        # shapes outside the benchmark configs that the matrix-core kernels also cover:
+        # head dim 32 (the D = 64 layout, padded) at config 2's FLOPs, and a sequence
+        # length with a partial last tile
+        out["attn_other_shapes"] = {
+            "d32": attn_config_bench(dev, lib, 8, 24, 1024, 32, 5, 1.0, args.steps),
+            "s1000": attn_config_bench(dev, lib, 2, 12, 1000, 64, 6, 1.0, args.steps)}
+        torch.cuda.empty_cache()
+        _progress("head dim 32 and S = 1000 done")
         # configs 3 and 4 (D = 128): parity cases, measured beside the headline
         out["attn_d128"] = {
             "config3": attn_config_bench(dev, lib, 2, 16, 4096, 128, 3, 0.5, args.steps),

@@ -77,19 +77,21 @@ __device__ __forceinline__ float half_f32(uint32_t x) {
   else return (float)__builtin_bit_cast(_Float16, (uint16_t)x);
 }
 
-// The same for 16-bit O and dO with 16-byte aligned rows and D = 64 * NCH:
-// lane l of a group of eight loads bytes [16(l%8), 16(l%8)+16) of each
-// 128-byte chunk, so one wave instruction reads eight whole rows; every lane
-// takes R rows (32 apart) and issues all its loads before the first use.
-template <int DT, int NCH, int R>
+// The same for 16-bit O and dO with 16-byte aligned rows and D = 8 * LPR *
+// NCH: lane l of a group of LPR (8; 4 at D = 32, 2 at D = 16) loads bytes
+// [16(l%LPR), 16(l%LPR)+16) of each 16*LPR-byte chunk, so one wave
+// instruction reads 64/LPR whole rows; every lane takes R rows (256/LPR
+// apart) and issues all its loads before the first use.
+template <int DT, int NCH, int R, int LPR = 8>
 __global__ __launch_bounds__(256) void attn_delta_v16_kernel(AttnArgs a, FastDiv divS,
                                                              FastDiv divH, uint32_t nrows) {
-  const int sub = threadIdx.x & 7;
-  const uint32_t rbase = blockIdx.x * (32 * R) + (threadIdx.x >> 3);
+  constexpr int RPW = 256 / LPR;  // rows per workgroup and pass
+  const int sub = threadIdx.x & (LPR - 1);
+  const uint32_t rbase = blockIdx.x * (RPW * R) + (threadIdx.x / LPR);
   u32x4 ov[R][NCH], dv[R][NCH];
 #pragma unroll
   for (int r = 0; r < R; ++r) {
-    const uint32_t row = rbase + 32 * r;
+    const uint32_t row = rbase + RPW * r;
     if (row < nrows) {
       const uint32_t bh = fdiv(row, divS);
       const uint32_t s = row - bh * divS.d;
@@ -99,8 +101,8 @@ __global__ __launch_bounds__(256) void attn_delta_v16_kernel(AttnArgs a, FastDiv
       const uint16_t* d = (const uint16_t*)a.dout.ptr + b * a.dout.sb + h * a.dout.sh + s * a.dout.ss;
 #pragma unroll
       for (int k = 0; k < NCH; ++k) {
-        ov[r][k] = *(const u32x4*)(o + 64 * k + 8 * sub);
-        dv[r][k] = *(const u32x4*)(d + 64 * k + 8 * sub);
+        ov[r][k] = *(const u32x4*)(o + 8 * LPR * k + 8 * sub);
+        dv[r][k] = *(const u32x4*)(d + 8 * LPR * k + 8 * sub);
       }
     } else {
 #pragma unroll
@@ -118,10 +120,8 @@ __global__ __launch_bounds__(256) void attn_delta_v16_kernel(AttnArgs a, FastDiv
         acc += half_f32<DT>(x & 0xffffu) * half_f32<DT>(y & 0xffffu);
         acc += half_f32<DT>(x >> 16) * half_f32<DT>(y >> 16);
       }
-    acc += __shfl_xor(acc, 1, 64);
-    acc += __shfl_xor(acc, 2, 64);
-    acc += __shfl_xor(acc, 4, 64);
-    const uint32_t row = rbase + 32 * r;
+    acc = group_sum<LPR>(acc);  // the xor-1, xor-2, xor-4 tree, by DPP
+    const uint32_t row = rbase + RPW * r;
     if (row < nrows && sub == 0) {
       a.delta[row] = acc;
       a.delta[nrows + row] = a.lse[row] * kLog2e;
@@ -1072,6 +1072,19 @@ hipError_t launch_delta_t(const AttnArgs& a, hipStream_t st) {
         hipLaunchKernelGGL((attn_delta_v16_kernel<DT, 1, R>), g4, dim3(256), 0, st, a, dS, dH, nrows);
       else
         hipLaunchKernelGGL((attn_delta_v16_kernel<DT, 2, R>), g4, dim3(256), 0, st, a, dS, dH, nrows);
+      return hipGetLastError();
+    }
+    // D = 32 and 16: four and two lanes per row (64 and 128 rows per
+    // workgroup and pass)
+    if (a16(a.o) && a16(a.dout) && (a.D == 32 || a.D == 16)) {
+      if (a.D == 32)
+        hipLaunchKernelGGL((attn_delta_v16_kernel<DT, 1, R, 4>),
+                           dim3((nrows + 64 * R - 1) / (64 * R)), dim3(256), 0, st, a, dS, dH,
+                           nrows);
+      else
+        hipLaunchKernelGGL((attn_delta_v16_kernel<DT, 1, R, 2>),
+                           dim3((nrows + 128 * R - 1) / (128 * R)), dim3(256), 0, st, a, dS, dH,
+                           nrows);
       return hipGetLastError();
     }
   }
