@@ -170,7 +170,7 @@ mi::AttnArgs grad_args(int B, int H, int S, int D, int causal, float scale, cons
 
 extern "C" {
 
-int mi_version(void) { return (2 << 16) | 4; }
+int mi_version(void) { return (2 << 16) | 5; }
 
 const char* mi_status_str(mi_status s) {
   switch (s) {
