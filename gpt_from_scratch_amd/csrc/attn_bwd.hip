@@ -25,6 +25,10 @@
 //   * causal: key tiles only visit query tiles at or after the diagonal, query
 //     tiles only key tiles at or before it; 32-row blocks entirely above the
 //     diagonal are skipped per wave, blocks that straddle it are masked.
+//   * head dims 16 and 32 run the D = 64 kernels with DP valid columns, and
+//     sequence lengths that are not a multiple of 64 run the RAG
+//     instantiations (rows past S staged as zeros and not stored); both are
+//     template parameters, so the other instantiations are unaffected.
 #include <type_traits>
 
 #include "mi_device.h"

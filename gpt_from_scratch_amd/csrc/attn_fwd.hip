@@ -42,6 +42,10 @@
 //     head is B*H).  Workgroups w and w + #CU share a CU, so every odd round
 //     of #CU workgroups is taken in reverse (XCD kept): a CU's co-resident
 //     tiles pair heavy with light.
+//   * head dims 16 and 32 run the D = 64 kernel with DP valid columns, and
+//     sequence lengths that are not a multiple of 64 the RAG instantiation
+//     (rows past S staged as zeros, the last key tile's keys past S masked,
+//     rows past S not stored); both are template parameters.
 #include <atomic>
 #include <type_traits>
 
