@@ -30,16 +30,21 @@ ALLOWED_SCRATCH = re.compile(r"attn_bwd_dkdv_kernel<mi::(BF16|F16), 128, true, t
                              r"(16|32|64), true>")
 
 
-def _hipflags():
-    """HIPFLAGS of the library's Makefile, so the report is the shipped build's."""
+def _hipflags(src):
+    """HIPFLAGS of the library's Makefile, with the additions of src's object
+    target, so the report is the shipped build's."""
     text = open(os.path.join(CSRC, "Makefile")).read()
     m = re.search(r"^HIPFLAGS = (.*?)(?<!\\)\n", text, re.S | re.M)
     flags = m.group(1).replace("\\\n", " ").replace("$(ARCH)", "gfx950").split()
+    stem = src.rsplit(".", 1)[0]
+    for extra in re.findall(r"^\$\(BUILD\)/" + re.escape(stem) + r"\.o: HIPFLAGS \+= (.*)$",
+                            text, re.M):
+        flags += extra.split()
     return [f for f in flags if f != "-fPIC"]
 
 
 def _report(src, tmp):
-    cmd = [HIPCC] + _hipflags() + ["-I" + os.path.join(ROOT, "include"), "--cuda-device-only",
+    cmd = [HIPCC] + _hipflags(src) + ["-I" + os.path.join(ROOT, "include"), "--cuda-device-only",
                                    "-c", os.path.join(CSRC, src), "-o", os.path.join(tmp, src + ".o"),
                                    "-Rpass-analysis=kernel-resource-usage"]
     out = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
