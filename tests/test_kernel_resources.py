@@ -21,12 +21,9 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "gpt_from_scratch_amd", "csrc")
 HIPCC = "/opt/rocm/bin/hipcc"
 SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "attn_valu.hip", "rope.hip", "model_ops.hip")
-# the causal D = 128 dK/dV launch with the rotating stores (mi_attn_bwd_rope):
-# 8 bytes per lane, one register reloaded once per step; the causal combined
-# backward (head dims 16-64) for sequence lengths that are not a multiple of
-# 64 (36-44 bytes: scalar registers spilled)
-ALLOWED_SCRATCH = re.compile(r"attn_bwd_dkdv_kernel<mi::(BF16|F16), 128, true, true(, false)?>"
-                             r"|attn_bwd_kernel<mi::(BF16|F16), 64, true, (true|false), "
+# the causal combined backward (head dims 16-64) for sequence lengths that
+# are not a multiple of 64 (36 bytes per lane: scalar registers spilled)
+ALLOWED_SCRATCH = re.compile(r"attn_bwd_kernel<mi::(BF16|F16), 64, true, (true|false), "
                              r"(16|32|64), true>")
 
 
