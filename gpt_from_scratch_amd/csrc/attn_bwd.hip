@@ -186,29 +186,43 @@ __device__ __forceinline__ int bwd_swz(int r) {
   else return s;
 }
 
-// Per-lane LDS element offsets of the two tile reads: 16-byte row reads (row
+// Per-lane LDS byte offsets of the two tile reads: 16-byte row reads (row
 // l%32, chunk 2ks + l/32) and transposing reads (rows 4(l/32) + (l%16)/4 and,
 // for the operand's second half, those + 8; column 32db + 16((l/16)%2) +
 // 4(l%4)).  A 3-bit swz only changes the low three bits of a chunk index, so
-// chunk c + 8 sits 64 elements after chunk c, and swz repeats every 16 rows:
+// chunk c + 8 sits 128 bytes after chunk c, and swz repeats every 16 rows:
 // four row offsets and two (D = 128: the second half is 8 rows on, same
 // swizzle) or four transposing offsets, plus immediates, cover every read.
 // With SW16 bit 3 of the position is bit 3 of the chunk XOR bit 3 of the row:
 // eight row offsets; the transposing reads' first half (rows < 8) is as
-// without, the second half flips bit 3 (+64 elements for chunks < 8, -64 above).
+// without, the second half flips bit 3 (+128 bytes for chunks < 8, -128 above).
+// The offsets hold the lane part only: every read adds its tile buffer and
+// block as a constant, which the LDS instruction takes as its immediate
+// offset.  refresh() at the top of each step keeps the compiler from
+// hoisting "buffer + offset" sums out of the step loop, which would hold one
+// register per buffer, parity and offset (34 in the dK/dV loop, 24 in the dQ
+// loop) instead of one per offset.
 template <int D, bool SW16 = false>
 struct LdsOffsets {
   static constexpr bool R8 = D == 128 && SW16;
   int r4[R8 ? 8 : 4], t2[2], t2h[D == 64 || R8 ? 2 : 1];
   __device__ __forceinline__ int row(int ks) const {
     if constexpr (R8) return r4[ks];
-    else return r4[ks & 3] + 64 * (ks >> 2);
+    else return r4[ks & 3] + 128 * (ks >> 2);
   }
-  __device__ __forceinline__ int tr(int db) const { return t2[db & 1] + 64 * (db >> 1); }
+  __device__ __forceinline__ int tr(int db) const { return t2[db & 1] + 128 * (db >> 1); }
   __device__ __forceinline__ int tr_hi(int db) const {
-    if constexpr (D == 64) return t2h[db & 1] + 64 * (db >> 1);
-    else if constexpr (R8) return t2h[db & 1] + 64 * (1 - (db >> 1));
-    else return tr(db) + 8 * D;
+    if constexpr (D == 64) return t2h[db & 1] + 128 * (db >> 1);
+    else if constexpr (R8) return t2h[db & 1] + 128 * (1 - (db >> 1));
+    else return tr(db) + 16 * D;
+  }
+  __device__ __forceinline__ void refresh() {
+#pragma unroll
+    for (int i = 0; i < (R8 ? 8 : 4); ++i) opaque(r4[i]);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) opaque(t2[i]);
+#pragma unroll
+    for (int i = 0; i < (D == 64 || R8 ? 2 : 1); ++i) opaque(t2h[i]);
   }
 };
 
@@ -220,25 +234,31 @@ __device__ __forceinline__ LdsOffsets<D, SW16> lds_offsets(int lane) {
   if constexpr (LdsOffsets<D, SW16>::R8) {
 #pragma unroll
     for (int ks = 0; ks < 8; ++ks)
-      o.r4[ks] = l32 * D + (((2 * ks + g) ^ bwd_swz<D, SW16>(l32)) << 3);
+      o.r4[ks] = 2 * (l32 * D + (((2 * ks + g) ^ bwd_swz<D, SW16>(l32)) << 3));
   } else {
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks)
-      o.r4[ks] = l32 * D + (((2 * ks + g) ^ bwd_swz<D, SW16>(l32)) << 3);
+      o.r4[ks] = 2 * (l32 * D + (((2 * ks + g) ^ bwd_swz<D, SW16>(l32)) << 3));
   }
 #pragma unroll
   for (int db = 0; db < 2; ++db) {
     const int r = 4 * g + ((lane & 15) >> 2);
     const int ch = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-    o.t2[db] = r * D + ((ch ^ bwd_swz<D, SW16>(r)) << 3) + 4 * (lane & 1);
+    o.t2[db] = 2 * (r * D + ((ch ^ bwd_swz<D, SW16>(r)) << 3) + 4 * (lane & 1));
     if constexpr (D == 64)
-      o.t2h[db] = (r + 8) * D + ((ch ^ bwd_swz<D>(r + 8)) << 3) + 4 * (lane & 1);
+      o.t2h[db] = 2 * ((r + 8) * D + ((ch ^ bwd_swz<D>(r + 8)) << 3) + 4 * (lane & 1));
     else if constexpr (LdsOffsets<D, SW16>::R8)
       // rows r + 8 (< 16): low three bits as row r, bit 3 of the chunk
-      // flipped; the +64 / -64 of that flip is tr_hi's immediate
-      o.t2h[db] = (r + 8) * D + ((ch ^ (bwd_swz<D, SW16>(r + 8) & 7)) << 3) + 4 * (lane & 1);
+      // flipped; the +128 / -128 bytes of that flip is tr_hi's immediate
+      o.t2h[db] = 2 * ((r + 8) * D + ((ch ^ (bwd_swz<D, SW16>(r + 8) & 7)) << 3) + 4 * (lane & 1));
   }
   return o;
+}
+
+// The element of type T at `bytes` bytes past an LDS buffer.
+template <typename T>
+__device__ __forceinline__ const T* lds_at(const void* base, int bytes) {
+  return (const T*)((const char*)base + bytes);
 }
 
 // The transposed A operand from its two halves (rows k0..k0+7 and k0+8..+15).
@@ -541,9 +561,11 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[K_IN_LDS ? C::OWN * D : 8];
   uint16_t* const kw_lds = k_lds + (K_IN_LDS ? wave * 32 * D : 0);
 
-  // per-lane LDS offsets: 16-byte row reads (row l32, chunk 2ks + g) and
-  // transposing reads (row 4g + (lane%16)/4, column 32db + 16((lane/16)%2) + 4(lane%4))
-  const LdsOffsets<D> lo = lds_offsets<D>(lane);
+  // per-lane LDS byte offsets: 16-byte row reads (row l32, chunk 2ks + g) and
+  // transposing reads (row 4g + (lane%16)/4, column 32db + 16((lane/16)%2) + 4(lane%4)),
+  // and the lane's part of the lse / delta reads (query rows 4g + i of each group of 8)
+  LdsOffsets<D> lo = lds_offsets<D>(lane);
+  int slo = 16 * g;
 
   const int q_begin = first_row<D, CAUSAL>(it);
   const int nq = RAG ? (S - q_begin + C::TILE - 1) / C::TILE : (S - q_begin) / C::TILE;
@@ -594,6 +616,8 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
     if (!LAST && (D == 64 || j + 1 < nq))
       dma_stage<D, DP, RAG>(src, 0, q0 + C::TILE, bufs[P ^ 1], S);
 
+    lo.refresh();
+    opaque(slo);
     if (wave_valid && (!MASKED || q0 + C::TILE - 1 >= kw)) {
       const uint16_t* Qs = bufs[P].t0;
       const uint16_t* dOs = bufs[P].t1;
@@ -608,27 +632,27 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
         f32x16 s = f32x16{}, dp;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const f32x4 d4 = *(const f32x4*)(&sl[C::TILE + 32 * qb + 8 * jj + 4 * g]);
+          const f32x4 d4 = *lds_at<f32x4>(sl, slo + 4 * (C::TILE + 32 * qb + 8 * jj));
 #pragma unroll
           for (int i = 0; i < 4; ++i) dp[4 * jj + i] = d4[i];
         }
 #pragma unroll
         for (int ks = 0; ks < KSP; ++ks) {
-          const u32x4 qa = *(const u32x4*)(&Qs[32 * qb * D + lo.row(ks)]);
+          const u32x4 qa = *lds_at<u32x4>(Qs, 64 * qb * D + lo.row(ks));
           if constexpr (K_IN_LDS)
-            s = E::mfma(qa, *(const u32x4*)(&kw_lds[lo.row(ks)]), s);
+            s = E::mfma(qa, *lds_at<u32x4>(kw_lds, lo.row(ks)), s);
           else
             s = E::mfma(qa, kf[ks], s);
         }
 #pragma unroll
         for (int ks = 0; ks < KSP; ++ks) {
-          const u32x4 da = *(const u32x4*)(&dOs[32 * qb * D + lo.row(ks)]);
+          const u32x4 da = *lds_at<u32x4>(dOs, 64 * qb * D + lo.row(ks));
           dp = E::mfma(da, vn[ks], dp);
         }
         const bool diag = MASKED && qbs == kw;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
-          const f32x4 l4 = *(const f32x4*)(&sl[32 * qb + 8 * jj + 4 * g]);
+          const f32x4 l4 = *lds_at<f32x4>(sl, slo + 4 * (32 * qb + 8 * jj));
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 4 * jj + i;
@@ -655,10 +679,12 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
           for (int db = 0; db < DBP; ++db) {
-            const int off = (32 * qb + 16 * hh) * D;
-            dv[db] = E::mfma(tr_operand2(&dOs[off + lo.tr(db)], &dOs[off + lo.tr_hi(db)]),
+            const int off = 2 * (32 * qb + 16 * hh) * D;  // bytes
+            dv[db] = E::mfma(tr_operand2(lds_at<uint16_t>(dOs, off + lo.tr(db)),
+                                         lds_at<uint16_t>(dOs, off + lo.tr_hi(db))),
                              pb[qb][hh], dv[db]);
-            dk[db] = E::mfma(tr_operand2(&Qs[off + lo.tr(db)], &Qs[off + lo.tr_hi(db)]),
+            dk[db] = E::mfma(tr_operand2(lds_at<uint16_t>(Qs, off + lo.tr(db)),
+                                         lds_at<uint16_t>(Qs, off + lo.tr_hi(db))),
                              sb[qb][hh], dk[db]);
           }
         }
@@ -750,7 +776,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   const bool wave_valid = qw < S;
 
   // D = 128: the 4-bit swizzle (conflict-free row reads), see bwd_swz
-  const LdsOffsets<D, D == 128> lo = lds_offsets<D, D == 128>(lane);
+  LdsOffsets<D, D == 128> lo = lds_offsets<D, D == 128>(lane);
 
   const int kv_end = CAUSAL ? min(q0 + C::OWN, S) : S;
   const int nkv = RAG ? (kv_end + C::TILE - 1) / C::TILE : kv_end / C::TILE;
@@ -787,6 +813,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
     const int kv0 = j * C::TILE;
     if (!LAST) dma_stage<D, DP, RAG>(src, 1, kv0 + C::TILE, bufs[P ^ 1], S);
 
+    lo.refresh();
     if (wave_valid && (!MASKED || kv0 <= qw + 31)) {
       const uint16_t* Ks = bufs[P].t0;
       const uint16_t* Vs = bufs[P].t1;
@@ -800,12 +827,12 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
         f32x16 s = f32x16{}, dp = ndl;
 #pragma unroll
         for (int ks = 0; ks < KSP; ++ks) {
-          const u32x4 ka = *(const u32x4*)(&Ks[32 * kb * D + lo.row(ks)]);
+          const u32x4 ka = *lds_at<u32x4>(Ks, 64 * kb * D + lo.row(ks));
           s = E::mfma(ka, qf[ks], s);
         }
 #pragma unroll
         for (int ks = 0; ks < KSP; ++ks) {
-          const u32x4 va = *(const u32x4*)(&Vs[32 * kb * D + lo.row(ks)]);
+          const u32x4 va = *lds_at<u32x4>(Vs, 64 * kb * D + lo.row(ks));
           dp = E::mfma(va, df[ks], dp);
         }
         const bool diag = MASKED && kvb == qw;
@@ -832,8 +859,9 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
         for (int hh = 0; hh < 2; ++hh) {
 #pragma unroll
           for (int db = 0; db < DBP; ++db) {
-            const int off = (32 * kb + 16 * hh) * D;
-            acc[db] = E::mfma(tr_operand2(&Ks[off + lo.tr(db)], &Ks[off + lo.tr_hi(db)]),
+            const int off = 2 * (32 * kb + 16 * hh) * D;  // bytes
+            acc[db] = E::mfma(tr_operand2(lds_at<uint16_t>(Ks, off + lo.tr(db)),
+                                          lds_at<uint16_t>(Ks, off + lo.tr_hi(db))),
                               sb[kb][hh], acc[db]);
           }
         }

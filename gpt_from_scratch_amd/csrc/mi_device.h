@@ -259,6 +259,10 @@ __device__ __forceinline__ void buffer_load_lds4(__amdgpu_buffer_rsrc_t rs, uint
                                            voffset, 0, 0, 0);
 }
 
+// x unchanged, in a VGPR, through an empty volatile asm: the compiler can no
+// longer treat x as loop-invariant where this runs inside a loop body.
+__device__ __forceinline__ void opaque(int& x) { asm volatile("" : "+v"(x)); }
+
 __device__ __forceinline__ u32x2 ds_read_tr16(const uint16_t* p) {
   typedef __attribute__((ext_vector_type(4))) short s16x4;
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
