@@ -201,14 +201,18 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
   //   V^T operand of P V (transposing read), O^T block db: row 4g + (lane%16)/4
   //   (+16 per half-block, +8 for the second read), column 32db +
   //   16((lane/16)%2) + 4(lane%4).
+  // Byte offsets, the lane part only: each read adds its tile buffer and block
+  // as a constant that the LDS instruction takes as its immediate.  They are
+  // refreshed (opaque) at the top of every step, so the compiler cannot hoist
+  // one "buffer + offset" register per buffer out of the step loop.
   int kro[C::KS], vro[C::DB];
 #pragma unroll
-  for (int ks = 0; ks < C::KS; ++ks) kro[ks] = l32 * D + (((2 * ks + g) ^ swz_k<D>(l32)) << 3);
+  for (int ks = 0; ks < C::KS; ++ks) kro[ks] = 2 * (l32 * D + (((2 * ks + g) ^ swz_k<D>(l32)) << 3));
 #pragma unroll
   for (int db = 0; db < C::DB; ++db) {
     const int r = 4 * g + ((lane & 15) >> 2);
     const int ch = 4 * db + 2 * ((lane >> 4) & 1) + ((lane & 3) >> 1);
-    vro[db] = r * D + ((ch ^ swz_v<D>(r)) << 3) + 4 * (lane & 1);
+    vro[db] = 2 * (r * D + ((ch ^ swz_v<D>(r)) << 3) + 4 * (lane & 1));
   }
 
   // ---- per-wave compute pieces ----
@@ -225,7 +229,7 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
     for (int ks = 0; ks < KSP; ++ks) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const u32x4 kf = *(const u32x4*)(&kt[32 * kb * D + kro[ks]]);
+        const u32x4 kf = *(const u32x4*)((const char*)kt + 64 * kb * D + kro[ks]);
         s[kb] = E::mfma(kf, qf[ks], ks == 0 ? f32x16{} : s[kb]);
       }
     }
@@ -299,8 +303,10 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
       for (int hh = 0; hh < 2; ++hh)
 #pragma unroll
         for (int db = 0; db < DBP; ++db)
-          acc[db] = E::mfma(tr_operand(&vt[(32 * kb + 16 * hh) * D + vro[db]], D), pb[kb][hh],
-                            acc[db]);
+          acc[db] = E::mfma(tr_operand((const uint16_t*)((const char*)vt +
+                                                         2 * (32 * kb + 16 * hh) * D + vro[db]),
+                                       D),
+                            pb[kb][hh], acc[db]);
   };
 
   // ---- steps over key tiles [0, nkv) ----
@@ -315,6 +321,10 @@ __global__ __launch_bounds__(256, FwdCfg<D>::WAVES_PER_EU) void attn_fwd_mfma_ke
     constexpr int I = decltype(slot)::value;
     const uint16_t* kt = I ? K1 : K0;
     const uint16_t* vt = I ? V1 : V0;
+#pragma unroll
+    for (int ks = 0; ks < C::KS; ++ks) opaque(kro[ks]);
+#pragma unroll
+    for (int db = 0; db < C::DB; ++db) opaque(vro[db]);
     if (j + 1 < nkv) {
       dma(kp, a.k.ss, kdo, j + 1, I ? K0 : K1);
       dma(vp, a.v.ss, vdo, j + 1, I ? V0 : V1);
