@@ -38,6 +38,10 @@ namespace mi {
 
 namespace {
 
+#ifndef BWD_PREFETCH
+#define BWD_PREFETCH 1
+#endif
+
 // ---------------------------------------------------------------------------
 // delta[b,h,s] = sum_d dO[b,h,s,d] * O[b,h,s,d]   (fp32 accumulation), and
 // the second half of the workspace: lse * log2(e), the form the dK/dV loop
@@ -546,6 +550,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
   using C = BwdCfg<D>;
   constexpr int KSP = DP / 16;         // k-steps over the valid columns
   constexpr int DBP = (DP + 31) / 32;  // accumulator blocks holding valid columns
+  constexpr bool PREFETCH = BWD_PREFETCH && D == 64;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
@@ -624,31 +629,60 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
       const float* sl = bufs[P].sl;
       u32x4 pb[C::TB][2], sb[C::TB][2];
       bool live[C::TB];
-#pragma unroll
-      for (int qb = 0; qb < C::TB; ++qb) {
-        const int qbs = q0 + 32 * qb;
-        live[qb] = !MASKED || (qbs + 31 >= kw);
-        if (!live[qb]) continue;
-        f32x16 s = f32x16{}, dp;
+      // Each block's A operands and delta rows are requested before its first
+      // product: block 0's at the top of the step, block 1's right after
+      // block 0's products are issued (one LDS round trip per block instead
+      // of one per product).  The scheduling barriers keep the compiler from
+      // sinking the reads back next to their uses.
+      u32x4 qa[KSP], da[KSP];
+      f32x16 sacc[C::TB], dpacc[C::TB];
+      auto read_ops = [&](int qb) __attribute__((always_inline)) {
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
           const f32x4 d4 = *lds_at<f32x4>(sl, slo + 4 * (C::TILE + 32 * qb + 8 * jj));
 #pragma unroll
-          for (int i = 0; i < 4; ++i) dp[4 * jj + i] = d4[i];
+          for (int i = 0; i < 4; ++i) dpacc[qb][4 * jj + i] = d4[i];
         }
 #pragma unroll
         for (int ks = 0; ks < KSP; ++ks) {
-          const u32x4 qa = *lds_at<u32x4>(Qs, 64 * qb * D + lo.row(ks));
-          if constexpr (K_IN_LDS)
-            s = E::mfma(qa, *lds_at<u32x4>(kw_lds, lo.row(ks)), s);
-          else
-            s = E::mfma(qa, kf[ks], s);
+          qa[ks] = *lds_at<u32x4>(Qs, 64 * qb * D + lo.row(ks));
+          da[ks] = *lds_at<u32x4>(dOs, 64 * qb * D + lo.row(ks));
         }
+      };
+      if constexpr (PREFETCH) {
+        read_ops(0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
-        for (int ks = 0; ks < KSP; ++ks) {
-          const u32x4 da = *lds_at<u32x4>(dOs, 64 * qb * D + lo.row(ks));
-          dp = E::mfma(da, vn[ks], dp);
+      for (int qb = 0; qb < C::TB; ++qb) {
+        const int qbs = q0 + 32 * qb;
+        live[qb] = !MASKED || (qbs + 31 >= kw);
+        if constexpr (!PREFETCH) read_ops(qb);
+        if (live[qb]) {
+          sacc[qb] = f32x16{};
+#pragma unroll
+          for (int ks = 0; ks < KSP; ++ks) {
+            if constexpr (K_IN_LDS)
+              sacc[qb] = E::mfma(qa[ks], *lds_at<u32x4>(kw_lds, lo.row(ks)), sacc[qb]);
+            else
+              sacc[qb] = E::mfma(qa[ks], kf[ks], sacc[qb]);
+          }
+#pragma unroll
+          for (int ks = 0; ks < KSP; ++ks) dpacc[qb] = E::mfma(da[ks], vn[ks], dpacc[qb]);
         }
+        if constexpr (PREFETCH) {
+          if (qb + 1 < C::TB) {
+            read_ops(qb + 1);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+#pragma unroll
+      for (int qb = 0; qb < C::TB; ++qb) {
+        if (!live[qb]) continue;
+        const int qbs = q0 + 32 * qb;
+        f32x16& s = sacc[qb];
+        f32x16& dp = dpacc[qb];
         const bool diag = MASKED && qbs == kw;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
@@ -765,6 +799,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   using C = BwdCfg<D>;
   constexpr int KSP = DP / 16;         // k-steps over the valid columns
   constexpr int DBP = (DP + 31) / 32;  // accumulator blocks holding valid columns
+  constexpr bool PREFETCH = BWD_PREFETCH && D == 64;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
@@ -819,22 +854,48 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
       const uint16_t* Vs = bufs[P].t1;
       u32x4 sb[C::TB][2];
       bool live[C::TB];
+      // Each block's A operands requested before its first product (block
+      // 0's at the top of the step, block 1's once block 0's products are
+      // issued), as in the dK/dV item.
+      u32x4 ka[KSP], va[KSP];
+      f32x16 sacc[C::TB], dpacc[C::TB];
+      auto read_ops = [&](int kb) __attribute__((always_inline)) {
+#pragma unroll
+        for (int ks = 0; ks < KSP; ++ks) {
+          ka[ks] = *lds_at<u32x4>(Ks, 64 * kb * D + lo.row(ks));
+          va[ks] = *lds_at<u32x4>(Vs, 64 * kb * D + lo.row(ks));
+        }
+      };
+      if constexpr (PREFETCH) {
+        read_ops(0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
 #pragma unroll
       for (int kb = 0; kb < C::TB; ++kb) {
         const int kvb = kv0 + 32 * kb;
         live[kb] = !MASKED || (kvb <= qw + 31);
+        if constexpr (!PREFETCH) read_ops(kb);
+        if (live[kb]) {
+          sacc[kb] = f32x16{};
+          dpacc[kb] = ndl;
+#pragma unroll
+          for (int ks = 0; ks < KSP; ++ks) sacc[kb] = E::mfma(ka[ks], qf[ks], sacc[kb]);
+#pragma unroll
+          for (int ks = 0; ks < KSP; ++ks) dpacc[kb] = E::mfma(va[ks], df[ks], dpacc[kb]);
+        }
+        if constexpr (PREFETCH) {
+          if (kb + 1 < C::TB) {
+            read_ops(kb + 1);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+      }
+#pragma unroll
+      for (int kb = 0; kb < C::TB; ++kb) {
         if (!live[kb]) continue;
-        f32x16 s = f32x16{}, dp = ndl;
-#pragma unroll
-        for (int ks = 0; ks < KSP; ++ks) {
-          const u32x4 ka = *lds_at<u32x4>(Ks, 64 * kb * D + lo.row(ks));
-          s = E::mfma(ka, qf[ks], s);
-        }
-#pragma unroll
-        for (int ks = 0; ks < KSP; ++ks) {
-          const u32x4 va = *lds_at<u32x4>(Vs, 64 * kb * D + lo.row(ks));
-          dp = E::mfma(va, df[ks], dp);
-        }
+        const int kvb = kv0 + 32 * kb;
+        f32x16& s = sacc[kb];
+        f32x16& dp = dpacc[kb];
         const bool diag = MASKED && kvb == qw;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
