@@ -38,10 +38,6 @@ namespace mi {
 
 namespace {
 
-#ifndef BWD_PREFETCH
-#define BWD_PREFETCH 1
-#endif
-
 // ---------------------------------------------------------------------------
 // delta[b,h,s] = sum_d dO[b,h,s,d] * O[b,h,s,d]   (fp32 accumulation), and
 // the second half of the workspace: lse * log2(e), the form the dK/dV loop
@@ -550,7 +546,7 @@ __device__ __forceinline__ void dkdv_item(const AttnArgs& a, const BwdItem& it,
   using C = BwdCfg<D>;
   constexpr int KSP = DP / 16;         // k-steps over the valid columns
   constexpr int DBP = (DP + 31) / 32;  // accumulator blocks holding valid columns
-  constexpr bool PREFETCH = BWD_PREFETCH && D == 64;
+  constexpr bool PREFETCH = D == 64;  // operands a block ahead (D = 128 has no registers for it)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
@@ -799,7 +795,7 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   using C = BwdCfg<D>;
   constexpr int KSP = DP / 16;         // k-steps over the valid columns
   constexpr int DBP = (DP + 31) / 32;  // accumulator blocks holding valid columns
-  constexpr bool PREFETCH = BWD_PREFETCH && D == 64;
+  constexpr bool PREFETCH = D == 64;  // operands a block ahead (D = 128 has no registers for it)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
