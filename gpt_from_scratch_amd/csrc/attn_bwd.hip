@@ -865,17 +865,26 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
       if constexpr (PREFETCH) {
         read_ops(0);
         __builtin_amdgcn_sched_barrier(0);
+      } else if constexpr (D == 128) {
+        // one block per tile: its K operands up front, its V operands while
+        // the S^T products run (one LDS round trip before each chain)
+#pragma unroll
+        for (int ks = 0; ks < KSP; ++ks) ka[ks] = *lds_at<u32x4>(Ks, lo.row(ks));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < KSP; ++ks) va[ks] = *lds_at<u32x4>(Vs, lo.row(ks));
       }
 #pragma unroll
       for (int kb = 0; kb < C::TB; ++kb) {
         const int kvb = kv0 + 32 * kb;
         live[kb] = !MASKED || (kvb <= qw + 31);
-        if constexpr (!PREFETCH) read_ops(kb);
+        if constexpr (!PREFETCH && D != 128) read_ops(kb);
         if (live[kb]) {
           sacc[kb] = f32x16{};
           dpacc[kb] = ndl;
 #pragma unroll
           for (int ks = 0; ks < KSP; ++ks) sacc[kb] = E::mfma(ka[ks], qf[ks], sacc[kb]);
+          if constexpr (D == 128) __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
           for (int ks = 0; ks < KSP; ++ks) dpacc[kb] = E::mfma(va[ks], df[ks], dpacc[kb]);
         }
