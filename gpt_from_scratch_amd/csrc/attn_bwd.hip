@@ -352,7 +352,7 @@ __device__ __forceinline__ void store_block_rows_rope_t(const f32x16 (&acc)[D / 
                     Tab4<TDT>::get(cs[i], k), Tab4<TDT>::get(sn[i], k), true, re, ro);
         o[k] = E::pack2(re, ro);
       }
-      if (!TAIL || r < nrows) *(u32x4*)(grow + (int64_t)r * ss + 8 * c) = o;
+      if (!TAIL || r < nrows) __builtin_nontemporal_store(o, (u32x4*)(grow + (int64_t)r * ss + 8 * c));
     }
   }
 }
