@@ -3,12 +3,11 @@
 The attention kernels (matrix-core and exact-fp32), RoPE and the model
 operators must not use scratch memory (register spills or run-time-indexed
 private arrays), and the hot attention kernels must keep the occupancy their
-tiling assumes.  The documented exceptions are the causal D = 128 dK/dV launch
-with the rotating stores (one spilled register) and the causal combined
-backward for sequence lengths that are not a multiple of 64 (36-44 bytes per
-lane of spilled scalar registers).  At
-D = 64 every backward launch, the separate dK/dV and dQ ones included, runs the
-combined kernel, which has no scratch."""
+tiling assumes.  The one documented exception is the causal combined backward
+at head dims 16 and 32 for sequence lengths that are not a multiple of 64 (36
+bytes per lane of spilled scalar registers).  At D = 64 every backward launch,
+the separate dK/dV and dQ ones included, runs the combined kernel, which has
+no scratch."""
 import os
 import re
 import shutil
@@ -21,8 +20,9 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "gpt_from_scratch_amd", "csrc")
 HIPCC = "/opt/rocm/bin/hipcc"
 SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "attn_valu.hip", "rope.hip", "model_ops.hip")
-# the causal combined backward (head dims 16-64) for sequence lengths that
-# are not a multiple of 64 (36 bytes per lane: scalar registers spilled)
+# the causal combined backward for sequence lengths that are not a multiple
+# of 64 (36 bytes per lane: scalar registers spilled; only the head dims 16
+# and 32 instantiations spill at present, the pattern also admits D = 64)
 ALLOWED_SCRATCH = re.compile(r"attn_bwd_kernel<mi::(BF16|F16), 64, true, (true|false), "
                              r"(16|32|64), true>")
 
