@@ -20,11 +20,10 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "gpt_from_scratch_amd", "csrc")
 HIPCC = "/opt/rocm/bin/hipcc"
 SOURCES = ("attn_fwd.hip", "attn_bwd.hip", "attn_valu.hip", "rope.hip", "model_ops.hip")
-# the causal combined backward for sequence lengths that are not a multiple
-# of 64 (36 bytes per lane: scalar registers spilled; only the head dims 16
-# and 32 instantiations spill at present, the pattern also admits D = 64)
+# the causal combined backward at head dims 16 and 32 for sequence lengths
+# that are not a multiple of 64 (36 bytes per lane: scalar registers spilled)
 ALLOWED_SCRATCH = re.compile(r"attn_bwd_kernel<mi::(BF16|F16), 64, true, (true|false), "
-                             r"(16|32|64), true>")
+                             r"(16|32), true>")
 
 
 def _hipflags(src):
