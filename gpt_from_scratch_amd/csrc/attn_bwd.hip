@@ -795,7 +795,8 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
   using C = BwdCfg<D>;
   constexpr int KSP = DP / 16;         // k-steps over the valid columns
   constexpr int DBP = (DP + 31) / 32;  // accumulator blocks holding valid columns
-  constexpr bool PREFETCH = D == 64;  // operands a block ahead (D = 128 has no registers for it)
+  static_assert(D == 64 || D == 128, "head dim of the item layout");
+  constexpr bool PREFETCH = D == 64;  // operands a block ahead (D = 128: one block per tile, below)
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform (SGPR)
   const int l32 = lane & 31;
@@ -878,7 +879,6 @@ __device__ __forceinline__ void dq_item(const AttnArgs& a, const BwdItem& it,
       for (int kb = 0; kb < C::TB; ++kb) {
         const int kvb = kv0 + 32 * kb;
         live[kb] = !MASKED || (kvb <= qw + 31);
-        if constexpr (!PREFETCH && D != 128) read_ops(kb);
         if (live[kb]) {
           sacc[kb] = f32x16{};
           dpacc[kb] = ndl;
