@@ -714,7 +714,9 @@ def main():
     roofline = {"kernel": dom, "bound": "mfma", "achieved": round(achieved, 2),
                 "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                "algorithmic_flop_per_launch": kflops[dom], "traffic": read_traffic(dom)}
+                "algorithmic_flop_per_launch": kflops[dom], "traffic": read_traffic(dom),
+                "traffic_source": "profiles/traffic_c2.txt: rocprofv3 FETCH_SIZE and WRITE_SIZE "
+                                  "passes of this bench command, scaled by the in-run copy kernel"}
 
     # The same step with its operands out of the Infinity Cache: NC buffer sets
     # (RoPE'd q/k, the qkv tensor V is a view of, dO, O, LSE, workspace, dQ,
